@@ -1,0 +1,372 @@
+"""ORACLE — CPU restatement of torchtitan's MoE layer hot path. TEST INFRASTRUCTURE.
+
+This module is the checker for the MI355X kernels. Only tests/, the smoke()
+of __graft_entry__.py and bench.py's cpu_baseline leg may import it; the
+product (torchtitan_amd) never does.
+
+It restates the reference's algorithm (QIU023/torchtitan):
+  torchtitan/models/common/moe.py:24-489       (router, reorderer, experts, MoE.forward)
+  torchtitan/ops/scatter_add.py:10-48          (deterministic scatter_add + backward)
+  torchtitan/models/common/feed_forward.py:34-54
+  torchtitan/distributed/expert_parallel.py:26-67 (_generate_permute_indices)
+with the GPU lowering of the ops the reference calls made explicit, because on
+the GPU those are what define the reference's results:
+  * torch.topk(sorted=False): radix order, lowest index first among ties, output
+    slots = keys above the k-th key by ascending index, then k-th-key ties;
+  * torch.sum over a short row: pairwise tree over adjacent lanes;
+  * torch.histc(int64): bincount (the reference's CPU histc rejects int64);
+  * deterministic scatter_add: fp32 sum of a token's rows in ascending position,
+    added to the destination with one rounding;
+  * x[token_idx] backward: accumulate in ascending position, rounding each add.
+Those lowering claims are pinned by GPU tests that run the same torch ops on
+the device (tests/test_gpu_oracle_pins.py); the arithmetic is pinned by closed
+forms, brute force and finite differences (tests/test_oracle.py).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+# ---------------------------------------------------------------------------
+# selection rules (numpy)
+# ---------------------------------------------------------------------------
+
+
+def radix_key(x: np.ndarray) -> np.ndarray:
+    """Order-preserving uint32 key of fp32 values: -0 < +0, NaN largest."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b = x.view(np.uint32)
+    mask = np.where(b & np.uint32(0x80000000), np.uint32(0xFFFFFFFF), np.uint32(0x80000000))
+    k = b ^ mask
+    return np.where(np.isnan(x), np.uint32(0xFFFFFFFF), k).astype(np.uint32)
+
+
+def topk_gpu_order(values: np.ndarray, k: int) -> np.ndarray:
+    """Indices of torch.topk(values, k, dim=-1, sorted=False) on the GPU
+    (moe.py:199-201, :247-249): the k largest radix keys, lowest index first
+    among equal keys; emitted as the entries whose key exceeds the k-th key in
+    ascending index, then the k-th-key ties in ascending index."""
+    v = np.asarray(values, dtype=np.float32)
+    n, e = v.shape
+    key = radix_key(v).astype(np.int64)
+    # stable sort by key descending == ascending index among ties
+    order = np.argsort(-key, axis=1, kind="stable")[:, :k]
+    sel_key = np.take_along_axis(key, order, axis=1)
+    kth = sel_key[:, k - 1 : k]
+    cls = (sel_key <= kth).astype(np.int64)  # 0: above the k-th key, 1: tie with it
+    comb = cls * (e + 1) + order
+    out_rank = np.argsort(comb, axis=1, kind="stable")
+    return np.take_along_axis(order, out_rank, axis=1).astype(np.int64)
+
+
+def gpu_row_sum(v: torch.Tensor) -> torch.Tensor:
+    """Sum over the last dim (size n <= 64) in torch's GPU reduction order for a
+    short contiguous row: bw = largest power of two <= n; lane x forms
+    v[x] + v[x+bw]; then lanes combine pairwise with offsets 1, 2, 4, ...
+    Differentiable (plain torch indexing and adds)."""
+    n = v.shape[-1]
+    bw = 1
+    while bw * 2 <= n:
+        bw *= 2
+    parts = []
+    for x in range(bw):
+        p = v[..., x]
+        if x + bw < n:
+            p = p + v[..., x + bw]
+        parts.append(p)
+    off = 1
+    while off < bw:
+        parts = [parts[i] + parts[i + off] if i % (2 * off) == 0 else parts[i] for i in range(bw)]
+        off *= 2
+    return parts[0]
+
+
+def node_limited_choice(choice: np.ndarray, n_groups: int, n_limited: int) -> np.ndarray:
+    """_get_node_limited_routing_scores (moe.py:169-209): group score = sum of the
+    two largest scores in the group; keep the n_limited best groups
+    (topk sorted=False rule); set the other groups' experts to -inf."""
+    n, e = choice.shape
+    epg = e // n_groups
+    g = np.asarray(choice, dtype=np.float32).reshape(n, n_groups, epg)
+    key = radix_key(g).astype(np.int64)
+    top2 = np.argsort(-key, axis=2, kind="stable")[:, :, :2]
+    vals = np.take_along_axis(g, top2, axis=2)
+    group_scores = (vals[:, :, 0] + vals[:, :, 1]).astype(np.float32)
+    keep = topk_gpu_order(group_scores, n_limited)
+    mask = np.ones((n, n_groups), dtype=bool)
+    np.put_along_axis(mask, keep, False, axis=1)
+    out = np.where(mask[:, :, None], np.float32(-np.inf), g).astype(np.float32)
+    return out.reshape(n, e)
+
+
+# ---------------------------------------------------------------------------
+# router (moe.py:211-276)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class RouterCfg:
+    num_experts: int
+    top_k: int
+    score_func: str = "sigmoid"
+    num_expert_groups: int | None = None
+    num_limited_groups: int | None = None
+    route_norm: bool = False
+    route_scale: float = 1.0
+    force_load_balance: bool = False
+
+
+def score_fn(logits: torch.Tensor, score_func: str) -> torch.Tensor:
+    """moe.py:236-241 (fp32)."""
+    if score_func == "sigmoid":
+        return torch.sigmoid(logits)
+    if score_func == "softmax":
+        return F.softmax(logits, dim=1)
+    raise NotImplementedError(f"Unknown score function {score_func}")
+
+
+def select_experts(scores: np.ndarray, expert_bias: np.ndarray | None, cfg: RouterCfg) -> np.ndarray:
+    """Expert choice from fp32 scores (moe.py:243-261). Returns [N,K] int64."""
+    n = scores.shape[0]
+    if cfg.force_load_balance:
+        return (np.arange(n * cfg.top_k, dtype=np.int64).reshape(n, cfg.top_k)) % cfg.num_experts
+    choice = scores if expert_bias is None else (scores + expert_bias[None, :]).astype(np.float32)
+    if cfg.num_expert_groups is not None:
+        choice = node_limited_choice(choice, cfg.num_expert_groups, cfg.num_limited_groups)
+    return topk_gpu_order(choice, cfg.top_k)
+
+
+def router_forward(logits: torch.Tensor, expert_bias: torch.Tensor | None, cfg: RouterCfg,
+                   scores: torch.Tensor | None = None):
+    """Returns (top_scores [N,K] f32, idx [N,K] i64, counts [E] i64, scores [N,E] f32).
+    `scores` may be supplied to route from given score-function outputs (to
+    compare selection bit-exactly with a device that computed them)."""
+    if scores is None:
+        scores = score_fn(logits.float(), cfg.score_func)
+    bias_np = expert_bias.detach().float().cpu().numpy() if expert_bias is not None else None
+    idx_np = select_experts(scores.detach().cpu().numpy(), bias_np, cfg)
+    idx = torch.from_numpy(idx_np).to(scores.device)
+    top_scores = scores.gather(1, idx)
+    if cfg.route_norm:
+        den = gpu_row_sum(top_scores).unsqueeze(-1) + 1e-20
+        top_scores = top_scores / den
+    top_scores = top_scores * cfg.route_scale
+    counts = torch.bincount(idx.view(-1), minlength=cfg.num_experts)
+    return top_scores, idx, counts, scores
+
+
+# ---------------------------------------------------------------------------
+# reorderer (moe.py:291-332) and EP permute indices (expert_parallel.py:26-67)
+# ---------------------------------------------------------------------------
+
+
+def reorder(top_scores: torch.Tensor, idx: torch.Tensor, num_experts: int):
+    """(scores_sorted [R], token_idx [R] i64, counts [E] i64, perm [R] i64)."""
+    k = idx.shape[1]
+    flat = idx.reshape(-1)
+    counts = torch.bincount(flat, minlength=num_experts)
+    perm = torch.from_numpy(np.argsort(flat.cpu().numpy(), kind="stable")).to(flat.device)
+    scores_sorted = top_scores.reshape(-1)[perm]
+    return scores_sorted, perm // k, counts, perm
+
+
+def generate_permute_indices(tokens_per_expert_group, experts_per_rank: int, num_ranks: int):
+    """Rank-major -> expert-major gather indices (expert_parallel.py:26-67)."""
+    t = np.asarray(tokens_per_expert_group, dtype=np.int64)
+    mat = t.reshape(num_ranks, experts_per_rank)
+    in_start = (np.cumsum(t) - t).reshape(num_ranks, experts_per_rank)
+    seg_len = mat.T.reshape(-1)
+    seg_in = in_start.T.reshape(-1)
+    seg_out = np.cumsum(seg_len) - seg_len
+    out = np.empty(int(t.sum()), dtype=np.int64)
+    for s in range(seg_len.shape[0]):
+        n = int(seg_len[s])
+        out[seg_out[s] : seg_out[s] + n] = seg_in[s] + np.arange(n)
+    return out, mat.sum(axis=0)
+
+
+# ---------------------------------------------------------------------------
+# row movement with the GPU accumulation semantics
+# ---------------------------------------------------------------------------
+
+
+class _IndexRows(torch.autograd.Function):
+    """routed = x[token_idx] (moe.py:445); backward accumulates each token's rows
+    in ascending position, rounding to x's dtype after every add."""
+
+    @staticmethod
+    def forward(ctx, x, token_idx):
+        ctx.save_for_backward(token_idx)
+        ctx.n = x.shape[0]
+        return x[token_idx]
+
+    @staticmethod
+    def backward(ctx, g):
+        (token_idx,) = ctx.saved_tensors
+        return index_backward(g, token_idx, ctx.n), None
+
+
+def index_backward(g: torch.Tensor, token_idx: torch.Tensor, n: int) -> torch.Tensor:
+    dtype = g.dtype
+    order = torch.from_numpy(np.argsort(token_idx.cpu().numpy(), kind="stable"))
+    t_sorted = token_idx[order]
+    counts = torch.bincount(token_idx, minlength=n)
+    maxk = int(counts.max().item()) if counts.numel() else 0
+    acc = torch.zeros(n, g.shape[1], dtype=torch.float32)
+    start = torch.cumsum(counts, 0) - counts
+    rank = torch.arange(order.numel()) - start[t_sorted]
+    for j in range(maxk):
+        sel = rank == j
+        rows = order[sel]
+        toks = t_sorted[sel]
+        acc[toks] = (acc[toks] + g[rows].float()).to(dtype).float()
+    return acc.to(dtype)
+
+
+class _Combine(torch.autograd.Function):
+    """deterministic_scatter_add(out, token_idx expanded, src) (scatter_add.py:10-48):
+    each token's rows summed in fp32 from zero in ascending position, then added to
+    out with one rounding. Backward: grad passes to out; grad_src = gather."""
+
+    @staticmethod
+    def forward(ctx, out, token_idx, src):
+        ctx.save_for_backward(token_idx)
+        acc = torch.zeros(out.shape, dtype=torch.float32)
+        order = torch.from_numpy(np.argsort(token_idx.cpu().numpy(), kind="stable"))
+        t_sorted = token_idx[order]
+        counts = torch.bincount(token_idx, minlength=out.shape[0])
+        start = torch.cumsum(counts, 0) - counts
+        rank = torch.arange(order.numel()) - start[t_sorted]
+        maxk = int(counts.max().item()) if counts.numel() else 0
+        for j in range(maxk):
+            sel = rank == j
+            acc[t_sorted[sel]] += src[order[sel]].float()
+        return (out.float() + acc).to(out.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        (token_idx,) = ctx.saved_tensors
+        return g, None, g[token_idx]
+
+
+# ---------------------------------------------------------------------------
+# experts (moe.py:24-70) and the shared expert (feed_forward.py:53-54)
+# ---------------------------------------------------------------------------
+
+
+def experts_grouped_mm(w1, w2, w3, x, counts):
+    """_run_experts_grouped_mm: bf16 per-segment GEMMs, fp32 accumulate, bf16
+    outputs, each bf16 elementwise op rounded (moe.py:53-70). Uses per-segment
+    matmuls, which is what torch._grouped_mm computes per group."""
+    xb, w1b, w2b, w3b = x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16()
+    outs = []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        xe = xb[start : start + c]
+        g = (xe.float() @ w1b[e].float().t()).bfloat16()
+        u = (xe.float() @ w3b[e].float().t()).bfloat16()
+        h = F.silu(g) * u
+        outs.append((h.float() @ w2b[e].float().t()).bfloat16())
+        start += c
+    tail = xb.new_zeros(xb.shape[0] - start, w2.shape[1])
+    return torch.cat(outs + [tail], 0).type_as(x)
+
+
+def experts_for_loop(w1, w2, w3, x, counts):
+    """_run_experts_for_loop (moe.py:24-50): matmuls in the input dtype."""
+    outs = []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        xe = x[start : start + c]
+        h = F.silu(xe @ w1[e].t()) * (xe @ w3[e].t())
+        outs.append(h @ w2[e].t())
+        start += c
+    return torch.cat(outs, 0)
+
+
+def feed_forward(x, w1, w2, w3):
+    return F.linear(F.silu(F.linear(x, w1)) * F.linear(x, w3), w2)
+
+
+# ---------------------------------------------------------------------------
+# MoE.forward (moe.py:380-477)
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class MoECfg:
+    router: RouterCfg
+    dim: int
+    hidden_dim: int
+    score_before_experts: bool = True
+    use_grouped_mm: bool = True
+    has_shared: bool = False
+
+
+def moe_forward(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None):
+    """params: 'gate' [E,D], 'w1','w2','w3' experts, optional 'sw1','sw2','sw3'
+    shared expert, optional 'expert_bias' [E]. Records intermediates in `aux`."""
+    bs, slen, dim = x.shape
+    x2 = x.reshape(-1, dim)
+    logits = F.linear(x2.float(), params["gate"].float())  # fp32 gate (autocast on GPU)
+    top_scores, idx, counts, scores = router_forward(logits, params.get("expert_bias"), cfg.router)
+    scores_sorted, token_idx, counts2, perm = reorder(top_scores, idx, cfg.router.num_experts)
+    routed_input = _IndexRows.apply(x2, token_idx)
+    if cfg.score_before_experts:
+        routed_input = (routed_input.float() * scores_sorted.reshape(-1, 1)).to(x2.dtype)
+    run = experts_grouped_mm if cfg.use_grouped_mm else experts_for_loop
+    routed_output = run(params["w1"], params["w2"], params["w3"], routed_input, counts2)
+    if cfg.has_shared:
+        out = feed_forward(x2, params["sw1"], params["sw2"], params["sw3"])
+    else:
+        out = torch.zeros_like(x2)
+    if not cfg.score_before_experts:
+        routed_output = (routed_output.float() * scores_sorted.reshape(-1, 1)).to(x2.dtype)
+    out = _Combine.apply(out, token_idx, routed_output)
+    if aux is not None:
+        aux.update(logits=logits, scores=scores, top_scores=top_scores, idx=idx, counts=counts,
+                   scores_sorted=scores_sorted, token_idx=token_idx, perm=perm,
+                   routed_input=routed_input, routed_output=routed_output)
+    return out.reshape(bs, slen, dim)
+
+
+# ---------------------------------------------------------------------------
+# the reference's router op sequence in plain torch ops (device-agnostic)
+# ---------------------------------------------------------------------------
+
+
+def router_forward_torch(logits: torch.Tensor, expert_bias: torch.Tensor | None, cfg: RouterCfg):
+    """moe.py:236-274 op for op. Run on the GPU it is the reference router after
+    the gate; the GPU tests use it to pin the selection / summation rules that
+    router_forward restates. (histc on int64 is GPU-only, so counts use it only
+    off the CPU.)"""
+    scores = score_fn(logits.float(), cfg.score_func)
+    choice = scores if expert_bias is None else scores + expert_bias
+    if cfg.num_expert_groups is not None:
+        g, gk = cfg.num_expert_groups, cfg.num_limited_groups
+        grouped = choice.view(-1, g, cfg.num_experts // g)
+        top2, _ = grouped.topk(2, dim=-1)
+        group_scores = top2.sum(dim=-1)
+        _, group_idx = torch.topk(group_scores, k=gk, dim=-1, sorted=False)
+        group_mask = torch.ones_like(group_scores, dtype=torch.bool)
+        group_mask.scatter_(1, group_idx, False)
+        choice = grouped.masked_fill(group_mask.unsqueeze(-1), float("-inf")).view(-1, cfg.num_experts)
+    _, idx = torch.topk(choice, k=cfg.top_k, dim=-1, sorted=False)
+    top_scores = scores.gather(dim=1, index=idx)
+    if cfg.force_load_balance:
+        n = scores.shape[0]
+        idx = torch.arange(n * cfg.top_k, device=scores.device, dtype=torch.int64).reshape(n, cfg.top_k)
+        idx = idx % cfg.num_experts
+        top_scores = scores.gather(dim=1, index=idx)
+    if cfg.route_norm:
+        top_scores = top_scores / (top_scores.sum(dim=-1, keepdim=True) + 1e-20)
+    top_scores = top_scores * cfg.route_scale
+    if logits.device.type == "cpu":
+        counts = torch.bincount(idx.view(-1), minlength=cfg.num_experts)
+    else:
+        counts = torch.histc(idx.view(-1), bins=cfg.num_experts, min=0, max=cfg.num_experts)
+    return top_scores, idx, counts, scores

@@ -1,0 +1,248 @@
+"""GPU parity of the MI355X kernels against the oracle (oracle/moe_ref.py).
+
+Bars:
+  * routing indices, token counts, permutation, permute and combine: bit-exact;
+  * bf16 GEMM outputs and gradients: normwise max relative error
+    max|ours - ref| / max|ref| <= 1e-2 against the fp32-accumulated reference.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as R
+from tests.conftest import banner
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+
+
+def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    den = b.abs().max().item()
+    return (a - b).abs().max().item() / (den if den > 0 else 1.0)
+
+
+def ops():
+    from torchtitan_amd import ops as _ops
+
+    return _ops
+
+
+ROUTER_CASES = {
+    # name: (N, E, K, score_func, groups, limited, norm, scale, bias, force_lb, tie_levels)
+    "tiny_softmax_e8_k2": (4096, 8, 2, "softmax", None, None, False, 1.0, False, False, 0),
+    "kimi_sigmoid_bias_e256_k8": (4096, 256, 8, "sigmoid", None, None, True, 2.5, True, False, 0),
+    "dsv3_group_limited": (2048, 256, 8, "sigmoid", 8, 4, True, 2.5, True, False, 0),
+    "softmax_e96_k6": (1024, 96, 6, "softmax", None, None, True, 1.0, False, False, 0),
+    "ties_sigmoid_e64_k4": (2048, 64, 4, "sigmoid", None, None, False, 1.0, False, False, 5),
+    "ties_group_e32_g4": (1024, 32, 4, "sigmoid", 4, 2, True, 1.0, False, False, 3),
+    "force_load_balance": (1000, 16, 3, "sigmoid", None, None, True, 1.0, False, True, 0),
+}
+
+
+def _router_inputs(n, e, tie_levels, bias, seed):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(n, e, generator=g)
+    if tie_levels:
+        logits = torch.round(logits * tie_levels) / tie_levels  # many exact ties
+    b = (torch.rand(e, generator=g) * 0.02 - 0.01) if bias else None
+    if tie_levels and bias:
+        b = torch.round(b * 100) / 100
+    return logits, b
+
+
+@pytest.mark.parametrize("name", list(ROUTER_CASES))
+def test_router_bit_exact(dev, name):
+    n, e, k, sf, groups, limited, norm, scale, bias, flb, ties = ROUTER_CASES[name]
+    banner(f"router {name}")
+    logits, b = _router_inputs(n, e, ties, bias, seed=1234)
+    cfg = R.RouterCfg(num_experts=e, top_k=k, score_func=sf, num_expert_groups=groups,
+                      num_limited_groups=limited, route_norm=norm, route_scale=scale,
+                      force_load_balance=flb)
+    o = ops()
+    top, idx, counts, scores = o.router(
+        logits.to(dev), b.to(dev) if b is not None else None, e, k, o.SCORE_FUNCS[sf],
+        groups or 0, limited or 0, norm, scale, flb,
+    )
+    torch.cuda.synchronize()
+    # 1. score function: bit-identical to torch's on the device
+    ref_scores = R.score_fn(logits.to(dev), sf)
+    assert torch.equal(scores, ref_scores), "score function differs from torch on the GPU"
+    # 2. selection, slot order, gathered/normalised scores: bit-exact vs the oracle
+    o_top, o_idx, o_counts, _ = R.router_forward(None, b, cfg, scores=scores.cpu())
+    assert torch.equal(idx.cpu(), o_idx), "selected experts differ from the oracle"
+    assert torch.equal(counts.cpu(), o_counts)
+    assert torch.equal(top.cpu(), o_top), "top scores differ from the oracle"
+    # 3. and identical to the reference op sequence run by torch on the GPU
+    t_top, t_idx, t_counts, _ = R.router_forward_torch(logits.to(dev), b.to(dev) if b is not None else None, cfg)
+    assert torch.equal(idx, t_idx)
+    assert torch.equal(counts, t_counts)
+    assert torch.equal(top, t_top)
+
+
+@pytest.mark.parametrize("name", ["kimi_sigmoid_bias_e256_k8", "tiny_softmax_e8_k2", "dsv3_group_limited"])
+def test_router_backward(dev, name):
+    n, e, k, sf, groups, limited, norm, scale, bias, flb, ties = ROUTER_CASES[name]
+    banner(f"router backward {name}")
+    logits, b = _router_inputs(n, e, ties, bias, seed=99)
+    g = torch.randn(n, k, generator=torch.Generator().manual_seed(5))
+    o = ops()
+    lg = logits.to(dev).requires_grad_(True)
+    top, idx, counts, scores = o.router(lg, b.to(dev) if b is not None else None, e, k,
+                                        o.SCORE_FUNCS[sf], groups or 0, limited or 0, norm, scale, flb)
+    (top * g.to(dev)).sum().backward()
+    # oracle gradient: same selection, autograd through the restated ops in fp64
+    cfg = R.RouterCfg(num_experts=e, top_k=k, score_func=sf, num_expert_groups=groups,
+                      num_limited_groups=limited, route_norm=norm, route_scale=scale)
+    l64 = logits.double().requires_grad_(True)
+    s64 = R.score_fn(l64, sf)
+    ts = s64.gather(1, idx.cpu())
+    if norm:
+        ts = ts / (ts.sum(-1, keepdim=True) + 1e-20)
+    ts = ts * scale
+    (ts * g.double()).sum().backward()
+    assert rel_err(lg.grad, l64.grad) < 1e-5
+
+
+def test_reorder_exact(dev):
+    banner("reorder")
+    n, e, k = 5000, 64, 6
+    logits, _ = _router_inputs(n, e, 0, False, seed=7)
+    o = ops()
+    top, idx, _, _ = o.router(logits.to(dev), None, e, k, 1, 0, 0, False, 1.0, False)
+    ss, tok, counts, offs, slot_pos, tok_pos = o.reorder(top, idx, e)
+    torch.cuda.synchronize()
+    r_ss, r_tok, r_counts, r_perm = R.reorder(top.cpu(), idx.cpu(), e)
+    assert torch.equal(tok.cpu(), r_tok)
+    assert torch.equal(ss.cpu(), r_ss)
+    assert torch.equal(counts.cpu(), r_counts)
+    assert torch.equal(offs.cpu().long(), torch.cumsum(r_counts, 0))
+    # slot_pos is the inverse of the stable argsort, tok_pos its per-token sorted rows
+    inv = torch.empty_like(r_perm)
+    inv[r_perm] = torch.arange(r_perm.numel())
+    assert torch.equal(slot_pos.cpu().long().view(-1), inv)
+    assert torch.equal(tok_pos.cpu().long(), torch.sort(inv.view(n, k), dim=1).values)
+    # torch's own stable argsort on the device agrees
+    assert torch.equal(tok, torch.argsort(idx.view(-1), stable=True) // k)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("score_before", [True, False])
+def test_permute_combine_exact(dev, dtype, score_before):
+    banner(f"permute/combine dtype={dtype} score_before={score_before}")
+    n, e, k, d = 3000, 32, 4, 512
+    gen = torch.Generator().manual_seed(11)
+    logits = torch.randn(n, e, generator=gen)
+    x = torch.randn(n, d, generator=gen).to(dtype)
+    shared = torch.randn(n, d, generator=gen).to(dtype)
+    routed = torch.randn(n * k, d, generator=gen).to(dtype)
+    gout = torch.randn(n, d, generator=gen).to(dtype)
+    o = ops()
+    top, idx, _, _ = o.router(logits.to(dev), None, e, k, 1, 0, 0, True, 2.0, False)
+    ss, tok, counts, offs, slot_pos, tok_pos = o.reorder(top, idx, e)
+    xs = x.to(dev).requires_grad_(True)
+    sc = ss.detach().clone().requires_grad_(True)
+    # permute
+    ri = o.permute(xs, slot_pos, tok_pos, sc if score_before else None)
+    ref = x[tok.cpu()]
+    if score_before:
+        ref = (ref.float() * ss.cpu().reshape(-1, 1)).to(dtype)
+    assert torch.equal(ri.detach().cpu(), ref)
+    # combine (forward) vs the oracle's deterministic scatter-add restatement
+    rs = routed.to(dev).requires_grad_(True)
+    sh = shared.to(dev).requires_grad_(True)
+    out = o.combine(sh, rs, slot_pos, tok_pos, None if score_before else sc)
+    src = routed if score_before else (routed.float() * ss.cpu().reshape(-1, 1)).to(dtype)
+    r_out = R._Combine.apply(shared, tok.cpu(), src)
+    assert torch.equal(out.detach().cpu(), r_out)
+    # backward of the combine and of the permute
+    out.backward(gout.to(dev))
+    assert torch.equal(sh.grad.cpu(), gout)
+    gr_ref = gout[tok.cpu()]
+    if not score_before:
+        gr_ref = (gr_ref.float() * ss.cpu().reshape(-1, 1)).to(dtype)
+    assert torch.equal(rs.grad.cpu(), gr_ref)
+    gri = torch.randn(n * k, d, generator=gen).to(dtype)
+    ri.backward(gri.to(dev))
+    g_in = gri if not score_before else (gri.float() * ss.cpu().reshape(-1, 1)).to(dtype)
+    assert torch.equal(xs.grad.cpu(), R.index_backward(g_in, tok.cpu(), n))
+    # score gradients (fp32 dot products over D; order differs from torch's reduction)
+    if score_before:
+        ds_ref = (gri.double() * x[tok.cpu()].double()).sum(1)
+    else:
+        ds_ref = (gout[tok.cpu()].double() * routed.double()).sum(1)
+    assert rel_err(sc.grad, ds_ref) < 1e-5
+
+
+def _gemm_inputs(e, d, h, counts, seed, std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    r = int(sum(counts))
+    x = torch.randn(r, d, generator=g).bfloat16()
+    w1 = (torch.randn(e, h, d, generator=g) * std).bfloat16()
+    w2 = (torch.randn(e, d, h, generator=g) * std).bfloat16()
+    w3 = (torch.randn(e, h, d, generator=g) * std).bfloat16()
+    dy = torch.randn(r, d, generator=g).bfloat16()
+    return x, w1, w2, w3, dy, torch.tensor(counts, dtype=torch.int64)
+
+
+GEMM_CASES = {
+    "uniform_e8": (8, 256, 512, [130, 128, 127, 1, 255, 256, 257, 100]),
+    "empty_and_skewed": (8, 512, 256, [0, 700, 0, 3, 0, 0, 129, 0]),
+    "single_expert": (1, 256, 256, [333]),
+}
+
+
+@pytest.mark.parametrize("name", list(GEMM_CASES))
+def test_grouped_swiglu_fwd_bwd(dev, name):
+    e, d, h, counts = GEMM_CASES[name]
+    banner(f"grouped swiglu {name}")
+    x, w1, w2, w3, dy, cnt = _gemm_inputs(e, d, h, counts, seed=3)
+    o = ops()
+    xs, w1s, w2s, w3s = (t.to(dev).requires_grad_(True) for t in (x, w1, w2, w3))
+    y, g, u, hh = o.grouped_swiglu(xs, w1s, w2s, w3s, cnt.to(dev))
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    # fp32 reference from the same bf16 inputs, with the reference's bf16 roundings
+    xr, w1r, w2r, w3r = (t.float().requires_grad_(True) for t in (x, w1, w2, w3))
+    ys, gs, us, hs = [], [], [], []
+    start = 0
+    for ei, c in enumerate(counts):
+        xe = xr[start : start + c]
+        ge = xe @ w1r[ei].t()
+        ue = xe @ w3r[ei].t()
+        he = torch.nn.functional.silu(ge) * ue
+        ys.append(he @ w2r[ei].t())
+        gs.append(ge); us.append(ue); hs.append(he)
+        start += c
+    yr = torch.cat(ys)
+    yr.backward(dy.float())
+    assert rel_err(y, yr) < BF16_TOL
+    assert rel_err(g, torch.cat(gs)) < BF16_TOL
+    assert rel_err(u, torch.cat(us)) < BF16_TOL
+    assert rel_err(hh, torch.cat(hs)) < BF16_TOL
+    assert rel_err(xs.grad, xr.grad) < BF16_TOL
+    for ours, ref, nm in ((w1s.grad, w1r.grad, "w1"), (w2s.grad, w2r.grad, "w2"), (w3s.grad, w3r.grad, "w3")):
+        assert rel_err(ours, ref) < BF16_TOL, nm
+        for ei, c in enumerate(counts):
+            if c == 0:
+                assert torch.count_nonzero(ours[ei]).item() == 0, f"{nm}[{ei}] of an empty expert"
+    # forward also matches the oracle's bf16 grouped-mm restatement
+    assert rel_err(y, R.experts_grouped_mm(w1, w2, w3, x, cnt)) < BF16_TOL
+
+
+def test_grouped_swiglu_deterministic(dev):
+    banner("grouped swiglu run-to-run")
+    e, d, h, counts = GEMM_CASES["uniform_e8"]
+    x, w1, w2, w3, dy, cnt = _gemm_inputs(e, d, h, counts, seed=4)
+    o = ops()
+    outs = []
+    for _ in range(2):
+        xs, w1s, w2s, w3s = (t.to(dev).requires_grad_(True) for t in (x, w1, w2, w3))
+        y, *_ = o.grouped_swiglu(xs, w1s, w2s, w3s, cnt.to(dev))
+        y.backward(dy.to(dev))
+        outs.append([y.detach(), xs.grad, w1s.grad, w2s.grad, w3s.grad])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

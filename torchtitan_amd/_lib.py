@@ -1,0 +1,97 @@
+"""ctypes binding of libmoe_mi355x.so (declared in include/moe_mi355x.h).
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already loaded (same soname, libamdhip64.so.7). There is no
+fallback: if the library is missing, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmoe_mi355x.so")
+_lib = None
+_lock = threading.Lock()
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+
+# name -> argtypes (restype int unless listed in _RESTYPES)
+SIGNATURES: dict[str, list] = {
+    "moe_router_fwd": [P, P, I64, I32, I32, I32, I32, I32, I32, F32, I32, P, P, P, P],
+    "moe_router_bwd": [P, P, P, I64, I32, I32, I32, I32, F32, P, P],
+    "moe_reorder_workspace_bytes": [I64, I32],
+    "moe_histogram": [P, I64, I32, I32, P, I64, P, P, P],
+    "moe_reorder": [P, P, I64, I32, I32, P, I64, P, P, P, P, P, P, P],
+    "moe_reorder_bwd": [P, P, I64, I32, P, P],
+    "moe_permute": [P, P, P, I64, I32, I32, I32, P, P],
+    "moe_permute_bwd": [P, P, P, P, I64, I32, I32, I32, I32, P, P, P],
+    "moe_combine": [P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_combine_bwd": [P, P, P, P, P, I64, I32, I32, I32, P, P, P],
+    "moe_grouped_swiglu_fwd": [P, P, P, P, P, I64, I32, I32, I32, P, P, P, P, P],
+    "moe_grouped_swiglu_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P, P, P],
+}
+_RESTYPES = {"moe_reorder_workspace_bytes": ctypes.c_int64}
+
+_ERRORS = {
+    -1: "invalid argument",
+    -2: "unsupported shape",
+    -3: "kernel launch failed",
+    -4: "workspace too small",
+}
+
+
+class MoEKernelError(RuntimeError):
+    pass
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise MoEKernelError(
+                    f"{_LIB_PATH} is missing: build the MI355X kernels first "
+                    "(python -m torchtitan_amd.build)"
+                )
+            handle = ctypes.CDLL(_LIB_PATH)
+            for name, argtypes in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise MoEKernelError(f"{what}: {_ERRORS.get(status, 'error')} (status {status})")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise MoEKernelError(
+                "the MI355X MoE kernels run on the GPU only; got a tensor on " f"{t.device}"
+            )

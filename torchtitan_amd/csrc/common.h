@@ -1,0 +1,131 @@
+// Shared device helpers for the MI355X (gfx950) MoE kernels.
+//
+// Everything here is written for CDNA4: 64-wide wavefronts, LDS-resident
+// scratch, bf16 stored as raw uint16_t and widened to fp32 for arithmetic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moe_mi355x.h"
+
+#define MOE_API extern "C" __attribute__((visibility("default")))
+
+namespace moe {
+
+constexpr int kWave = 64;
+
+// Status codes returned by every C-ABI entry point (mirrored in include/moe_mi355x.h).
+enum Status : int {
+  kOk = 0,
+  kErrInvalidArgument = -1,
+  kErrUnsupportedShape = -2,
+  kErrLaunch = -3,
+  kErrWorkspace = -4,
+};
+
+inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32. The narrowing conversion is round-to-nearest-even with NaN
+// mapped to the canonical quiet NaN 0x7FC0, which is what torch's bf16 casts do.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (f != f) ? 0x7fc0u : r;
+}
+
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// lo/hi bf16 of a packed dword
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// ---------------------------------------------------------------------------
+// Order-preserving map of fp32 onto uint32 used for top-k selection: larger
+// key == larger value, -0.0 sorts below +0.0 and every NaN is the largest key.
+// This is the radix order torch's GPU top-k selects in.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t radix_key(float v) {
+  uint32_t x = __float_as_uint(v);
+  uint32_t mask = (x & 0x80000000u) ? 0xffffffffu : 0x80000000u;
+  return (v == v) ? (x ^ mask) : 0xffffffffu;
+}
+
+// ---------------------------------------------------------------------------
+// Wavefront helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    uint64_t o = __shfl_xor(v, off);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Block-wide exclusive prefix sum over up to 4*blockDim.x int32 values held
+// 4 per thread (thread t owns elements 4t..4t+3). `tmp` is LDS scratch of at
+// least blockDim.x/64 ints. Returns the block total; `out` receives the
+// exclusive prefixes. Must be called by every thread of the block.
+__device__ __forceinline__ int block_exclusive_scan4(const int (&v)[4], int (&out)[4], int* tmp) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int local = v[0] + v[1] + v[2] + v[3];
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) tmp[wv] = incl;
+  __syncthreads();
+  int wave_base = 0, total = 0;
+  for (int w = 0; w < nw; ++w) {
+    int s = tmp[w];
+    if (w < wv) wave_base += s;
+    total += s;
+  }
+  __syncthreads();
+  int run = wave_base + incl - local;
+  out[0] = run; run += v[0];
+  out[1] = run; run += v[1];
+  out[2] = run; run += v[2];
+  out[3] = run;
+  return total;
+}
+
+// Wave-cooperative sum of n <= 64 fp32 values (lane x holds value x, lanes
+// >= n hold anything) in the association order of torch's GPU reduction of a
+// short contiguous row (ATen Reduce.cuh): with bw = largest power of two <= n,
+// thread x first forms v[x] + v[x+bw], then partials are combined by
+// shfl_down with offsets 1, 2, 4, ... (a pairwise tree over adjacent
+// threads). Returns the total on every lane.
+__device__ __forceinline__ float wave_torch_row_sum(float v, int n) {
+  const int lane = threadIdx.x & 63;
+  int bw = 1;
+  while (bw * 2 <= n) bw *= 2;
+  float hi = __shfl_down(v, bw);
+  float p = (lane + bw < n) ? (v + hi) : v;
+  for (int off = 1; off < bw; off <<= 1) p = p + __shfl_down(p, off);
+  return __shfl(p, 0);
+}
+
+}  // namespace moe

@@ -1,0 +1,563 @@
+// Token reordering, permute and combine for MI355X.
+//
+// Reordering (torchtitan/models/common/moe.py:291-332) is a stable counting
+// sort of the flat expert ids by (expert, token): because top-k returns
+// distinct experts per token, a token appears at most once per expert, so a
+// token's rank inside an expert segment is the number of earlier tokens that
+// chose the same expert. Each 256-token block builds, in LDS, one 64-bit
+// occupancy word per (expert, wave); ranks are popcounts of those words and
+// the per-expert segment offsets come from an atomics-free scan over the
+// per-block counts.
+//
+// Permute (moe.py:445-451) reads each token row once and writes its K copies
+// (scaled by the routing score when score_before_experts). Combine
+// (moe.py:465-475 via torchtitan/ops/scatter_add.py:10-20) reduces each
+// token's K rows in ascending sorted position, accumulating in fp32 and
+// rounding once onto the shared-expert output, which is how the reference's
+// deterministic scatter_add lowers on the GPU (index_put with accumulate,
+// duplicates summed in sorted order). All row traffic uses 128-bit accesses.
+#include "common.h"
+
+namespace moe {
+
+constexpr int kBlockTokens = 256;   // tokens per histogram / scatter block
+constexpr int kMaxExperts = 1024;   // LDS occupancy words: 1024 x 4 x 8 B = 32 KB
+constexpr int kMaxTopK = 32;
+
+// ---------------------------------------------------------------------------
+// Occupancy words: bits[e][w] bit l set <=> token (block*256 + 64*w + l) chose e.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void build_occupancy(uint64_t (*bits)[4], const int64_t* __restrict__ idx,
+                                                int64_t n_tokens, int K, int E) {
+  for (int i = threadIdx.x; i < E * 4; i += blockDim.x) (&bits[0][0])[i] = 0ull;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kBlockTokens + threadIdx.x;
+  if (t < n_tokens) {
+    for (int j = 0; j < K; ++j) {
+      const int64_t e = idx[t * K + j];
+      if (e >= 0 && e < E) atomicOr((unsigned long long*)&bits[e][wv], 1ull << lane);
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void hist_kernel(const int64_t* __restrict__ idx, int64_t n_tokens,
+                                                   int K, int E, int32_t* __restrict__ block_hist) {
+  __shared__ uint64_t bits[kMaxExperts][4];
+  build_occupancy(bits, idx, n_tokens, K, E);
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    block_hist[(int64_t)blockIdx.x * E + e] =
+        __popcll(bits[e][0]) + __popcll(bits[e][1]) + __popcll(bits[e][2]) + __popcll(bits[e][3]);
+  }
+}
+
+// Single block of 256 threads; thread t owns experts 4t..4t+3.
+// block_hist[b][e] -> block_base[b][e] = start[e] + sum_{b'<b} hist[b'][e]
+__global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ block_hist, int n_blocks,
+                                                   int E, int32_t* __restrict__ block_base,
+                                                   int64_t* __restrict__ counts,
+                                                   int32_t* __restrict__ offsets) {
+  __shared__ int tmp[8];
+  int tot[4], start[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = threadIdx.x * 4 + i;
+    int run = 0;
+    if (e < E) {
+      for (int b = 0; b < n_blocks; ++b) {
+        const int v = block_hist[(int64_t)b * E + e];
+        if (block_base) block_base[(int64_t)b * E + e] = run;
+        run += v;
+      }
+    }
+    tot[i] = run;
+  }
+  block_exclusive_scan4(tot, start, tmp);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = threadIdx.x * 4 + i;
+    if (e < E) {
+      if (counts) counts[e] = tot[i];
+      if (offsets) offsets[e] = start[i] + tot[i];
+      if (block_base)
+        for (int b = 0; b < n_blocks; ++b) block_base[(int64_t)b * E + e] += start[i];
+    }
+  }
+}
+
+struct ScatterParams {
+  const int64_t* idx;         // [N, K]
+  const float* top_scores;    // [N, K] nullable
+  const int32_t* block_base;  // [NB, E]
+  int64_t n_tokens;
+  int K, E;
+  int64_t* token_idx;       // [R] token of each sorted position
+  float* scores_sorted;     // [R] nullable
+  int32_t* slot_pos;        // [N, K] sorted position of (token, slot)
+  int32_t* tok_pos;         // [N, K] a token's sorted positions, ascending
+};
+
+__global__ __launch_bounds__(256) void scatter_kernel(ScatterParams p) {
+  __shared__ uint64_t bits[kMaxExperts][4];
+  build_occupancy(bits, p.idx, p.n_tokens, p.K, p.E);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kBlockTokens + threadIdx.x;
+  if (t >= p.n_tokens) return;
+  const int K = p.K, E = p.E;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int32_t* base = p.block_base + (int64_t)blockIdx.x * E;
+  int ev[kMaxTopK];
+  int pv[kMaxTopK];
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    ev[j] = -1;
+    pv[j] = 0;
+    if (j < K) {
+      const int64_t e = p.idx[t * K + j];
+      if (e >= 0 && e < E) {
+        int rank = __popcll(bits[e][wv] & below);
+        for (int w = 0; w < wv; ++w) rank += __popcll(bits[e][w]);
+        const int pos = base[e] + rank;
+        ev[j] = (int)e;
+        pv[j] = pos;
+        p.token_idx[pos] = t;
+        if (p.scores_sorted) p.scores_sorted[pos] = p.top_scores[t * K + j];
+        p.slot_pos[t * K + j] = pos;
+      }
+    }
+  }
+  // positions are monotone in the expert id, so ascending position == ascending expert
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    if (j < K) {
+      int r = 0;
+#pragma unroll
+      for (int i = 0; i < kMaxTopK; ++i) r += (i < K) && (ev[i] < ev[j]);
+      p.tok_pos[t * K + r] = pv[j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row movement. Rows are D elements of bf16 (uint16_t) or fp32, moved as
+// 16-byte chunks (8 bf16 or 4 fp32); arithmetic is fp32 and results are
+// rounded to the row type once, as torch's elementwise ops on that dtype do.
+// ---------------------------------------------------------------------------
+template <typename T> struct Chunk;
+template <> struct Chunk<uint16_t> {
+  static constexpr int kN = 8;
+  static __device__ __forceinline__ void unpack(uint4 v, float (&f)[8]) {
+    f[0] = bf_lo(v.x); f[1] = bf_hi(v.x); f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+    f[4] = bf_lo(v.z); f[5] = bf_hi(v.z); f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+  }
+  static __device__ __forceinline__ uint4 pack(const float (&f)[8]) {
+    return make_uint4(pack_bf2(f[0], f[1]), pack_bf2(f[2], f[3]), pack_bf2(f[4], f[5]), pack_bf2(f[6], f[7]));
+  }
+  static __device__ __forceinline__ float round(float f) { return round_bf(f); }
+};
+template <> struct Chunk<float> {
+  static constexpr int kN = 4;
+  static __device__ __forceinline__ void unpack(uint4 v, float (&f)[4]) {
+    f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+  }
+  static __device__ __forceinline__ uint4 pack(const float (&f)[4]) {
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+  }
+  static __device__ __forceinline__ float round(float f) { return f; }
+};
+
+template <typename T>
+__device__ __forceinline__ uint4 scale_chunk(uint4 v, float s) {
+  constexpr int n = Chunk<T>::kN;
+  float f[n];
+  Chunk<T>::unpack(v, f);
+#pragma unroll
+  for (int i = 0; i < n; ++i) f[i] = f[i] * s;
+  return Chunk<T>::pack(f);
+}
+
+template <typename T>
+__device__ __forceinline__ float dot_chunk(uint4 a, uint4 b) {
+  constexpr int n = Chunk<T>::kN;
+  float fa[n], fb[n];
+  Chunk<T>::unpack(a, fa);
+  Chunk<T>::unpack(b, fb);
+  float d = 0.f;
+#pragma unroll
+  for (int i = 0; i < n; ++i) d += fa[i] * fb[i];
+  return d;
+}
+
+// out[slot_pos[t,k]] = src[t] (* scores_sorted[slot_pos[t,k]]), all k < K.
+// Used for the permute (moe.py:445-451) and for the backward gather of the
+// combine (scatter_add.py:28-33), which is the same movement unscaled.
+template <typename T>
+__global__ __launch_bounds__(256) void expand_rows_kernel(const T* __restrict__ src, int64_t n_tokens,
+                                                          int D, int K,
+                                                          const int32_t* __restrict__ slot_pos,
+                                                          const float* __restrict__ scores_sorted,
+                                                          T* __restrict__ out) {
+  constexpr int n = Chunk<T>::kN;
+  const int cpr = D / n;
+  const int64_t total = n_tokens * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
+       c += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = c / cpr;
+    const int ch = (int)(c - t * cpr);
+    const uint4 v = *(const uint4*)(src + t * D + ch * n);
+    for (int j = 0; j < K; ++j) {
+      const int64_t pos = slot_pos[t * K + j];
+      const uint4 w = scores_sorted ? scale_chunk<T>(v, scores_sorted[pos]) : v;
+      *(uint4*)(out + pos * D + ch * n) = w;
+    }
+  }
+}
+
+// out[t] = round( shared[t] + sum_k r_k ), the sum in fp32 from 0 in ascending
+// sorted position; r_k = routed[pos_k], or round(routed[pos_k] * score) when
+// the score is applied after the experts (moe.py:465-469).
+template <typename T>
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shared_out,
+                                                      const T* __restrict__ routed,
+                                                      const int32_t* __restrict__ tok_pos,
+                                                      const float* __restrict__ scores_sorted,
+                                                      int64_t n_tokens, int D, int K,
+                                                      T* __restrict__ out) {
+  constexpr int n = Chunk<T>::kN;
+  const int cpr = D / n;
+  const int64_t total = n_tokens * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
+       c += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = c / cpr;
+    const int ch = (int)(c - t * cpr);
+    float a[n];
+#pragma unroll
+    for (int i = 0; i < n; ++i) a[i] = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int64_t pos = tok_pos[t * K + k];
+      uint4 v = *(const uint4*)(routed + pos * D + ch * n);
+      if (scores_sorted) v = scale_chunk<T>(v, scores_sorted[pos]);
+      float f[n];
+      Chunk<T>::unpack(v, f);
+#pragma unroll
+      for (int i = 0; i < n; ++i) a[i] += f[i];
+    }
+    float b[n];
+    if (shared_out) {
+      Chunk<T>::unpack(*(const uint4*)(shared_out + t * D + ch * n), b);
+    } else {
+#pragma unroll
+      for (int i = 0; i < n; ++i) b[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < n; ++i) b[i] = b[i] + a[i];
+    *(uint4*)(out + t * D + ch * n) = Chunk<T>::pack(b);
+  }
+}
+
+// Backward of the combine when the score is applied after the experts:
+//   grad_routed[pos] = round(grad_out[t] * s[pos]);  grad_s[pos] = sum_d grad_out[t,d] * routed[pos,d]
+// One wavefront per token.
+template <typename T, int MAXK>
+__global__ __launch_bounds__(256) void combine_bwd_scored_kernel(
+    const T* __restrict__ grad_out, const T* __restrict__ routed, const int32_t* __restrict__ tok_pos,
+    const float* __restrict__ scores_sorted, int64_t n_tokens, int D, int K, T* __restrict__ grad_routed,
+    float* __restrict__ grad_scores) {
+  constexpr int n = Chunk<T>::kN;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int cpr = D / n;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wv; t < n_tokens; t += (int64_t)gridDim.x * 4) {
+    float part[MAXK];
+    int64_t pos[MAXK];
+    float sc[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+      part[k] = 0.f;
+      pos[k] = (k < K) ? (int64_t)tok_pos[t * K + k] : 0;
+      sc[k] = (k < K) ? scores_sorted[pos[k]] : 0.f;
+    }
+    for (int ch = lane; ch < cpr; ch += kWave) {
+      const uint4 g = *(const uint4*)(grad_out + t * D + ch * n);
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k) {
+        if (k < K) {
+          const uint4 r = *(const uint4*)(routed + pos[k] * D + ch * n);
+          part[k] += dot_chunk<T>(g, r);
+          *(uint4*)(grad_routed + pos[k] * D + ch * n) = scale_chunk<T>(g, sc[k]);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+      if (k < K) {
+        const float s = wave_sum_f32(part[k]);
+        if (lane == 0) grad_scores[pos[k]] = s;
+      }
+    }
+  }
+}
+
+// Backward of routed_input = x[token_idx] (* score) (moe.py:445-451):
+//   g = grad_routed[pos]; d_xg = round(g * s) (or g unscaled);
+//   grad_x[t] accumulates d_xg over the token's positions in ascending order,
+//   rounding to the row type after every add when round_each (ATen's
+//   index_put with accumulate on row slices), else once at the end;
+//   grad_s[pos] = sum_d g * x[t]   (only when scores are given).
+// One wavefront per token.
+template <typename T, int MAXK>
+__global__ __launch_bounds__(256) void permute_bwd_kernel(
+    const T* __restrict__ grad_routed, const T* __restrict__ x, const int32_t* __restrict__ tok_pos,
+    const float* __restrict__ scores_sorted, int64_t n_tokens, int D, int K, int round_each,
+    T* __restrict__ grad_x, float* __restrict__ grad_scores) {
+  constexpr int n = Chunk<T>::kN;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int cpr = D / n;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wv; t < n_tokens; t += (int64_t)gridDim.x * 4) {
+    float part[MAXK];
+    float sc[MAXK];
+    int64_t pos[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+      part[k] = 0.f;
+      pos[k] = (k < K) ? (int64_t)tok_pos[t * K + k] : 0;
+      sc[k] = (k < K && scores_sorted) ? scores_sorted[pos[k]] : 1.0f;
+    }
+    for (int ch = lane; ch < cpr; ch += kWave) {
+      uint4 xv = make_uint4(0, 0, 0, 0);
+      if (scores_sorted) xv = *(const uint4*)(x + t * D + ch * n);
+      float a[n];
+#pragma unroll
+      for (int i = 0; i < n; ++i) a[i] = 0.f;
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k) {
+        if (k < K) {
+          uint4 g = *(const uint4*)(grad_routed + pos[k] * D + ch * n);
+          if (scores_sorted) {
+            part[k] += dot_chunk<T>(g, xv);
+            g = scale_chunk<T>(g, sc[k]);
+          }
+          float f[n];
+          Chunk<T>::unpack(g, f);
+#pragma unroll
+          for (int i = 0; i < n; ++i) a[i] = round_each ? Chunk<T>::round(a[i] + f[i]) : (a[i] + f[i]);
+        }
+      }
+      *(uint4*)(grad_x + t * D + ch * n) = Chunk<T>::pack(a);
+    }
+    if (scores_sorted && grad_scores) {
+#pragma unroll
+      for (int k = 0; k < MAXK; ++k) {
+        if (k < K) {
+          const float s = wave_sum_f32(part[k]);
+          if (lane == 0) grad_scores[pos[k]] = s;
+        }
+      }
+    }
+  }
+}
+
+// grad_top_scores[t, j] = grad_scores_sorted[slot_pos[t, j]] (backward of moe.py:325)
+__global__ __launch_bounds__(256) void gather_scores_kernel(const float* __restrict__ grad_sorted,
+                                                            const int32_t* __restrict__ slot_pos,
+                                                            int64_t n, float* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = 0.0f + grad_sorted[slot_pos[i]];
+}
+
+static int stream_grid(int64_t work, int per_block = 256, int cap = 8192) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g > cap) g = cap;
+  return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+MOE_API int64_t moe_reorder_workspace_bytes(int64_t n_tokens, int32_t n_experts) {
+  const int64_t nb = (n_tokens + kBlockTokens - 1) / kBlockTokens;
+  return 2 * nb * n_experts * (int64_t)sizeof(int32_t);
+}
+
+static int check_idx_args(int64_t n_tokens, int32_t top_k, int32_t n_experts) {
+  if (n_tokens < 0 || top_k < 1 || top_k > kMaxTopK || n_experts < 1 || n_experts > kMaxExperts ||
+      top_k > n_experts || n_tokens * top_k >= (int64_t)INT32_MAX)
+    return kErrInvalidArgument;
+  return kOk;
+}
+
+MOE_API int moe_histogram(const int64_t* selected_experts, int64_t n_tokens, int32_t top_k,
+                          int32_t n_experts, void* workspace, int64_t workspace_bytes,
+                          int64_t* counts, int32_t* offsets, hipStream_t stream) {
+  int st = check_idx_args(n_tokens, top_k, n_experts);
+  if (st) return st;
+  if (workspace_bytes < moe_reorder_workspace_bytes(n_tokens, n_experts)) return kErrWorkspace;
+  const int nb = (int)((n_tokens + kBlockTokens - 1) / kBlockTokens);
+  int32_t* block_hist = (int32_t*)workspace;
+  if (nb > 0)
+    hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
+                       top_k, n_experts, block_hist);
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, stream, block_hist, nb, n_experts,
+                     (int32_t*)nullptr, counts, offsets);
+  return launch_status();
+}
+
+MOE_API int moe_reorder(const int64_t* selected_experts, const float* top_scores, int64_t n_tokens,
+                        int32_t top_k, int32_t n_experts, void* workspace, int64_t workspace_bytes,
+                        float* scores_sorted, int64_t* token_idx, int64_t* counts, int32_t* offsets,
+                        int32_t* slot_pos, int32_t* tok_pos, hipStream_t stream) {
+  int st = check_idx_args(n_tokens, top_k, n_experts);
+  if (st) return st;
+  if (workspace_bytes < moe_reorder_workspace_bytes(n_tokens, n_experts)) return kErrWorkspace;
+  if (!slot_pos || !tok_pos || !token_idx || (scores_sorted && !top_scores)) return kErrInvalidArgument;
+  const int nb = (int)((n_tokens + kBlockTokens - 1) / kBlockTokens);
+  int32_t* block_hist = (int32_t*)workspace;
+  int32_t* block_base = block_hist + (int64_t)nb * n_experts;
+  if (nb > 0)
+    hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
+                       top_k, n_experts, block_hist);
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, stream, block_hist, nb, n_experts,
+                     block_base, counts, offsets);
+  if (nb > 0) {
+    ScatterParams p{selected_experts, top_scores, block_base, n_tokens, top_k, n_experts,
+                    token_idx, scores_sorted, slot_pos, tok_pos};
+    hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(256), 0, stream, p);
+  }
+  return launch_status();
+}
+
+MOE_API int moe_reorder_bwd(const float* grad_scores_sorted, const int32_t* slot_pos,
+                            int64_t n_tokens, int32_t top_k, float* grad_top_scores,
+                            hipStream_t stream) {
+  if (n_tokens < 0 || top_k < 1) return kErrInvalidArgument;
+  const int64_t n = n_tokens * top_k;
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(gather_scores_kernel, dim3(stream_grid(n)), dim3(256), 0, stream,
+                     grad_scores_sorted, slot_pos, n, grad_top_scores);
+  return launch_status();
+}
+
+static int check_row_args(int64_t n_tokens, int32_t dim, int32_t top_k, int32_t dtype) {
+  if (n_tokens < 0 || top_k < 1 || top_k > kMaxTopK) return kErrInvalidArgument;
+  if (dtype == MOE_DTYPE_BF16) return (dim >= 8 && dim % 8 == 0) ? kOk : kErrInvalidArgument;
+  if (dtype == MOE_DTYPE_FP32) return (dim >= 4 && dim % 4 == 0) ? kOk : kErrInvalidArgument;
+  return kErrInvalidArgument;
+}
+
+template <typename T>
+static void launch_expand(const void* src, int64_t n_tokens, int dim, int top_k, const int32_t* slot_pos,
+                          const float* scores, void* out, hipStream_t stream) {
+  hipLaunchKernelGGL(expand_rows_kernel<T>, dim3(stream_grid(n_tokens * (dim / Chunk<T>::kN))), dim3(256), 0,
+                     stream, (const T*)src, n_tokens, dim, top_k, slot_pos, scores, (T*)out);
+}
+
+template <typename T>
+static void launch_permute_bwd(const void* grad_routed, const void* x, const int32_t* tok_pos,
+                               const float* scores, int64_t n_tokens, int dim, int top_k, int round_each,
+                               void* grad_x, float* grad_scores, hipStream_t stream) {
+  const dim3 grid(stream_grid(n_tokens, 4, 16384));
+  if (top_k <= 8)
+    hipLaunchKernelGGL((permute_bwd_kernel<T, 8>), grid, dim3(256), 0, stream, (const T*)grad_routed,
+                       (const T*)x, tok_pos, scores, n_tokens, dim, top_k, round_each, (T*)grad_x, grad_scores);
+  else if (top_k <= 16)
+    hipLaunchKernelGGL((permute_bwd_kernel<T, 16>), grid, dim3(256), 0, stream, (const T*)grad_routed,
+                       (const T*)x, tok_pos, scores, n_tokens, dim, top_k, round_each, (T*)grad_x, grad_scores);
+  else
+    hipLaunchKernelGGL((permute_bwd_kernel<T, kMaxTopK>), grid, dim3(256), 0, stream, (const T*)grad_routed,
+                       (const T*)x, tok_pos, scores, n_tokens, dim, top_k, round_each, (T*)grad_x, grad_scores);
+}
+
+template <typename T>
+static void launch_combine_bwd_scored(const void* grad_out, const void* routed, const int32_t* tok_pos,
+                                      const float* scores, int64_t n_tokens, int dim, int top_k,
+                                      void* grad_routed, float* grad_scores, hipStream_t stream) {
+  const dim3 grid(stream_grid(n_tokens, 4, 16384));
+  if (top_k <= 8)
+    hipLaunchKernelGGL((combine_bwd_scored_kernel<T, 8>), grid, dim3(256), 0, stream, (const T*)grad_out,
+                       (const T*)routed, tok_pos, scores, n_tokens, dim, top_k, (T*)grad_routed, grad_scores);
+  else if (top_k <= 16)
+    hipLaunchKernelGGL((combine_bwd_scored_kernel<T, 16>), grid, dim3(256), 0, stream, (const T*)grad_out,
+                       (const T*)routed, tok_pos, scores, n_tokens, dim, top_k, (T*)grad_routed, grad_scores);
+  else
+    hipLaunchKernelGGL((combine_bwd_scored_kernel<T, kMaxTopK>), grid, dim3(256), 0, stream, (const T*)grad_out,
+                       (const T*)routed, tok_pos, scores, n_tokens, dim, top_k, (T*)grad_routed, grad_scores);
+}
+
+MOE_API int moe_permute(const void* x, const int32_t* slot_pos, const float* scores_sorted,
+                        int64_t n_tokens, int32_t dim, int32_t top_k, int32_t dtype, void* routed_input,
+                        hipStream_t stream) {
+  int st = check_row_args(n_tokens, dim, top_k, dtype);
+  if (st) return st;
+  if (n_tokens == 0) return kOk;
+  if (!x || !slot_pos || !routed_input) return kErrInvalidArgument;
+  if (dtype == MOE_DTYPE_BF16)
+    launch_expand<uint16_t>(x, n_tokens, dim, top_k, slot_pos, scores_sorted, routed_input, stream);
+  else
+    launch_expand<float>(x, n_tokens, dim, top_k, slot_pos, scores_sorted, routed_input, stream);
+  return launch_status();
+}
+
+MOE_API int moe_permute_bwd(const void* grad_routed, const void* x, const int32_t* tok_pos,
+                            const float* scores_sorted, int64_t n_tokens, int32_t dim, int32_t top_k,
+                            int32_t dtype, int32_t round_each, void* grad_x, float* grad_scores_sorted,
+                            hipStream_t stream) {
+  int st = check_row_args(n_tokens, dim, top_k, dtype);
+  if (st) return st;
+  if (scores_sorted && (!x || !grad_scores_sorted)) return kErrInvalidArgument;
+  if (n_tokens == 0) return kOk;
+  if (!grad_routed || !tok_pos || !grad_x) return kErrInvalidArgument;
+  if (dtype == MOE_DTYPE_BF16)
+    launch_permute_bwd<uint16_t>(grad_routed, x, tok_pos, scores_sorted, n_tokens, dim, top_k, round_each,
+                                 grad_x, grad_scores_sorted, stream);
+  else
+    launch_permute_bwd<float>(grad_routed, x, tok_pos, scores_sorted, n_tokens, dim, top_k, round_each,
+                              grad_x, grad_scores_sorted, stream);
+  return launch_status();
+}
+
+MOE_API int moe_combine(const void* shared_out, const void* routed_output, const int32_t* tok_pos,
+                        const float* scores_sorted, int64_t n_tokens, int32_t dim, int32_t top_k,
+                        int32_t dtype, void* out, hipStream_t stream) {
+  int st = check_row_args(n_tokens, dim, top_k, dtype);
+  if (st) return st;
+  if (n_tokens == 0) return kOk;
+  if (!routed_output || !tok_pos || !out) return kErrInvalidArgument;
+  const dim3 grid(stream_grid(n_tokens * (dim / (dtype == MOE_DTYPE_BF16 ? 8 : 4))));
+  if (dtype == MOE_DTYPE_BF16)
+    hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, dim3(256), 0, stream, (const uint16_t*)shared_out,
+                       (const uint16_t*)routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k,
+                       (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, stream, (const float*)shared_out,
+                       (const float*)routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k, (float*)out);
+  return launch_status();
+}
+
+MOE_API int moe_combine_bwd(const void* grad_out, const void* routed_output, const int32_t* slot_pos,
+                            const int32_t* tok_pos, const float* scores_sorted, int64_t n_tokens,
+                            int32_t dim, int32_t top_k, int32_t dtype, void* grad_routed,
+                            float* grad_scores_sorted, hipStream_t stream) {
+  int st = check_row_args(n_tokens, dim, top_k, dtype);
+  if (st) return st;
+  if (n_tokens == 0) return kOk;
+  if (!grad_out || !grad_routed) return kErrInvalidArgument;
+  if (scores_sorted) {
+    if (!routed_output || !grad_scores_sorted || !tok_pos) return kErrInvalidArgument;
+    if (dtype == MOE_DTYPE_BF16)
+      launch_combine_bwd_scored<uint16_t>(grad_out, routed_output, tok_pos, scores_sorted, n_tokens, dim,
+                                          top_k, grad_routed, grad_scores_sorted, stream);
+    else
+      launch_combine_bwd_scored<float>(grad_out, routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k,
+                                       grad_routed, grad_scores_sorted, stream);
+  } else {
+    if (!slot_pos) return kErrInvalidArgument;
+    if (dtype == MOE_DTYPE_BF16)
+      launch_expand<uint16_t>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, stream);
+    else
+      launch_expand<float>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, stream);
+  }
+  return launch_status();
+}

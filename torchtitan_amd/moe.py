@@ -1,0 +1,258 @@
+"""Drop-in MoE layer for MI355X: same classes, Config fields, forward signatures
+and state_dict layout as torchtitan/models/common/moe.py, with the arithmetic
+on hand-written gfx950 kernels (``torchtitan_amd.ops``).
+
+Module map (reference file:line -> here):
+  _run_experts_for_loop      moe.py:24-50    -> _run_experts_for_loop
+  _run_experts_grouped_mm    moe.py:53-70    -> _run_experts_grouped_mm (ops.grouped_swiglu)
+  GroupedExperts             moe.py:73-116   -> GroupedExperts
+  TokenChoiceTopKRouter      moe.py:119-276  -> TokenChoiceTopKRouter (gate on torch, rest ops.router)
+  TokenReorderer             moe.py:281-332  -> TokenReorderer (ops.reorder)
+  MoE                        moe.py:335-489  -> MoE (ops.permute, ops.combine)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+from torch import nn
+
+from . import ops
+from .configurable import Module
+from .feed_forward import FeedForward
+from .linear import Linear
+
+__all__ = [
+    "GroupedExperts",
+    "MoE",
+    "ReorderResult",
+    "TokenChoiceTopKRouter",
+    "TokenReorderer",
+    "_run_experts_for_loop",
+    "_run_experts_grouped_mm",
+]
+
+
+def _local(t):
+    """DTensor -> local shard (moe.py:100-111); plain tensors pass through."""
+    to_local = getattr(t, "to_local", None)
+    return to_local() if callable(to_local) else t
+
+
+def _run_experts_for_loop(
+    w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor, x: torch.Tensor,
+    num_tokens_per_expert: torch.Tensor,
+) -> torch.Tensor:
+    """Reference readability path (moe.py:24-50): per-expert matmuls in the input
+    dtype with a host sync. On MI355X this runs the same grouped kernel as
+    _run_experts_grouped_mm on rows [0, sum(counts)) in bf16, then casts back."""
+    total = int(num_tokens_per_expert.sum().item())
+    out = x.new_zeros(x.shape)
+    if total:
+        out[:total] = _run_experts_grouped_mm(w1, w2, w3, x[:total], num_tokens_per_expert)
+    return out
+
+
+def _run_experts_grouped_mm(
+    w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor, x: torch.Tensor,
+    num_tokens_per_expert: torch.Tensor,
+) -> torch.Tensor:
+    """silu(x w1^T) * (x w3^T) then w2^T per expert segment, bf16 compute with fp32
+    accumulation, output cast back to x's dtype (moe.py:53-70)."""
+    y, _, _, _ = ops.grouped_swiglu(
+        x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16(), num_tokens_per_expert
+    )
+    return y.type_as(x)
+
+
+class GroupedExperts(Module):
+    @dataclass(kw_only=True, slots=True)
+    class Config(Module.Config):
+        dim: int
+        hidden_dim: int
+        num_experts: int
+        use_grouped_mm: bool = True
+
+    def __init__(self, config: Config):
+        super().__init__()
+        self.num_experts = config.num_experts
+        self.w1 = nn.Parameter(torch.empty(config.num_experts, config.hidden_dim, config.dim))
+        self.w2 = nn.Parameter(torch.empty(config.num_experts, config.dim, config.hidden_dim))
+        self.w3 = nn.Parameter(torch.empty(config.num_experts, config.hidden_dim, config.dim))
+        self.use_grouped_mm = config.use_grouped_mm
+
+    def forward(self, x: torch.Tensor, num_tokens_per_expert: torch.Tensor) -> torch.Tensor:
+        w1, w2, w3 = _local(self.w1), _local(self.w2), _local(self.w3)
+        if self.use_grouped_mm:
+            return _run_experts_grouped_mm(w1, w2, w3, x, num_tokens_per_expert)
+        return _run_experts_for_loop(w1, w2, w3, x, num_tokens_per_expert)
+
+
+class TokenChoiceTopKRouter(Module):
+    """Token-choice top-K routing with optional group-limited selection."""
+
+    @dataclass(kw_only=True, slots=True)
+    class Config(Module.Config):
+        num_experts: int
+        gate: Linear.Config
+        num_expert_groups: int | None = None
+        num_limited_groups: int | None = None
+        top_k: int = 1
+        score_func: Literal["softmax", "sigmoid"] = "sigmoid"
+        route_norm: bool = False
+        route_scale: float = 1.0
+        _debug_force_load_balance: bool = False
+
+    def __init__(self, config: Config):
+        super().__init__()
+        self.gate = config.gate.build()
+        self.num_experts = config.num_experts
+        self.num_expert_groups = config.num_expert_groups
+        self.num_limited_groups = config.num_limited_groups
+        self.top_k = config.top_k
+        self.score_func = config.score_func
+        self.route_norm = config.route_norm
+        self.route_scale = config.route_scale
+        self._debug_force_load_balance = config._debug_force_load_balance
+
+    def _group_config(self) -> tuple[int, int]:
+        """Validates the group-limited settings with the reference's errors (moe.py:182-193)."""
+        if self.num_expert_groups is None:
+            return 0, 0
+        if self.num_limited_groups is None:
+            raise ValueError("num_limited_groups must be set when num_expert_groups is set")
+        if self.num_experts % self.num_expert_groups != 0:
+            raise ValueError(
+                f"num_experts ({self.num_experts}) must be divisible by num_expert_groups "
+                f"({self.num_expert_groups})"
+            )
+        experts_per_group = self.num_experts // self.num_expert_groups
+        if experts_per_group < 2:
+            raise ValueError(f"experts_per_group ({experts_per_group}) must be >= 2")
+        return self.num_expert_groups, self.num_limited_groups
+
+    def forward(
+        self, x: torch.Tensor, expert_bias: torch.Tensor | None = None
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """x [bs*slen, dim] -> (top_scores [N,K] f32, selected_experts_indices [N,K] i64,
+        num_tokens_per_expert [E] i64)."""
+        # fp32 gate GEMM on torch, as in the reference (moe.py:231-232)
+        with torch.autocast(device_type=x.device.type, dtype=torch.float32):
+            logits = self.gate(x)
+        if self.score_func not in ops.SCORE_FUNCS:
+            raise NotImplementedError(f"Unknown score function {self.score_func}")
+        groups, limited = self._group_config()
+        top_scores, selected, counts, _scores = ops.router(
+            logits, expert_bias, self.num_experts, self.top_k, ops.SCORE_FUNCS[self.score_func],
+            groups, limited, bool(self.route_norm), float(self.route_scale),
+            bool(self._debug_force_load_balance),
+        )
+        return top_scores, selected, counts
+
+
+class ReorderResult(tuple):
+    """(top_scores_experts_sorted, token_indices_experts_sorted, num_tokens_per_expert),
+    unpacked like the reference's 3-tuple, carrying the index layouts the permute
+    and combine kernels use: ``offsets`` [E] int32 inclusive cumsum, ``slot_pos``
+    [N,K] sorted position of each (token, slot), ``tok_pos`` [N,K] each token's
+    sorted positions in ascending order."""
+
+    offsets: torch.Tensor
+    slot_pos: torch.Tensor
+    tok_pos: torch.Tensor
+
+    def __new__(cls, scores_sorted, token_idx, counts, offsets, slot_pos, tok_pos):
+        obj = super().__new__(cls, (scores_sorted, token_idx, counts))
+        obj.offsets = offsets
+        obj.slot_pos = slot_pos
+        obj.tok_pos = tok_pos
+        return obj
+
+
+class TokenReorderer(Module):
+    """Reorders (token, slot) pairs into expert-contiguous order (moe.py:281-332)."""
+
+    def __init__(self, *, num_experts: int, top_k: int):
+        super().__init__()
+        self.num_experts = num_experts
+        self.top_k = top_k
+
+    def forward(self, top_scores: torch.Tensor, selected_experts_indices: torch.Tensor) -> ReorderResult:
+        return ReorderResult(*ops.reorder(top_scores, selected_experts_indices, self.num_experts))
+
+
+class MoE(Module):
+    @dataclass(kw_only=True, slots=True)
+    class Config(Module.Config):
+        num_experts: int = 8
+        experts: GroupedExperts.Config
+        router: TokenChoiceTopKRouter.Config
+        score_before_experts: bool = True
+        load_balance_coeff: float | None = 1e-3
+        shared_experts: FeedForward.Config | None = None
+
+    def __init__(self, config: Config):
+        super().__init__()
+        num_experts = config.num_experts
+        self.experts = config.experts.build()
+        self.router = config.router.build()
+        self.reorderer = TokenReorderer(num_experts=num_experts, top_k=config.router.top_k)
+        self.shared_experts = config.shared_experts.build() if config.shared_experts is not None else None
+        self.score_before_experts = config.score_before_experts
+        # auxiliary-loss-free load balancing state (moe.py:359-378)
+        self.load_balance_coeff = config.load_balance_coeff
+        if self.load_balance_coeff is not None:
+            assert self.load_balance_coeff > 0.0
+            self.register_buffer("expert_bias", torch.zeros(num_experts, dtype=torch.float32), persistent=True)
+        else:
+            self.expert_bias = None
+        self.register_buffer(
+            "tokens_per_expert", torch.zeros(num_experts, dtype=torch.float32), persistent=False
+        )
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """x [bs, slen, dim] -> [bs, slen, dim]."""
+        to_local = getattr(x, "to_local", None)
+        if callable(to_local):
+            from torch.distributed.tensor import Partial
+
+            assert x.device_mesh.ndim == 1, f"Expected 1D mesh, got {x.device_mesh.ndim}D mesh"
+            assert x.device_mesh.mesh_dim_names == ("tp",), (
+                f"Expected TP mesh, got mesh_dim_names={x.device_mesh.mesh_dim_names}"
+            )
+            x = x.to_local(grad_placements=(Partial(),))
+        bs, slen, dim = x.shape
+        x = x.view(-1, dim)
+
+        top_scores, selected_experts_indices, num_tokens_per_expert = self.router(x, self.expert_bias)
+        with torch.no_grad():
+            self.tokens_per_expert.add_(num_tokens_per_expert)
+
+        layout = self.reorderer(top_scores, selected_experts_indices)
+        top_scores_experts_sorted, _token_indices_experts_sorted, num_tokens_per_expert = layout
+
+        # routed_input = x[token_idx] (* score when score_before_experts)
+        routed_input = ops.permute(
+            x, layout.slot_pos, layout.tok_pos,
+            top_scores_experts_sorted if self.score_before_experts else None,
+        )
+        routed_output = self.experts(routed_input, num_tokens_per_expert)
+
+        out = self.shared_experts(x) if self.shared_experts is not None else None
+
+        # deterministic scatter-add of each token's rows onto the shared output,
+        # scaling by the score here when it was not applied before the experts
+        out = ops.combine(
+            out, routed_output, layout.slot_pos, layout.tok_pos,
+            None if self.score_before_experts else top_scores_experts_sorted,
+        )
+        return out.reshape(bs, slen, dim)
+
+    def _init_self_buffers(self, *, buffer_device: torch.device | None = None) -> None:
+        assert isinstance(buffer_device, torch.device)
+        with torch.device(buffer_device):
+            self.tokens_per_expert = torch.zeros(self.experts.num_experts, dtype=torch.float32)
+            if self.load_balance_coeff is not None:
+                self.expert_bias = torch.zeros(self.experts.num_experts, dtype=torch.float32)

@@ -1,0 +1,442 @@
+"""torch.library custom ops over the MI355X MoE kernels (namespace ``moe_mi355x``).
+
+Each op is a thin host wrapper around one C-ABI entry point of
+``libmoe_mi355x.so``: it allocates outputs and workspaces with torch's caching
+allocator, passes raw device pointers and torch's current stream, and maps
+status codes to exceptions. Every op has a fake (meta) implementation so it
+stays opaque under ``torch.compile``, and an autograd formula, following the
+registration pattern of torchtitan/ops/scatter_add.py:10-48.
+
+There is no CPU or eager-torch fallback: the ops raise on non-GPU tensors and
+when the library is missing.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from ._lib import check, lib, ptr, require_gpu, stream_of
+
+SCORE_FUNCS = {"softmax": 0, "sigmoid": 1}
+DTYPE_CODES = {torch.bfloat16: 0, torch.float32: 1}
+
+# Gradient of x[token_idx] accumulates a token's K rows with a rounding to the
+# row dtype after each add, as ATen's index_put(accumulate=True) kernel does for
+# row slices on the GPU.
+PERMUTE_BWD_ROUND_EACH = True
+
+
+def _dtype_code(t: Tensor) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise TypeError(f"MoE row kernels support bfloat16 and float32 rows, got {t.dtype}") from None
+
+
+def _workspace(n_tokens: int, num_experts: int, device: torch.device) -> Tensor:
+    nbytes = lib().moe_reorder_workspace_bytes(n_tokens, num_experts)
+    return torch.empty(max(nbytes, 4), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# router: score function, bias, group limit, top-k, gather, norm, scale
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::router", mutates_args=())
+def router(
+    logits: Tensor,
+    expert_bias: Tensor | None,
+    num_experts: int,
+    top_k: int,
+    score_func: int,
+    num_expert_groups: int,
+    num_limited_groups: int,
+    route_norm: bool,
+    route_scale: float,
+    force_load_balance: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Returns (top_scores [N,K] f32, selected_experts [N,K] i64, counts [E] i64, scores [N,E] f32)."""
+    require_gpu(logits, expert_bias)
+    logits = logits.float().contiguous()
+    n = logits.shape[0]
+    dev = logits.device
+    bias = expert_bias.float().contiguous() if expert_bias is not None else None
+    scores = torch.empty_like(logits)
+    top_scores = torch.empty(n, top_k, dtype=torch.float32, device=dev)
+    idx = torch.empty(n, top_k, dtype=torch.int64, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    s = stream_of(logits)
+    check(
+        lib().moe_router_fwd(
+            ptr(logits), ptr(bias), n, num_experts, top_k, score_func, num_expert_groups,
+            num_limited_groups, int(route_norm), route_scale, int(force_load_balance),
+            ptr(scores), ptr(top_scores), ptr(idx), s,
+        ),
+        "moe_router_fwd",
+    )
+    ws = _workspace(n, num_experts, dev)
+    check(
+        lib().moe_histogram(ptr(idx), n, top_k, num_experts, ptr(ws), ws.numel(), ptr(counts), None, s),
+        "moe_histogram",
+    )
+    return top_scores, idx, counts, scores
+
+
+@router.register_fake
+def _(logits, expert_bias, num_experts, top_k, score_func, num_expert_groups, num_limited_groups,
+      route_norm, route_scale, force_load_balance):
+    n = logits.shape[0]
+    return (
+        logits.new_empty(n, top_k, dtype=torch.float32),
+        logits.new_empty(n, top_k, dtype=torch.int64),
+        logits.new_empty(num_experts, dtype=torch.int64),
+        logits.new_empty(logits.shape, dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op("moe_mi355x::router_backward", mutates_args=())
+def router_backward(
+    grad_top_scores: Tensor, scores: Tensor, selected_experts: Tensor, score_func: int,
+    route_norm: bool, route_scale: float,
+) -> Tensor:
+    require_gpu(grad_top_scores, scores, selected_experts)
+    g = grad_top_scores.float().contiguous()
+    n, e = scores.shape
+    k = selected_experts.shape[1]
+    out = torch.empty_like(scores)
+    check(
+        lib().moe_router_bwd(ptr(g), ptr(scores), ptr(selected_experts), n, e, k, score_func,
+                             int(route_norm), route_scale, ptr(out), stream_of(scores)),
+        "moe_router_bwd",
+    )
+    return out
+
+
+@router_backward.register_fake
+def _(grad_top_scores, scores, selected_experts, score_func, route_norm, route_scale):
+    return torch.empty_like(scores)
+
+
+def _router_setup(ctx, inputs, output):
+    (_logits, _bias, _e, _k, score_func, _g, _gk, route_norm, route_scale, _flb) = inputs
+    _top, idx, counts, scores = output
+    ctx.save_for_backward(scores, idx)
+    ctx.cfg = (score_func, route_norm, route_scale)
+    ctx.mark_non_differentiable(idx, counts, scores)
+
+
+def _router_bwd(ctx, g_top, _g_idx, _g_counts, _g_scores):
+    scores, idx = ctx.saved_tensors
+    score_func, route_norm, route_scale = ctx.cfg
+    if g_top is None:
+        g_top = torch.zeros(idx.shape, dtype=torch.float32, device=idx.device)
+    grad_logits = router_backward(g_top, scores, idx, score_func, route_norm, route_scale)
+    return grad_logits, None, None, None, None, None, None, None, None, None
+
+
+router.register_autograd(_router_bwd, setup_context=_router_setup)
+
+
+# ---------------------------------------------------------------------------
+# reorder: counting-sort permutation by expert
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::reorder", mutates_args=())
+def reorder(
+    top_scores: Tensor, selected_experts: Tensor, num_experts: int
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Returns (scores_sorted [R] f32, token_idx [R] i64, counts [E] i64,
+    offsets [E] i32, slot_pos [N,K] i32, tok_pos [N,K] i32)."""
+    require_gpu(top_scores, selected_experts)
+    idx = selected_experts.contiguous()
+    ts = top_scores.float().contiguous()
+    n, k = idx.shape
+    dev = idx.device
+    r = n * k
+    scores_sorted = torch.empty(r, dtype=torch.float32, device=dev)
+    token_idx = torch.empty(r, dtype=torch.int64, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    offsets = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    slot_pos = torch.empty(n, k, dtype=torch.int32, device=dev)
+    tok_pos = torch.empty(n, k, dtype=torch.int32, device=dev)
+    ws = _workspace(n, num_experts, dev)
+    check(
+        lib().moe_reorder(ptr(idx), ptr(ts), n, k, num_experts, ptr(ws), ws.numel(),
+                          ptr(scores_sorted), ptr(token_idx), ptr(counts), ptr(offsets),
+                          ptr(slot_pos), ptr(tok_pos), stream_of(idx)),
+        "moe_reorder",
+    )
+    return scores_sorted, token_idx, counts, offsets, slot_pos, tok_pos
+
+
+@reorder.register_fake
+def _(top_scores, selected_experts, num_experts):
+    n, k = selected_experts.shape
+    e = selected_experts
+    return (
+        e.new_empty(n * k, dtype=torch.float32),
+        e.new_empty(n * k, dtype=torch.int64),
+        e.new_empty(num_experts, dtype=torch.int64),
+        e.new_empty(num_experts, dtype=torch.int32),
+        e.new_empty(n, k, dtype=torch.int32),
+        e.new_empty(n, k, dtype=torch.int32),
+    )
+
+
+@torch.library.custom_op("moe_mi355x::reorder_backward", mutates_args=())
+def reorder_backward(grad_scores_sorted: Tensor, slot_pos: Tensor) -> Tensor:
+    require_gpu(grad_scores_sorted, slot_pos)
+    g = grad_scores_sorted.float().contiguous()
+    n, k = slot_pos.shape
+    out = torch.empty(n, k, dtype=torch.float32, device=g.device)
+    check(lib().moe_reorder_bwd(ptr(g), ptr(slot_pos), n, k, ptr(out), stream_of(g)), "moe_reorder_bwd")
+    return out
+
+
+@reorder_backward.register_fake
+def _(grad_scores_sorted, slot_pos):
+    return slot_pos.new_empty(slot_pos.shape, dtype=torch.float32)
+
+
+def _reorder_setup(ctx, inputs, output):
+    _ts, _idx, _e = inputs
+    _ss, token_idx, counts, offsets, slot_pos, tok_pos = output
+    ctx.save_for_backward(slot_pos)
+    ctx.mark_non_differentiable(token_idx, counts, offsets, slot_pos, tok_pos)
+
+
+def _reorder_bwd(ctx, g_sorted, *_ignored):
+    (slot_pos,) = ctx.saved_tensors
+    if g_sorted is None:
+        return None, None, None
+    return reorder_backward(g_sorted, slot_pos), None, None
+
+
+reorder.register_autograd(_reorder_bwd, setup_context=_reorder_setup)
+
+
+# ---------------------------------------------------------------------------
+# permute: routed_input = x[token_idx] (* score)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::permute", mutates_args=())
+def permute(x: Tensor, slot_pos: Tensor, tok_pos: Tensor, scores_sorted: Tensor | None) -> Tensor:
+    require_gpu(x, slot_pos, scores_sorted)
+    x = x.contiguous()
+    n, d = x.shape
+    k = slot_pos.shape[1]
+    out = x.new_empty(n * k, d)
+    sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
+    check(
+        lib().moe_permute(ptr(x), ptr(slot_pos), ptr(sc), n, d, k, _dtype_code(x), ptr(out), stream_of(x)),
+        "moe_permute",
+    )
+    return out
+
+
+@permute.register_fake
+def _(x, slot_pos, tok_pos, scores_sorted):
+    return x.new_empty(x.shape[0] * slot_pos.shape[1], x.shape[1])
+
+
+@torch.library.custom_op("moe_mi355x::permute_backward", mutates_args=())
+def permute_backward(
+    grad_routed: Tensor, x: Tensor, tok_pos: Tensor, scores_sorted: Tensor | None, round_each: bool
+) -> tuple[Tensor, Tensor]:
+    require_gpu(grad_routed, x, tok_pos, scores_sorted)
+    g = grad_routed.contiguous()
+    n, d = x.shape
+    k = tok_pos.shape[1]
+    grad_x = x.new_empty(n, d)
+    grad_s = torch.empty(n * k if scores_sorted is not None else 0, dtype=torch.float32, device=x.device)
+    sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
+    check(
+        lib().moe_permute_bwd(ptr(g), ptr(x), ptr(tok_pos), ptr(sc), n, d, k, _dtype_code(x),
+                              int(round_each), ptr(grad_x), ptr(grad_s) if sc is not None else None,
+                              stream_of(x)),
+        "moe_permute_bwd",
+    )
+    return grad_x, grad_s
+
+
+@permute_backward.register_fake
+def _(grad_routed, x, tok_pos, scores_sorted, round_each):
+    k = tok_pos.shape[1]
+    ns = x.shape[0] * k if scores_sorted is not None else 0
+    return x.new_empty(x.shape), x.new_empty(ns, dtype=torch.float32)
+
+
+def _permute_setup(ctx, inputs, output):
+    x, slot_pos, tok_pos, scores_sorted = inputs
+    ctx.has_scores = scores_sorted is not None
+    ctx.save_for_backward(x, tok_pos, scores_sorted if scores_sorted is not None else None)
+
+
+def _permute_bwd(ctx, g):
+    x, tok_pos, scores_sorted = ctx.saved_tensors
+    grad_x, grad_s = permute_backward(g, x, tok_pos, scores_sorted if ctx.has_scores else None,
+                                      PERMUTE_BWD_ROUND_EACH)
+    return grad_x, None, None, (grad_s if ctx.has_scores else None)
+
+
+permute.register_autograd(_permute_bwd, setup_context=_permute_setup)
+
+
+# ---------------------------------------------------------------------------
+# grouped SwiGLU experts: _run_experts_grouped_mm
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::grouped_swiglu", mutates_args=())
+def grouped_swiglu(
+    x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """bf16 grouped SwiGLU. Returns (y [R,D], g [R,H], u [R,H], h [R,H]); g, u, h are
+    the saved activations for the backward."""
+    require_gpu(x, w1, w2, w3, num_tokens_per_expert)
+    for t, name in ((x, "x"), (w1, "w1"), (w2, "w2"), (w3, "w3")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"grouped_swiglu expects bfloat16 {name}, got {t.dtype}")
+    x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    g = x.new_empty(r, h_dim)
+    u = x.new_empty(r, h_dim)
+    h = x.new_empty(r, h_dim)
+    y = x.new_empty(r, d)
+    check(
+        lib().moe_grouped_swiglu_fwd(ptr(x), ptr(w1), ptr(w2), ptr(w3), ptr(counts), r, e, d, h_dim,
+                                     ptr(g), ptr(u), ptr(h), ptr(y), stream_of(x)),
+        "moe_grouped_swiglu_fwd",
+    )
+    return y, g, u, h
+
+
+@grouped_swiglu.register_fake
+def _(x, w1, w2, w3, num_tokens_per_expert):
+    r, d = x.shape
+    h_dim = w1.shape[1]
+    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_backward", mutates_args=())
+def grouped_swiglu_backward(
+    dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
+    g: Tensor, u: Tensor, h: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
+    dy = dy.to(torch.bfloat16).contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    dgu = x.new_empty(r, 2 * h_dim)
+    dx = x.new_empty(r, d)
+    dw1 = torch.empty_like(w1)
+    dw2 = torch.empty_like(w2)
+    dw3 = torch.empty_like(w3)
+    check(
+        lib().moe_grouped_swiglu_bwd(ptr(dy), ptr(x), ptr(w1), ptr(w2), ptr(w3), ptr(counts), ptr(g),
+                                     ptr(u), ptr(h), r, e, d, h_dim, ptr(dgu), ptr(dx), ptr(dw1),
+                                     ptr(dw2), ptr(dw3), stream_of(x)),
+        "moe_grouped_swiglu_bwd",
+    )
+    return dx, dw1, dw2, dw3
+
+
+@grouped_swiglu_backward.register_fake
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h):
+    return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
+
+
+def _gs_setup(ctx, inputs, output):
+    x, w1, w2, w3, counts = inputs
+    _y, g, u, h = output
+    ctx.save_for_backward(x, w1, w2, w3, counts, g, u, h)
+    ctx.mark_non_differentiable(g, u, h)
+
+
+def _gs_bwd(ctx, dy, _dg, _du, _dh):
+    x, w1, w2, w3, counts, g, u, h = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None, None
+    dx, dw1, dw2, dw3 = grouped_swiglu_backward(dy, x, w1, w2, w3, counts, g, u, h)
+    return dx, dw1, dw2, dw3, None
+
+
+grouped_swiglu.register_autograd(_gs_bwd, setup_context=_gs_setup)
+
+
+# ---------------------------------------------------------------------------
+# combine: out = shared + sum of a token's routed rows (deterministic)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::combine", mutates_args=())
+def combine(
+    shared_out: Tensor | None, routed_output: Tensor, slot_pos: Tensor, tok_pos: Tensor,
+    scores_sorted: Tensor | None,
+) -> Tensor:
+    require_gpu(shared_out, routed_output, tok_pos, scores_sorted)
+    routed = routed_output.contiguous()
+    n, k = tok_pos.shape
+    d = routed.shape[1]
+    base = shared_out.to(routed.dtype).contiguous() if shared_out is not None else None
+    out = routed.new_empty(n, d)
+    sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
+    check(
+        lib().moe_combine(ptr(base), ptr(routed), ptr(tok_pos), ptr(sc), n, d, k, _dtype_code(routed),
+                          ptr(out), stream_of(routed)),
+        "moe_combine",
+    )
+    return out
+
+
+@combine.register_fake
+def _(shared_out, routed_output, slot_pos, tok_pos, scores_sorted):
+    return routed_output.new_empty(tok_pos.shape[0], routed_output.shape[1])
+
+
+@torch.library.custom_op("moe_mi355x::combine_backward", mutates_args=())
+def combine_backward(
+    grad_out: Tensor, routed_output: Tensor, slot_pos: Tensor, tok_pos: Tensor,
+    scores_sorted: Tensor | None,
+) -> tuple[Tensor, Tensor]:
+    require_gpu(grad_out, routed_output, slot_pos, tok_pos, scores_sorted)
+    g = grad_out.to(routed_output.dtype).contiguous()
+    n, k = tok_pos.shape
+    d = g.shape[1]
+    grad_routed = g.new_empty(n * k, d)
+    grad_s = torch.empty(n * k if scores_sorted is not None else 0, dtype=torch.float32, device=g.device)
+    sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
+    check(
+        lib().moe_combine_bwd(ptr(g), ptr(routed_output), ptr(slot_pos), ptr(tok_pos), ptr(sc), n, d, k,
+                              _dtype_code(g), ptr(grad_routed), ptr(grad_s) if sc is not None else None,
+                              stream_of(g)),
+        "moe_combine_bwd",
+    )
+    return grad_routed, grad_s
+
+
+@combine_backward.register_fake
+def _(grad_out, routed_output, slot_pos, tok_pos, scores_sorted):
+    n, k = tok_pos.shape
+    ns = n * k if scores_sorted is not None else 0
+    return routed_output.new_empty(n * k, routed_output.shape[1]), grad_out.new_empty(ns, dtype=torch.float32)
+
+
+def _combine_setup(ctx, inputs, output):
+    shared_out, routed_output, slot_pos, tok_pos, scores_sorted = inputs
+    ctx.has_shared = shared_out is not None
+    ctx.shared_dtype = shared_out.dtype if shared_out is not None else None
+    ctx.has_scores = scores_sorted is not None
+    ctx.save_for_backward(routed_output if ctx.has_scores else None, slot_pos, tok_pos, scores_sorted)
+
+
+def _combine_bwd(ctx, g):
+    routed, slot_pos, tok_pos, scores_sorted = ctx.saved_tensors
+    if ctx.has_scores:
+        grad_routed, grad_s = combine_backward(g, routed, slot_pos, tok_pos, scores_sorted)
+    else:
+        dummy = g.new_empty(0, g.shape[1])
+        grad_routed, _ = combine_backward(g, dummy, slot_pos, tok_pos, None)
+        grad_s = None
+    grad_shared = g.to(ctx.shared_dtype) if ctx.has_shared else None
+    return grad_shared, grad_routed, None, None, grad_s
+
+
+combine.register_autograd(_combine_bwd, setup_context=_combine_setup)
