@@ -1,0 +1,338 @@
+"""Benchmark of the MI355X MoE layer hot path (forward + backward of one MoE layer).
+
+Workload (default): the Kimi-Linear-48B-A3B-shape MoE layer, bf16 — dim 2304,
+256 routed experts, top-8 sigmoid scores + per-expert bias ~ U(-0.01, 0.01),
+route norm on, route scale 2.5, SwiGLU experts with hidden 1024 plus one shared
+SwiGLU expert with hidden 1024, 16384 tokens (batch 4 x seq 4096), x ~ N(0,1),
+weights N(0, 0.02), backward seeded with g ~ N(0,1). Synthetic data and
+random-init weights; everything is resident in HBM before timing starts.
+
+A step is MoE.forward + backward of that layer (torchtitan/models/common/moe.py:380-477
+and its autograd). The JSON line reports routed tokens/s (N*K per step), the
+grouped-GEMM TFLOP/s over the six grouped GEMM kernels, per-kernel HIP-event
+timings taken inside the timed steps, the roofline of the dominant kernel, and
+the reference's CPU MoE path (the oracle's op-for-op restatement) timed on a
+bounded token sample on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload kimi|dsv3|zipf]
+                       [--no-cpu-baseline] [--cpu-tokens N]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+
+WORKLOADS = {
+    # name: dict of layer shape and routing settings
+    "kimi": dict(
+        desc="Kimi-Linear-48B-A3B-shape MoE layer",
+        bs=4, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+        score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.01, zipf=None,
+    ),
+    "dsv3": dict(
+        desc="DeepSeek-V3-style group-limited MoE layer",
+        bs=1, slen=8192, dim=7168, experts=256, top_k=8, hidden=2048, shared_hidden=2048,
+        score_func="sigmoid", route_norm=True, route_scale=2.5, groups=8, limited=4,
+        score_before=False, std=0.006, bias=0.01, zipf=None,
+    ),
+    "zipf": dict(
+        desc="Kimi-shape MoE layer with Zipf(1.2)-skewed expert load",
+        bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+        score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.01, zipf=1.2,
+    ),
+}
+
+GEMM_ENTRIES = (
+    "moe_grouped_gemm_gate_up",
+    "moe_grouped_gemm_down",
+    "moe_grouped_gemm_bwd_dgu",
+    "moe_grouped_gemm_bwd_dx",
+    "moe_grouped_gemm_bwd_dw13",
+    "moe_grouped_gemm_bwd_dw2",
+)
+
+
+def kernel_work(name: str, w: dict) -> tuple[str, float]:
+    """Algorithmic work of one launch of C-ABI entry `name` for workload `w`:
+    ("mfma", flops) for the grouped GEMMs, ("hbm", bytes) for the data movers.
+    Bytes count each tensor element the launch must read or write once."""
+    n = w["bs"] * w["slen"]
+    d, e, k, h = w["dim"], w["experts"], w["top_k"], w["hidden"]
+    r = n * k
+    b = 2  # bf16 rows
+    flops = {
+        "moe_grouped_gemm_gate_up": 4 * r * d * h,
+        "moe_grouped_gemm_down": 2 * r * d * h,
+        "moe_grouped_gemm_bwd_dgu": 2 * r * d * h,
+        "moe_grouped_gemm_bwd_dx": 4 * r * d * h,
+        "moe_grouped_gemm_bwd_dw13": 4 * r * d * h,
+        "moe_grouped_gemm_bwd_dw2": 2 * r * d * h,
+    }
+    if name in flops:
+        return "mfma", float(flops[name])
+    nbytes = {
+        # logits [N,E] f32 read; scores [N,E] f32, top scores f32 and ids i64 [N,K] written
+        "moe_router_fwd": 4 * n * e + 4 * n * e + 12 * n * k,
+        "moe_histogram": 8 * n * k + 8 * e,
+        # ids read twice (histogram + scatter), sorted scores/token ids and two int32 maps written
+        "moe_reorder": 16 * n * k + 4 * n * k + 4 * r + 8 * r + 8 * n * k,
+        # x read once, K copies written, slot map + sorted scores read
+        "moe_permute": n * d * b + r * d * b + 4 * n * k + 4 * r,
+        # routed rows + shared rows read, out written, tok map + scores read
+        "moe_combine": r * d * b + 2 * n * d * b + 4 * n * k,
+        # grad_out read, K copies written (score_before) or + routed rows read (score_after)
+        "moe_combine_bwd": n * d * b + r * d * b + 4 * n * k,
+        # grad_routed read, x read, grad_x written, score grads written
+        "moe_permute_bwd": r * d * b + 2 * n * d * b + 4 * n * k + 8 * r,
+        "moe_reorder_bwd": 4 * r + 4 * n * k + 4 * n * k,
+        "moe_router_bwd": 4 * n * k + 8 * n * k + 4 * n * e + 4 * n * e,
+    }
+    return "hbm", float(nbytes.get(name, 0))
+
+
+def make_layer(w: dict, device: torch.device, seed: int):
+    from torchtitan_amd import FeedForward, GroupedExperts, Linear, MoE, TokenChoiceTopKRouter
+
+    d, e, h, hs = w["dim"], w["experts"], w["hidden"], w["shared_hidden"]
+    cfg = MoE.Config(
+        num_experts=e,
+        experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e),
+        router=TokenChoiceTopKRouter.Config(
+            num_experts=e, gate=Linear.Config(in_features=d, out_features=e), top_k=w["top_k"],
+            score_func=w["score_func"], route_norm=w["route_norm"], route_scale=w["route_scale"],
+            num_expert_groups=w["groups"], num_limited_groups=w["limited"],
+        ),
+        score_before_experts=w["score_before"],
+        load_balance_coeff=1e-3,
+        shared_experts=FeedForward.Config(
+            w1=Linear.Config(in_features=d, out_features=hs),
+            w2=Linear.Config(in_features=hs, out_features=d),
+            w3=Linear.Config(in_features=d, out_features=hs),
+        ) if hs else None,
+    )
+    with torch.device("meta"):
+        moe = cfg.build()
+    moe = moe.to_empty(device=device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in moe.named_parameters():
+            p.data = torch.empty(p.shape, dtype=torch.bfloat16, device=device).normal_(0.0, w["std"], generator=gen)
+        bias = (torch.rand(e, generator=gen, device=device) * 2 - 1) * w["bias"]
+        if w["zipf"]:
+            # Zipf(s) per-expert boost on a random expert order: a few experts take
+            # most tokens and a tail of experts gets none.
+            ranks = torch.randperm(e, generator=gen, device=device).float() + 1.0
+            bias = bias + 0.35 * ranks.pow(-w["zipf"]) * e ** 0.0 - 0.35 * (ranks > e * 0.9).float()
+        moe.expert_bias.copy_(bias)
+        moe.tokens_per_expert.zero_()
+    return moe
+
+
+def cpu_baseline(moe, w: dict, x: torch.Tensor, g: torch.Tensor, n_tokens: int) -> dict:
+    """The reference's CPU MoE path (oracle restatement of moe.py:380-477 with the
+    same torch calls; histc -> bincount on the CPU) on the first n_tokens tokens,
+    forward + backward, 1 warmup + median of 3, on this host's cores."""
+    from oracle import moe_ref as R
+
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(threads)
+    sd = {k: v.detach().cpu() for k, v in moe.state_dict().items()}
+    params = {
+        "gate": sd["router.gate.weight"], "w1": sd["experts.w1"], "w2": sd["experts.w2"],
+        "w3": sd["experts.w3"], "expert_bias": sd["expert_bias"],
+    }
+    if w["shared_hidden"]:
+        params.update(sw1=sd["shared_experts.w1.weight"], sw2=sd["shared_experts.w2.weight"],
+                      sw3=sd["shared_experts.w3.weight"])
+    for k in ("gate", "w1", "w2", "w3", "sw1", "sw2", "sw3"):
+        if k in params:
+            params[k].requires_grad_(True)
+    rc = R.RouterCfg(num_experts=w["experts"], top_k=w["top_k"], score_func=w["score_func"],
+                     num_expert_groups=w["groups"], num_limited_groups=w["limited"],
+                     route_norm=w["route_norm"], route_scale=w["route_scale"])
+    cfg = R.MoECfg(router=rc, dim=w["dim"], hidden_dim=w["hidden"], score_before_experts=w["score_before"],
+                   use_grouped_mm=True, has_shared=bool(w["shared_hidden"]))
+    xs = x.reshape(-1, w["dim"])[:n_tokens].detach().cpu().reshape(1, n_tokens, w["dim"])
+    gs = g.reshape(-1, w["dim"])[:n_tokens].detach().cpu().reshape(1, n_tokens, w["dim"])
+    times = []
+    for it in range(4):
+        for p in params.values():
+            p.grad = None
+        xi = xs.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        out = R.moe_forward_reference_ops(params, xi, cfg)
+        out.backward(gs)
+        times.append(time.perf_counter() - t0)
+        print(f"[bench] cpu baseline iteration {it}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
+    t = statistics.median(times[1:])
+    return {
+        "value": n_tokens * w["top_k"] / t,
+        "unit": "routed tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference op sequence (torch ops, CPU, bf16 grouped_mm) fwd+bwd on the first "
+                   f"{n_tokens} of {w['bs'] * w['slen']} tokens of the same layer; median of 3 after 1 warmup; "
+                   f"{t:.2f} s/iter"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="kimi", choices=sorted(WORKLOADS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the MoE layer runs with all experts resident on a single "
+              "MI355X (no expert parallelism, no collectives); --gpus above 1 is not supported.",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    from torchtitan_amd import _lib
+
+    _lib.lib()  # fail loudly if the HIP library is missing
+    w = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n = w["bs"] * w["slen"]
+    k = w["top_k"]
+    moe = make_layer(w, dev, args.seed)
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    x = torch.randn(w["bs"], w["slen"], w["dim"], generator=gen, device=dev).bfloat16()
+    g = torch.randn(w["bs"], w["slen"], w["dim"], generator=gen, device=dev).bfloat16()
+    x.requires_grad_(True)
+    params = list(moe.parameters())
+
+    def step():
+        for p in params:
+            p.grad = None
+        x.grad = None
+        out = moe(x)
+        out.backward(g)
+
+    print(f"[bench] workload {args.workload}: warmup {args.warmup}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        counts = moe.router(x.detach().view(-1, w["dim"]), moe.expert_bias)[2].cpu()
+
+    timer = _lib.KernelTimer()
+    _lib.set_timer(timer)
+    print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.set_timer(None)
+    ms = (t1 - t0) * 1e3 / args.steps
+
+    durations = timer.durations_ms()
+    kernels = {}
+    for name, ds in sorted(durations.items()):
+        per_step = len(ds) / args.steps
+        avg = sum(ds) / len(ds)
+        bound, work = kernel_work(name, w)
+        if bound == "mfma":
+            achieved, peak, unit = work / (avg * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+        else:
+            achieved, peak, unit = work / (avg * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+        kernels[name] = {
+            "launches_per_step": per_step, "avg_ms": round(avg, 4), "bound": bound,
+            "achieved": round(achieved, 1), "unit": unit, "frac": round(achieved / peak, 4),
+        }
+    gemm_ms = sum(kernels[nm]["avg_ms"] * kernels[nm]["launches_per_step"] for nm in GEMM_ENTRIES if nm in kernels)
+    gemm_flops = 18.0 * n * k * w["dim"] * w["hidden"]
+    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
+    dom = max(kernels, key=lambda nm: kernels[nm]["avg_ms"] * kernels[nm]["launches_per_step"])
+    dk = kernels[dom]
+    roofline = {
+        "kernel": dom,
+        "bound": dk["bound"],
+        "achieved": dk["achieved"],
+        "peak": PEAK_BF16_TFLOPS if dk["bound"] == "mfma" else PEAK_HBM_GBS,
+        "unit": dk["unit"],
+        "frac": dk["frac"],
+        "traffic": None,
+    }
+    mover = ("moe_permute", "moe_combine", "moe_combine_bwd", "moe_permute_bwd")
+    mover_ms = sum(kernels[m]["avg_ms"] for m in mover if m in kernels)
+    mover_bytes = sum(kernel_work(m, w)[1] for m in mover if m in kernels)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print(f"[bench] cpu baseline on {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(moe, w, x, g, min(args.cpu_tokens, n))
+
+    line = {
+        "metric": "MoE layer fwd+bwd routed tokens/s; grouped-GEMM TFLOPS as % of MFMA peak",
+        "value": round(n * k / (ms * 1e-3), 1),
+        "unit": "routed tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, x ~ N(0,1), g ~ N(0,1))",
+        "config": {
+            "workload": f"{w['desc']}: N={n} tokens (bs {w['bs']} x seq {w['slen']}), dim {w['dim']}, "
+                        f"{w['experts']} experts top-{k} {w['score_func']}"
+                        f"{' group-limited ' + str(w['limited']) + '/' + str(w['groups']) if w['groups'] else ''}"
+                        f" + bias, hidden {w['hidden']}, shared hidden {w['shared_hidden']}, fwd+bwd",
+            "tokens": n, "dim": w["dim"], "num_experts": w["experts"], "top_k": k,
+            "hidden": w["hidden"], "shared_hidden": w["shared_hidden"],
+            "parallelism": "single GPU, all experts resident",
+        },
+        "tokens_per_s": round(n / (ms * 1e-3), 1),
+        "grouped_gemm": {
+            "ms_per_step": round(gemm_ms, 4),
+            "tflops": round(gemm_tflops, 1),
+            "frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        },
+        "permute_combine": {
+            "ms_per_step": round(mover_ms, 4),
+            "gbs": round(mover_bytes / (mover_ms * 1e-3) / 1e9, 1) if mover_ms else None,
+            "frac_of_peak": round(mover_bytes / (mover_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if mover_ms else None,
+        },
+        "expert_load": {"max": int(counts.max()), "mean": float(counts.float().mean()),
+                        "empty": int((counts == 0).sum())},
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

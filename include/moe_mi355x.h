@@ -108,9 +108,10 @@ int moe_permute_bwd(const void* grad_routed, const void* x, const int32_t* tok_p
 /* out = deterministic_scatter_add(shared_out, token_idx, routed_output)
  * (torchtitan/ops/scatter_add.py:10-20, called at moe.py:471-475), with the
  * score_after scaling of moe.py:465-469 fused when scores_sorted != NULL.
- * shared_out [N,D] or NULL (zeros), routed_output [R,D] -> out [N,D]. Each
- * token's K rows are summed in fp32 from zero in ascending sorted position
- * and added to shared_out with one rounding. */
+ * shared_out [N,D] or NULL (zeros), routed_output [R,D] -> out [N,D].
+ * Starting from shared_out[t], token t's K rows are added in ascending sorted
+ * position with a rounding to the row type after every add (the order and
+ * rounding of the reference's deterministic scatter_add on the GPU). */
 int moe_combine(const void* shared_out, const void* routed_output, const int32_t* tok_pos,
                 const float* scores_sorted, int64_t n_tokens, int32_t dim, int32_t top_k,
                 int32_t dtype, void* out, moe_stream_t stream);
@@ -136,13 +137,46 @@ int moe_grouped_swiglu_fwd(const uint16_t* x, const uint16_t* w1, const uint16_t
 /* Autograd of _run_experts_grouped_mm (the three torch._grouped_mm backward
  * passes plus SwiGLU backward): dy [R,D] -> dx [R,D], dw1,dw3 [E,H,D],
  * dw2 [E,D,H] (experts with no tokens get zero gradients).
- * dgu_workspace is [R, 2H] bf16. */
+ * dgu_workspace is [R, 2H] bf16. Runs the four backward kernels below in
+ * order. */
 int moe_grouped_swiglu_bwd(const uint16_t* dy, const uint16_t* x, const uint16_t* w1,
                            const uint16_t* w2, const uint16_t* w3, const int64_t* counts,
                            const uint16_t* g, const uint16_t* u, const uint16_t* h,
                            int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
                            uint16_t* dgu_workspace, uint16_t* dx, uint16_t* dw1, uint16_t* dw2,
                            uint16_t* dw3, moe_stream_t stream);
+
+/* The grouped GEMM kernels one at a time (each is one launch). Same shapes and
+ * conventions as moe_grouped_swiglu_fwd / _bwd above.
+ *
+ * gate_up: the first two torch._grouped_mm of moe.py:62-67 fused with SwiGLU:
+ *   g = x.w1^T, u = x.w3^T, h = bf16(bf16(silu(g)) * u). */
+int moe_grouped_gemm_gate_up(const uint16_t* x, const uint16_t* w1, const uint16_t* w3,
+                             const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                             int32_t dim, int32_t hidden, uint16_t* g, uint16_t* u, uint16_t* h,
+                             moe_stream_t stream);
+/* down: y = h.w2^T (moe.py:68). */
+int moe_grouped_gemm_down(const uint16_t* h, const uint16_t* w2, const int64_t* counts,
+                          int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                          uint16_t* y, moe_stream_t stream);
+/* bwd_dgu: dh = dy.w2 (grad of moe.py:68 w.r.t. h) and the SwiGLU backward:
+ * dgu [R,2H] = [dg | du]. */
+int moe_grouped_gemm_bwd_dgu(const uint16_t* dy, const uint16_t* w2, const uint16_t* g,
+                             const uint16_t* u, const int64_t* counts, int64_t n_rows,
+                             int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dgu,
+                             moe_stream_t stream);
+/* bwd_dx: dx = dg.w1 + du.w3 (one GEMM over the concatenated 2H axis). */
+int moe_grouped_gemm_bwd_dx(const uint16_t* dgu, const uint16_t* w1, const uint16_t* w3,
+                            const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                            int32_t hidden, uint16_t* dx, moe_stream_t stream);
+/* bwd_dw13: dw1[e] = dg_e^T.x_e, dw3[e] = du_e^T.x_e (zeros for empty experts). */
+int moe_grouped_gemm_bwd_dw13(const uint16_t* dgu, const uint16_t* x, const int64_t* counts,
+                              int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                              uint16_t* dw1, uint16_t* dw3, moe_stream_t stream);
+/* bwd_dw2: dw2[e] = dy_e^T.h_e (zeros for empty experts). */
+int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, const int64_t* counts,
+                             int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                             uint16_t* dw2, moe_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -15,8 +15,9 @@ the GPU those are what define the reference's results:
     slots = keys above the k-th key by ascending index, then k-th-key ties;
   * torch.sum over a short row: pairwise tree over adjacent lanes;
   * torch.histc(int64): bincount (the reference's CPU histc rejects int64);
-  * deterministic scatter_add: fp32 sum of a token's rows in ascending position,
-    added to the destination with one rounding;
+  * deterministic scatter_add: starting from the destination row, add a token's
+    rows in ascending position, rounding to the row dtype after every add
+    (ATen's sorted index_put with accumulate);
   * x[token_idx] backward: accumulate in ascending position, rounding each add.
 Those lowering claims are pinned by GPU tests that run the same torch ops on
 the device (tests/test_gpu_oracle_pins.py); the arithmetic is pinned by closed
@@ -229,13 +230,15 @@ def index_backward(g: torch.Tensor, token_idx: torch.Tensor, n: int) -> torch.Te
 
 class _Combine(torch.autograd.Function):
     """deterministic_scatter_add(out, token_idx expanded, src) (scatter_add.py:10-48):
-    each token's rows summed in fp32 from zero in ascending position, then added to
-    out with one rounding. Backward: grad passes to out; grad_src = gather."""
+    starting from out[t], each of token t's rows is added in ascending position
+    with a rounding to out's dtype after every add. Backward: grad passes to out;
+    grad_src = gather."""
 
     @staticmethod
     def forward(ctx, out, token_idx, src):
         ctx.save_for_backward(token_idx)
-        acc = torch.zeros(out.shape, dtype=torch.float32)
+        dtype = out.dtype
+        acc = out.float().clone()
         order = torch.from_numpy(np.argsort(token_idx.cpu().numpy(), kind="stable"))
         t_sorted = token_idx[order]
         counts = torch.bincount(token_idx, minlength=out.shape[0])
@@ -244,8 +247,9 @@ class _Combine(torch.autograd.Function):
         maxk = int(counts.max().item()) if counts.numel() else 0
         for j in range(maxk):
             sel = rank == j
-            acc[t_sorted[sel]] += src[order[sel]].float()
-        return (out.float() + acc).to(out.dtype)
+            toks = t_sorted[sel]
+            acc[toks] = (acc[toks] + src[order[sel]].float()).to(dtype).float()
+        return acc.to(dtype)
 
     @staticmethod
     def backward(ctx, g):
@@ -307,12 +311,20 @@ class MoECfg:
     has_shared: bool = False
 
 
-def moe_forward(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None):
+def moe_forward(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None,
+                logits: torch.Tensor | None = None):
     """params: 'gate' [E,D], 'w1','w2','w3' experts, optional 'sw1','sw2','sw3'
-    shared expert, optional 'expert_bias' [E]. Records intermediates in `aux`."""
+    shared expert, optional 'expert_bias' [E]. Records intermediates in `aux`.
+    `logits` may carry the gate output computed elsewhere (the GPU's fp32 GEMM)
+    so that both sides route from the same bits."""
     bs, slen, dim = x.shape
     x2 = x.reshape(-1, dim)
-    logits = F.linear(x2.float(), params["gate"].float())  # fp32 gate (autocast on GPU)
+    gate_out = F.linear(x2.float(), params["gate"].float())  # fp32 gate (autocast on GPU)
+    if logits is None:
+        logits = gate_out
+    else:
+        # the given values (x - x == 0 exactly), with the gradient of the gate GEMM
+        logits = logits.to(gate_out.dtype) + (gate_out - gate_out.detach())
     top_scores, idx, counts, scores = router_forward(logits, params.get("expert_bias"), cfg.router)
     scores_sorted, token_idx, counts2, perm = reorder(top_scores, idx, cfg.router.num_experts)
     routed_input = _IndexRows.apply(x2, token_idx)
@@ -344,7 +356,9 @@ def router_forward_torch(logits: torch.Tensor, expert_bias: torch.Tensor | None,
     the gate; the GPU tests use it to pin the selection / summation rules that
     router_forward restates. (histc on int64 is GPU-only, so counts use it only
     off the CPU.)"""
-    scores = score_fn(logits.float(), cfg.score_func)
+    # the score function runs in the gate's output dtype: fp32 on the GPU
+    # (autocast), the input dtype on the CPU, as in the reference
+    scores = score_fn(logits, cfg.score_func)
     choice = scores if expert_bias is None else scores + expert_bias
     if cfg.num_expert_groups is not None:
         g, gk = cfg.num_expert_groups, cfg.num_limited_groups
@@ -370,3 +384,77 @@ def router_forward_torch(logits: torch.Tensor, expert_bias: torch.Tensor | None,
     else:
         counts = torch.histc(idx.view(-1), bins=cfg.num_experts, min=0, max=cfg.num_experts)
     return top_scores, idx, counts, scores
+
+
+# ---------------------------------------------------------------------------
+# MoE.forward as the reference's own op sequence (device-agnostic)
+# ---------------------------------------------------------------------------
+
+
+def _histc_counts(flat_idx: torch.Tensor, num_experts: int) -> torch.Tensor:
+    """moe.py:269-274 / :312-317. torch.histc rejects int64 on the CPU, so the
+    CPU run uses bincount, which is the same histogram for ids in [0, E)."""
+    if flat_idx.device.type == "cpu":
+        return torch.bincount(flat_idx, minlength=num_experts)
+    return torch.histc(flat_idx, bins=num_experts, min=0, max=num_experts)
+
+
+def _deterministic_scatter_add(out: torch.Tensor, index: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """torchtitan/ops/scatter_add.py:10-20 (forward; autograd through ATen's
+    scatter_add gives the same gather backward as :28-33)."""
+    prev = torch.are_deterministic_algorithms_enabled()
+    prev_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    torch.use_deterministic_algorithms(True, warn_only=False)
+    try:
+        return out.scatter_add(dim=0, index=index, src=src)
+    finally:
+        torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
+
+
+def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg) -> torch.Tensor:
+    """MoE.forward (moe.py:380-477) with the router (moe.py:211-274), the
+    reorderer (moe.py:291-332), _run_experts_grouped_mm (moe.py:53-70) and the
+    shared FeedForward (feed_forward.py:53-54) written as the same torch calls
+    the reference makes, so that it runs wherever torch does:
+      * the gate runs under torch.autocast(dtype=float32) as at moe.py:231-232
+        (honoured on the GPU, disabled with a warning on the CPU);
+      * torch.histc on the GPU, bincount on the CPU (_histc_counts);
+      * torch._grouped_mm in bf16, or the per-expert matmul loop when
+        cfg.use_grouped_mm is False.
+    This is the reference's CPU MoE path used as the CPU baseline, and, run on
+    the GPU, the op-for-op reference the fused kernels are compared against."""
+    rc = cfg.router
+    bs, slen, dim = x.shape
+    x2 = x.view(-1, dim)
+    gate_w = params["gate"]
+    import warnings
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        with torch.autocast(device_type=x.device.type, dtype=torch.float32):
+            logits = F.linear(x2, gate_w)
+    top_scores, idx, _counts, _scores = router_forward_torch(logits, params.get("expert_bias"), rc)
+    flat = idx.view(-1)
+    counts = _histc_counts(flat, rc.num_experts)
+    perm = torch.argsort(flat, stable=True)
+    scores_sorted = top_scores.view(-1)[perm]
+    token_idx = perm // rc.top_k
+    routed_input = x2[token_idx]
+    if cfg.score_before_experts:
+        routed_input = (routed_input.to(torch.float32) * scores_sorted.reshape(-1, 1)).to(x2.dtype)
+    w1, w2, w3 = params["w1"], params["w2"], params["w3"]
+    if cfg.use_grouped_mm:
+        offsets = torch.cumsum(counts, dim=0, dtype=torch.int32)
+        h = F.silu(torch._grouped_mm(routed_input.bfloat16(), w1.bfloat16().transpose(-2, -1), offs=offsets))
+        h = h * torch._grouped_mm(routed_input.bfloat16(), w3.bfloat16().transpose(-2, -1), offs=offsets)
+        routed_output = torch._grouped_mm(h, w2.bfloat16().transpose(-2, -1), offs=offsets).type_as(routed_input)
+    else:
+        routed_output = experts_for_loop(w1, w2, w3, routed_input, counts)
+    if cfg.has_shared:
+        out = feed_forward(x2, params["sw1"], params["sw2"], params["sw3"])
+    else:
+        out = torch.zeros_like(x2)
+    if not cfg.score_before_experts:
+        routed_output = (routed_output.to(torch.float32) * scores_sorted.reshape(-1, 1)).to(x2.dtype)
+    out = _deterministic_scatter_add(out, token_idx.reshape(-1, 1).expand(-1, dim), routed_output)
+    return out.reshape(bs, slen, dim)

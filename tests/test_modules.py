@@ -1,0 +1,131 @@
+"""Drop-in module API on the CPU: Config dataclasses, state_dict keys and shapes
+(torchtitan/models/common/moe.py:73-489, feed_forward.py:34-54), the Kimi
+mapping (kimi_linear/model.py:597-707) and the reference's Python-side errors."""
+
+import dataclasses
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from torchtitan_amd import FeedForward, GroupedExperts, Linear, MoE, TokenChoiceTopKRouter
+from torchtitan_amd.kimi import KimiMoE, init_kimi_moe_weights, kimi_moe_config
+
+
+def _cfg(d=64, e=8, h=32, hs=48, k=2, coeff=1e-3, groups=None, limited=None, score_func="sigmoid"):
+    return MoE.Config(
+        num_experts=e,
+        experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e),
+        router=TokenChoiceTopKRouter.Config(num_experts=e, gate=Linear.Config(in_features=d, out_features=e),
+                                            top_k=k, num_expert_groups=groups, num_limited_groups=limited,
+                                            score_func=score_func),
+        load_balance_coeff=coeff,
+        shared_experts=FeedForward.Config(w1=Linear.Config(in_features=d, out_features=hs),
+                                          w2=Linear.Config(in_features=hs, out_features=d),
+                                          w3=Linear.Config(in_features=d, out_features=hs)) if hs else None,
+    )
+
+
+def test_state_dict_layout():
+    with torch.device("meta"):
+        moe = _cfg().build()
+    sd = moe.state_dict()
+    shapes = {k: tuple(v.shape) for k, v in sd.items()}
+    assert shapes == {
+        "experts.w1": (8, 32, 64), "experts.w2": (8, 64, 32), "experts.w3": (8, 32, 64),
+        "router.gate.weight": (8, 64),
+        "shared_experts.w1.weight": (48, 64), "shared_experts.w2.weight": (64, 48),
+        "shared_experts.w3.weight": (48, 64),
+        "expert_bias": (8,),
+    }
+    assert sd["expert_bias"].dtype == torch.float32
+    # tokens_per_expert is a non-persistent buffer
+    assert "tokens_per_expert" in dict(moe.named_buffers()) and "tokens_per_expert" not in sd
+
+
+def test_no_bias_without_load_balancing_and_no_shared():
+    with torch.device("meta"):
+        moe = _cfg(coeff=None, hs=0).build()
+    assert moe.expert_bias is None and moe.shared_experts is None
+    assert set(moe.state_dict()) == {"experts.w1", "experts.w2", "experts.w3", "router.gate.weight"}
+
+
+def test_config_protocol():
+    cfg = _cfg()
+    with pytest.raises(TypeError):
+        GroupedExperts.Config(8, 4, 2)  # keyword-only
+    assert not hasattr(cfg, "__dict__")  # slots
+    built = cfg.build()
+    assert isinstance(built, MoE) and built.reorderer.top_k == 2
+    cfg2 = dataclasses.replace(cfg, score_before_experts=False)
+    assert cfg2.build().score_before_experts is False
+    assert cfg.to_dict()["router"]["top_k"] == 2
+
+
+def test_init_states_with_param_init():
+    init = {"w1": lambda p: torch.nn.init.constant_(p, 1.0), "w2": lambda p: torch.nn.init.zeros_(p),
+            "w3": lambda p: torch.nn.init.constant_(p, 2.0)}
+    ex = GroupedExperts.Config(dim=4, hidden_dim=3, num_experts=2, param_init=init).build()
+    ex.init_states()
+    assert torch.all(ex.w1 == 1) and torch.all(ex.w2 == 0) and torch.all(ex.w3 == 2)
+    moe = _cfg(hs=0).build()
+    moe._init_self_buffers(buffer_device=torch.device("cpu"))
+    assert torch.count_nonzero(moe.expert_bias) == 0 and torch.count_nonzero(moe.tokens_per_expert) == 0
+
+
+@pytest.mark.parametrize("e,groups,limited,msg", [
+    (8, 4, None, "num_limited_groups must be set"),
+    (10, 4, 2, "must be divisible"),
+    (8, 8, 2, "experts_per_group"),
+])
+def test_group_config_errors(e, groups, limited, msg):
+    r = TokenChoiceTopKRouter.Config(num_experts=e, gate=Linear.Config(in_features=4, out_features=e), top_k=1,
+                                     num_expert_groups=groups, num_limited_groups=limited).build()
+    with pytest.raises(ValueError, match=msg):
+        r(torch.zeros(3, 4))
+
+
+def test_unknown_score_function():
+    r = TokenChoiceTopKRouter.Config(num_experts=4, gate=Linear.Config(in_features=4, out_features=4), top_k=1,
+                                     score_func="relu").build()
+    with pytest.raises(NotImplementedError):
+        r(torch.zeros(3, 4))
+
+
+def test_feed_forward_is_swiglu():
+    ff = FeedForward.Config(w1=Linear.Config(in_features=8, out_features=6),
+                            w2=Linear.Config(in_features=6, out_features=8),
+                            w3=Linear.Config(in_features=8, out_features=6)).build()
+    x = torch.randn(5, 8)
+    ref = ff.w2.weight @ (torch.nn.functional.silu(ff.w1.weight @ x.t()) * (ff.w3.weight @ x.t()))
+    torch.testing.assert_close(ff(x), ref.t())
+
+
+KIMI_48B = SimpleNamespace(
+    hidden_size=2304, num_experts=256, num_experts_per_token=8, moe_intermediate_size=1024,
+    moe_renormalize=True, moe_router_activation_func="sigmoid", num_shared_experts=1,
+    routed_scaling_factor=2.446, num_expert_group=1, topk_group=1,
+)
+
+
+def test_kimi_mapping_and_names():
+    cfg = kimi_moe_config(KIMI_48B)
+    assert cfg.router.num_expert_groups is None and cfg.router.num_limited_groups is None
+    assert cfg.router.route_scale == 2.446 and cfg.router.route_norm and cfg.router.top_k == 8
+    assert cfg.shared_experts.w1.out_features == 1024 and cfg.score_before_experts
+    grouped = kimi_moe_config(SimpleNamespace(**{**vars(KIMI_48B), "num_expert_group": 8, "topk_group": 4}))
+    assert grouped.router.num_expert_groups == 8 and grouped.router.num_limited_groups == 4
+    with torch.device("meta"):
+        layer = KimiMoE(KIMI_48B)
+    names = set(layer.state_dict())
+    assert "_moe.experts.w1" in names and "_moe.router.gate.weight" in names and "_moe.expert_bias" in names
+    assert tuple(layer._moe.experts.w2.shape) == (256, 2304, 1024)
+
+
+def test_kimi_init():
+    small = SimpleNamespace(**{**vars(KIMI_48B), "hidden_size": 32, "num_experts": 4, "moe_intermediate_size": 16})
+    layer = KimiMoE(small)
+    layer._moe.expert_bias.fill_(3.0)
+    init_kimi_moe_weights(layer, std=0.02)
+    assert torch.count_nonzero(layer._moe.expert_bias) == 0
+    assert 0.01 < layer._moe.experts.w1.std().item() < 0.03

@@ -1,0 +1,394 @@
+"""Pins the oracle (oracle/moe_ref.py) on the CPU.
+
+What fixes each function, independently of the formula being checked:
+  * generate_permute_indices: the reference's own known-answer vectors
+    (tests/golden/ep_permute_kats.json, from tests/unit_tests/test_expert_parallel.py);
+  * radix_key, topk_gpu_order, node_limited_choice, select_experts: brute force
+    over tiny inputs and, where there are no ties, torch's CPU topk run through the
+    reference's op sequence (router_forward_torch);
+  * gpu_row_sum: exact on integer-valued floats, and the explicit trees for n=6, 8;
+  * reorder: brute-force stable sort by (expert, flat position) and the EP=1
+    identity of generate_permute_indices;
+  * _Combine / index_backward: sequential loops, ATen's CPU scatter_add (which
+    adds rows into the destination in index order, in its dtype) and the
+    autograd of x[token_idx] in fp32;
+  * experts_grouped_mm / experts_for_loop: torch._grouped_mm on the CPU (the
+    reference's third-party call) and a float64 textbook loop;
+  * router gradients: float64 finite differences;
+  * moe_forward: the reference op sequence (moe_forward_reference_ops) on the CPU.
+The GPU-lowering rules the oracle states (top-k tie order, deterministic
+scatter-add order, index-backward rounding, short-row sum order) are pinned
+against torch on the device in tests/test_gpu_oracle_pins.py.
+"""
+
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe_ref as R
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------------------
+# EP permute indices: the reference's known-answer vectors
+# ---------------------------------------------------------------------------
+
+
+def _kats():
+    with open(os.path.join(GOLDEN, "ep_permute_kats.json")) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _kats(), ids=lambda c: c["name"])
+def test_generate_permute_indices_known_answers(case):
+    idx, ntok = R.generate_permute_indices(case["tokens_per_expert_group"], case["experts_per_rank"],
+                                           case["num_ranks"])
+    total = sum(case["tokens_per_expert_group"])
+    assert idx.shape == (total,)
+    assert sorted(idx.tolist()) == list(range(total))
+    if case["expected_indices"] is not None:
+        assert idx.tolist() == case["expected_indices"]
+    if case["expected_num_tokens"] is not None:
+        assert ntok.tolist() == case["expected_num_tokens"]
+
+
+def test_permute_indices_planted_mistake_is_caught():
+    """A transposed (rank-major) output would pass the permutation check but not
+    the known answers."""
+    case = _kats()[0]
+    wrong = np.arange(sum(case["tokens_per_expert_group"]))
+    assert wrong.tolist() != case["expected_indices"]
+
+
+# ---------------------------------------------------------------------------
+# selection rules
+# ---------------------------------------------------------------------------
+
+
+def _total_order(v: float):
+    """Textbook total order of floats used by a radix select: NaN above all,
+    -0 below +0."""
+    if np.isnan(v):
+        return (2, 0.0, 0)
+    return (1, v, 0 if np.signbit(v) else 1)
+
+
+def test_radix_key_is_the_total_order():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(200).astype(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4e38, -3.4e38], dtype=np.float32),
+    ])
+    keys = R.radix_key(vals)
+    for i in range(len(vals)):
+        for j in range(0, len(vals), 7):
+            a, b = _total_order(float(vals[i])), _total_order(float(vals[j]))
+            assert (keys[i] < keys[j]) == (a < b)
+            assert (keys[i] == keys[j]) == (a == b or (np.isnan(vals[i]) and np.isnan(vals[j])))
+
+
+def _brute_topk(row, k):
+    keys = [_total_order(float(v)) for v in row]
+    order = sorted(range(len(row)), key=lambda i: (tuple(-x if isinstance(x, float) else -x for x in keys[i]), i))
+    chosen = order[:k]
+    kth = keys[chosen[-1]]
+    above = sorted(i for i in chosen if keys[i] > kth)
+    ties = sorted(i for i in chosen if keys[i] == kth)
+    return above + ties
+
+
+def test_topk_gpu_order_brute_force_with_ties():
+    rng = np.random.default_rng(1)
+    levels = np.array([-1.0, 0.0, -0.0, 0.5, 0.5, 2.0], dtype=np.float32)
+    for e in range(1, 7):
+        for k in range(1, e + 1):
+            vals = rng.choice(levels, size=(40, e)).astype(np.float32)
+            got = R.topk_gpu_order(vals, k)
+            for r in range(vals.shape[0]):
+                assert got[r].tolist() == _brute_topk(vals[r], k), (e, k, vals[r])
+
+
+def test_topk_set_matches_torch_without_ties():
+    g = torch.Generator().manual_seed(2)
+    v = torch.randn(500, 64, generator=g)
+    for k in (1, 4, 8):
+        got = R.topk_gpu_order(v.numpy(), k)
+        _, ref = torch.topk(v, k, dim=-1, sorted=False)
+        assert torch.equal(torch.sort(torch.from_numpy(got), 1).values, torch.sort(ref, 1).values)
+
+
+def _brute_node_limited(row, n_groups, n_limited):
+    e = len(row)
+    epg = e // n_groups
+    gs = []
+    for g in range(n_groups):
+        grp = sorted(row[g * epg:(g + 1) * epg], key=_total_order, reverse=True)
+        gs.append(np.float32(grp[0]) + np.float32(grp[1]))
+    keep = set(_brute_topk(np.array(gs, dtype=np.float32), n_limited))
+    return np.array([row[i] if (i // epg) in keep else -np.inf for i in range(e)], dtype=np.float32)
+
+
+def test_node_limited_choice_brute_force():
+    rng = np.random.default_rng(3)
+    for (e, g, gk) in ((8, 4, 2), (12, 3, 1), (16, 8, 4), (6, 3, 3)):
+        vals = np.round(rng.standard_normal((30, e)) * 2) / 2  # ties
+        vals = vals.astype(np.float32)
+        got = R.node_limited_choice(vals, g, gk)
+        for r in range(vals.shape[0]):
+            np.testing.assert_array_equal(got[r], _brute_node_limited(vals[r], g, gk))
+
+
+@pytest.mark.parametrize("sf,groups,norm,bias", [
+    ("sigmoid", None, True, True), ("softmax", None, False, False), ("sigmoid", (8, 4), True, True),
+    ("softmax", (4, 2), True, False),
+])
+def test_router_matches_reference_op_sequence_on_cpu(sf, groups, norm, bias):
+    """No exact ties in random fp32 logits: the reference op sequence run by torch
+    on the CPU selects the same sets; scores agree to rounding."""
+    g = torch.Generator().manual_seed(4)
+    n, e, k = 300, 64, 6
+    logits = torch.randn(n, e, generator=g)
+    b = torch.rand(e, generator=g) * 0.02 - 0.01 if bias else None
+    cfg = R.RouterCfg(num_experts=e, top_k=k, score_func=sf, route_norm=norm, route_scale=2.5,
+                      num_expert_groups=groups[0] if groups else None,
+                      num_limited_groups=groups[1] if groups else None)
+    top, idx, counts, scores = R.router_forward(logits, b, cfg)
+    t_top, t_idx, t_counts, t_scores = R.router_forward_torch(logits, b, cfg)
+    assert torch.equal(scores, t_scores)
+    si, order = torch.sort(idx, 1)
+    ti, torder = torch.sort(t_idx, 1)
+    assert torch.equal(si, ti)
+    torch.testing.assert_close(top.gather(1, order), t_top.gather(1, torder), rtol=1e-6, atol=0)
+    assert torch.equal(counts, t_counts)
+    assert int(counts.sum()) == n * k
+
+
+def test_force_load_balance_round_robin():
+    cfg = R.RouterCfg(num_experts=5, top_k=3, force_load_balance=True)
+    idx = R.select_experts(np.zeros((7, 5), np.float32), None, cfg)
+    assert idx.reshape(-1).tolist() == [i % 5 for i in range(21)]
+
+
+def test_score_fn_rejects_unknown():
+    with pytest.raises(NotImplementedError):
+        R.score_fn(torch.zeros(2, 2), "relu")
+
+
+# ---------------------------------------------------------------------------
+# short-row sum order
+# ---------------------------------------------------------------------------
+
+
+def test_gpu_row_sum_exact_on_integers_and_trees():
+    v = torch.arange(1, 65, dtype=torch.float32).reshape(1, 64)
+    for n in range(1, 65):
+        assert R.gpu_row_sum(v[:, :n]).item() == n * (n + 1) / 2
+    x = torch.randn(5, 8, dtype=torch.float32)
+    tree8 = ((x[:, 0] + x[:, 1]) + (x[:, 2] + x[:, 3])) + ((x[:, 4] + x[:, 5]) + (x[:, 6] + x[:, 7]))
+    assert torch.equal(R.gpu_row_sum(x), tree8)
+    y = x[:, :6]
+    tree6 = ((y[:, 0] + y[:, 4]) + (y[:, 1] + y[:, 5])) + (y[:, 2] + y[:, 3])
+    assert torch.equal(R.gpu_row_sum(y), tree6)
+
+
+# ---------------------------------------------------------------------------
+# reorder
+# ---------------------------------------------------------------------------
+
+
+def test_reorder_is_stable_sort_by_expert_then_position():
+    g = torch.Generator().manual_seed(5)
+    n, e, k = 200, 16, 4
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    top = torch.rand(n, k, generator=g)
+    ss, tok, counts, perm = R.reorder(top, idx, e)
+    flat = idx.reshape(-1).tolist()
+    brute = sorted(range(n * k), key=lambda p: (flat[p], p))
+    assert perm.tolist() == brute
+    assert tok.tolist() == [p // k for p in brute]
+    assert torch.equal(ss, top.reshape(-1)[torch.tensor(brute)])
+    assert counts.tolist() == [flat.count(i) for i in range(e)]
+    # token ids ascend inside each expert segment, and a token appears once per expert
+    start = 0
+    for c in counts.tolist():
+        seg = tok[start:start + c].tolist()
+        assert seg == sorted(seg) and len(set(seg)) == len(seg)
+        start += c
+
+
+def test_reorder_is_slot_order_invariant():
+    g = torch.Generator().manual_seed(6)
+    n, e, k = 100, 12, 3
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    top = torch.rand(n, k, generator=g)
+    shuffle = torch.stack([torch.randperm(k, generator=g) for _ in range(n)])
+    a = R.reorder(top, idx, e)
+    b = R.reorder(top.gather(1, shuffle), idx.gather(1, shuffle), e)
+    for x, y in zip(a[:3], b[:3]):
+        assert torch.equal(x, y)
+
+
+def test_ep1_permute_indices_are_identity():
+    idx, ntok = R.generate_permute_indices([5, 0, 3, 2], 4, 1)
+    assert idx.tolist() == list(range(10)) and ntok.tolist() == [5, 0, 3, 2]
+
+
+# ---------------------------------------------------------------------------
+# combine and index backward
+# ---------------------------------------------------------------------------
+
+
+def _seq_combine(out, token_idx, src):
+    acc = out.clone()
+    for p, t in enumerate(token_idx.tolist()):
+        acc[t] = (acc[t].float() + src[p].float()).to(out.dtype)
+    return acc
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_combine_matches_sequential_loop(dtype):
+    g = torch.Generator().manual_seed(7)
+    n, e, k, d = 64, 8, 3, 16
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    _, tok, _, _ = R.reorder(torch.rand(n, k, generator=g), idx, e)
+    out = torch.randn(n, d, generator=g).to(dtype)
+    src = torch.randn(n * k, d, generator=g).to(dtype)
+    got = R._Combine.apply(out, tok, src)
+    assert torch.equal(got, _seq_combine(out, tok, src))
+    if dtype == torch.float32:
+        # ATen's CPU scatter_add adds the source rows into the destination in
+        # index order in fp32: the same sequence of fp32 additions. (In bf16 the
+        # CPU kernel accumulates in fp32 and rounds once, unlike the GPU's sorted
+        # index_put, so only fp32 pins the order here.)
+        ref = R._deterministic_scatter_add(out, tok.reshape(-1, 1).expand(-1, d), src)
+        assert torch.equal(got, ref)
+
+
+def test_index_backward_matches_loop_with_rounding():
+    g = torch.Generator().manual_seed(8)
+    n, d = 40, 8
+    tok = torch.sort(torch.randint(0, n, (120,), generator=g)).values
+    grad = torch.randn(120, d, generator=g).bfloat16()
+    got = R.index_backward(grad, tok, n)
+    ref = torch.zeros(n, d, dtype=torch.bfloat16)
+    for p, t in enumerate(tok.tolist()):
+        ref[t] = (ref[t].float() + grad[p].float()).bfloat16()
+    assert torch.equal(got, ref)
+    # fp32: the same sums as autograd of x[token_idx]
+    x = torch.zeros(n, d, requires_grad=True)
+    x[tok].backward(grad.float())
+    torch.testing.assert_close(R.index_backward(grad.float(), tok, n), x.grad, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# experts
+# ---------------------------------------------------------------------------
+
+
+def _expert_inputs(e, d, h, counts, seed):
+    g = torch.Generator().manual_seed(seed)
+    r = sum(counts)
+    return (torch.randn(r, d, generator=g), torch.randn(e, h, d, generator=g) * 0.05,
+            torch.randn(e, d, h, generator=g) * 0.05, torch.randn(e, h, d, generator=g) * 0.05,
+            torch.tensor(counts))
+
+
+def test_experts_grouped_mm_matches_torch_grouped_mm():
+    x, w1, w2, w3, c = _expert_inputs(4, 32, 48, [5, 0, 17, 9], 9)
+    got = R.experts_grouped_mm(w1, w2, w3, x.bfloat16(), c)
+    offs = torch.cumsum(c, 0, dtype=torch.int32)
+    xb = x.bfloat16()
+    hh = F.silu(torch._grouped_mm(xb, w1.bfloat16().transpose(-2, -1), offs=offs))
+    hh = hh * torch._grouped_mm(xb, w3.bfloat16().transpose(-2, -1), offs=offs)
+    ref = torch._grouped_mm(hh, w2.bfloat16().transpose(-2, -1), offs=offs)
+    torch.testing.assert_close(got.float(), ref.float(), rtol=2e-2, atol=2e-2)
+
+
+def test_experts_for_loop_matches_float64_textbook():
+    x, w1, w2, w3, c = _expert_inputs(3, 16, 24, [4, 7, 2], 10)
+    got = R.experts_for_loop(w1, w2, w3, x, c)
+    rows = []
+    start = 0
+    for e, n in enumerate(c.tolist()):
+        for r in range(start, start + n):
+            xr = x[r].double()
+            gg = w1[e].double() @ xr
+            uu = w3[e].double() @ xr
+            hh = gg / (1 + torch.exp(-gg)) * uu
+            rows.append(w2[e].double() @ hh)
+        start += n
+    torch.testing.assert_close(got.double(), torch.stack(rows), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# router gradient
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("sf,norm", [("sigmoid", True), ("softmax", False), ("softmax", True)])
+def test_router_gradient_finite_differences(sf, norm):
+    g = torch.Generator().manual_seed(11)
+    n, e, k, scale = 6, 10, 3, 2.5
+    logits = torch.randn(n, e, generator=g, dtype=torch.float64)
+    w = torch.randn(n, k, generator=g, dtype=torch.float64)
+    cfg = R.RouterCfg(num_experts=e, top_k=k, score_func=sf, route_norm=norm, route_scale=scale)
+    _, idx, _, _ = R.router_forward(logits.float(), None, cfg)
+
+    def f(lg):
+        s = R.score_fn(lg, sf).gather(1, idx)
+        if norm:
+            s = s / (s.sum(-1, keepdim=True) + 1e-20)
+        return (s * scale * w).sum()
+
+    lg = logits.clone().requires_grad_(True)
+    f(lg).backward()
+    eps = 1e-6
+    fd = torch.zeros_like(logits)
+    for i in range(n):
+        for j in range(e):
+            p, m = logits.clone(), logits.clone()
+            p[i, j] += eps
+            m[i, j] -= eps
+            fd[i, j] = (f(p) - f(m)) / (2 * eps)
+    torch.testing.assert_close(lg.grad, fd, rtol=1e-6, atol=1e-8)
+
+
+# ---------------------------------------------------------------------------
+# whole layer vs the reference op sequence
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("score_before,grouped", [(True, False), (False, False), (True, True)])
+def test_moe_forward_matches_reference_op_sequence(score_before, grouped):
+    g = torch.Generator().manual_seed(12)
+    bs, slen, d, e, k, h, hs = 2, 24, 32, 8, 2, 48, 40
+    params = {
+        "gate": torch.randn(e, d, generator=g) * 0.1,
+        "w1": torch.randn(e, h, d, generator=g) * 0.05, "w2": torch.randn(e, d, h, generator=g) * 0.05,
+        "w3": torch.randn(e, h, d, generator=g) * 0.05,
+        "sw1": torch.randn(hs, d, generator=g) * 0.05, "sw2": torch.randn(d, hs, generator=g) * 0.05,
+        "sw3": torch.randn(hs, d, generator=g) * 0.05, "expert_bias": torch.rand(e, generator=g) * 0.02 - 0.01,
+    }
+    x = torch.randn(bs, slen, d, generator=g)
+    gout = torch.randn(bs, slen, d, generator=g)
+    rc = R.RouterCfg(num_experts=e, top_k=k, score_func="softmax", route_norm=True, route_scale=1.5)
+    cfg = R.MoECfg(router=rc, dim=d, hidden_dim=h, score_before_experts=score_before,
+                   use_grouped_mm=grouped, has_shared=True)
+    outs, grads = [], []
+    for fn in (R.moe_forward, R.moe_forward_reference_ops):
+        p = {n: t.clone().requires_grad_(n != "expert_bias") for n, t in params.items()}
+        xi = x.clone().requires_grad_(True)
+        out = fn(p, xi, cfg)
+        out.backward(gout)
+        outs.append(out.detach())
+        grads.append([xi.grad] + [p[n].grad for n in ("gate", "w1", "w2", "w3", "sw1")])
+    tol = dict(rtol=2e-2, atol=2e-2) if grouped else dict(rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(outs[0], outs[1], **tol)
+    for a, b in zip(grads[0], grads[1]):
+        torch.testing.assert_close(a, b, **tol)

@@ -36,6 +36,12 @@ SIGNATURES: dict[str, list] = {
     "moe_combine_bwd": [P, P, P, P, P, I64, I32, I32, I32, P, P, P],
     "moe_grouped_swiglu_fwd": [P, P, P, P, P, I64, I32, I32, I32, P, P, P, P, P],
     "moe_grouped_swiglu_bwd": [P, P, P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P, P, P],
+    "moe_grouped_gemm_gate_up": [P, P, P, P, I64, I32, I32, I32, P, P, P, P],
+    "moe_grouped_gemm_down": [P, P, P, I64, I32, I32, I32, P, P],
+    "moe_grouped_gemm_bwd_dgu": [P, P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_grouped_gemm_bwd_dx": [P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_grouped_gemm_bwd_dw13": [P, P, P, I64, I32, I32, I32, P, P, P],
+    "moe_grouped_gemm_bwd_dw2": [P, P, P, I64, I32, I32, I32, P, P],
 }
 _RESTYPES = {"moe_reorder_workspace_bytes": ctypes.c_int64}
 
@@ -79,6 +85,43 @@ def lib() -> ctypes.CDLL:
 def check(status: int, what: str) -> None:
     if status != 0:
         raise MoEKernelError(f"{what}: {_ERRORS.get(status, 'error')} (status {status})")
+
+
+class KernelTimer:
+    """Brackets every C-ABI launch with HIP events on the stream it is enqueued
+    on (torch's current stream), keyed by entry-point name. Events are only
+    read after the caller synchronises (``durations_ms``)."""
+
+    def __init__(self) -> None:
+        self.events: dict[str, list] = {}
+
+    def durations_ms(self) -> dict[str, list[float]]:
+        return {k: [a.elapsed_time(b) for a, b in v] for k, v in self.events.items()}
+
+
+_timer: KernelTimer | None = None
+
+
+def set_timer(timer: KernelTimer | None) -> None:
+    global _timer
+    _timer = timer
+
+
+def call(name: str, *args) -> None:
+    """Calls entry point `name` and raises on a non-zero status. When a
+    KernelTimer is installed, the launch is bracketed by events."""
+    fn = getattr(lib(), name)
+    t = _timer
+    if t is None:
+        check(fn(*args), name)
+        return
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    st = fn(*args)
+    b.record()
+    check(st, name)
+    t.events.setdefault(name, []).append((a, b))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

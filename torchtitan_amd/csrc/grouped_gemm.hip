@@ -298,8 +298,23 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // dx = dg.w1 + du.w3: the reference's autograd forms the two products as
+    // separate bf16 GEMM outputs and adds them in bf16, so the w1 half of the
+    // reduction is rounded and held (packed bf16) when the w3 half starts.
+    uint2 part[MODE == kBwdDx ? TM : 1][MODE == kBwdDx ? TN : 1];
+    const int kt_half = (MODE == kBwdDx) ? H / BK : -1;
+
     if (nk > 0) load_tile(0);
     for (int kt = 0; kt < nk; ++kt) {
+      if (MODE == kBwdDx && kt == kt_half) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            part[i][j] = make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3]));
+            acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          }
+      }
       __syncthreads();
       store_tile();
       __syncthreads();
@@ -357,8 +372,15 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int n = nt * BN + wn * WN + j * 16 + nq;
-            *(uint2*)(outp + (int64_t)r * D + n) =
-                make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3]));
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            if (MODE == kBwdDx) {
+              const uint2 pw = part[i % (MODE == kBwdDx ? TM : 1)][j % (MODE == kBwdDx ? TN : 1)];
+              v[0] = bf_lo(pw.x) + round_bf(v[0]);
+              v[1] = bf_hi(pw.x) + round_bf(v[1]);
+              v[2] = bf_lo(pw.y) + round_bf(v[2]);
+              v[3] = bf_hi(pw.y) + round_bf(v[3]);
+            }
+            *(uint2*)(outp + (int64_t)r * D + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
           }
         }
       }
@@ -464,22 +486,101 @@ static int check_gemm_shape(int64_t R, int32_t E, int32_t D, int32_t H) {
 
 using namespace moe;
 
+static int gemm_params(GemmParams& p, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                       int32_t dim, int32_t hidden) {
+  const int st = check_gemm_shape(n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (!counts) return kErrInvalidArgument;
+  p = GemmParams{};
+  p.counts = counts; p.R = n_rows; p.E = n_experts; p.D = dim; p.H = hidden;
+  return kOk;
+}
+
+MOE_API int moe_grouped_gemm_gate_up(const uint16_t* x, const uint16_t* w1, const uint16_t* w3,
+                                     const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                     int32_t dim, int32_t hidden, uint16_t* g, uint16_t* u,
+                                     uint16_t* h, hipStream_t stream) {
+  GemmParams p;
+  int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!x || !w1 || !w3 || !g || !u || !h) return kErrInvalidArgument;
+  p.x = x; p.w1 = w1; p.w3 = w3; p.out_g = g; p.out_u = u; p.out_h = h;
+  launch_mode<kFwdGateUp>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_down(const uint16_t* h, const uint16_t* w2, const int64_t* counts,
+                                  int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                                  uint16_t* y, hipStream_t stream) {
+  GemmParams p;
+  int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!h || !w2 || !y) return kErrInvalidArgument;
+  p.h = h; p.w2 = w2; p.out_y = y;
+  launch_mode<kFwdDown>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_bwd_dgu(const uint16_t* dy, const uint16_t* w2, const uint16_t* g,
+                                     const uint16_t* u, const int64_t* counts, int64_t n_rows,
+                                     int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dgu,
+                                     hipStream_t stream) {
+  GemmParams p;
+  int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!dy || !w2 || !g || !u || !dgu) return kErrInvalidArgument;
+  p.dy = dy; p.w2 = w2; p.g = g; p.u = u; p.out_dgu = dgu;
+  launch_mode<kBwdDh>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_bwd_dx(const uint16_t* dgu, const uint16_t* w1, const uint16_t* w3,
+                                    const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                    int32_t dim, int32_t hidden, uint16_t* dx, hipStream_t stream) {
+  GemmParams p;
+  int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!dgu || !w1 || !w3 || !dx) return kErrInvalidArgument;
+  p.dgu = dgu; p.w1 = w1; p.w3 = w3; p.out_dx = dx;
+  launch_mode<kBwdDx>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_bwd_dw13(const uint16_t* dgu, const uint16_t* x, const int64_t* counts,
+                                      int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                                      uint16_t* dw1, uint16_t* dw3, hipStream_t stream) {
+  GemmParams p;
+  int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (!dw1 || !dw3 || (n_rows > 0 && (!dgu || !x))) return kErrInvalidArgument;
+  p.dgu = dgu; p.x = x; p.out_dw1 = dw1; p.out_dw3 = dw3;
+  launch_mode<kBwdDw13>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, const int64_t* counts,
+                                     int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                                     uint16_t* dw2, hipStream_t stream) {
+  GemmParams p;
+  int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (!dw2 || (n_rows > 0 && (!dy || !h))) return kErrInvalidArgument;
+  p.dy = dy; p.h = h; p.out_dw2 = dw2;
+  launch_mode<kBwdDw2>(p, n_rows, stream);
+  return launch_status();
+}
+
 MOE_API int moe_grouped_swiglu_fwd(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
                                    const uint16_t* w3, const int64_t* counts, int64_t n_rows,
                                    int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* g,
                                    uint16_t* u, uint16_t* h, uint16_t* y, hipStream_t stream) {
-  int st = check_gemm_shape(n_rows, n_experts, dim, hidden);
+  int st = moe_grouped_gemm_gate_up(x, w1, w3, counts, n_rows, n_experts, dim, hidden, g, u, h, stream);
   if (st) return st;
-  if (!x || !w1 || !w2 || !w3 || !counts || !g || !u || !h || !y) return kErrInvalidArgument;
-  if (n_rows == 0) return kOk;
-  GemmParams p{};
-  p.counts = counts; p.R = n_rows; p.E = n_experts; p.D = dim; p.H = hidden;
-  p.x = x; p.w1 = w1; p.w2 = w2; p.w3 = w3;
-  p.out_g = g; p.out_u = u; p.out_h = h; p.out_y = y;
-  launch_mode<kFwdGateUp>(p, n_rows, stream);
-  p.h = h;
-  launch_mode<kFwdDown>(p, n_rows, stream);
-  return launch_status();
+  return moe_grouped_gemm_down(h, w2, counts, n_rows, n_experts, dim, hidden, y, stream);
 }
 
 MOE_API int moe_grouped_swiglu_bwd(const uint16_t* dy, const uint16_t* x, const uint16_t* w1,
@@ -488,20 +589,12 @@ MOE_API int moe_grouped_swiglu_bwd(const uint16_t* dy, const uint16_t* x, const 
                                    int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
                                    uint16_t* dgu_workspace, uint16_t* dx, uint16_t* dw1,
                                    uint16_t* dw2, uint16_t* dw3, hipStream_t stream) {
-  int st = check_gemm_shape(n_rows, n_experts, dim, hidden);
+  int st = moe_grouped_gemm_bwd_dgu(dy, w2, g, u, counts, n_rows, n_experts, dim, hidden,
+                                    dgu_workspace, stream);
   if (st) return st;
-  if (!counts || !w1 || !w2 || !w3 || !dw1 || !dw2 || !dw3) return kErrInvalidArgument;
-  if (n_rows > 0 && (!dy || !x || !g || !u || !h || !dgu_workspace || !dx)) return kErrInvalidArgument;
-  GemmParams p{};
-  p.counts = counts; p.R = n_rows; p.E = n_experts; p.D = dim; p.H = hidden;
-  p.x = x; p.w1 = w1; p.w2 = w2; p.w3 = w3; p.g = g; p.u = u; p.h = h; p.dy = dy;
-  p.out_dgu = dgu_workspace; p.dgu = dgu_workspace; p.out_dx = dx;
-  p.out_dw1 = dw1; p.out_dw2 = dw2; p.out_dw3 = dw3;
-  if (n_rows > 0) {
-    launch_mode<kBwdDh>(p, n_rows, stream);
-    launch_mode<kBwdDx>(p, n_rows, stream);
-  }
-  launch_mode<kBwdDw13>(p, n_rows, stream);
-  launch_mode<kBwdDw2>(p, n_rows, stream);
-  return launch_status();
+  st = moe_grouped_gemm_bwd_dx(dgu_workspace, w1, w3, counts, n_rows, n_experts, dim, hidden, dx, stream);
+  if (st) return st;
+  st = moe_grouped_gemm_bwd_dw13(dgu_workspace, x, counts, n_rows, n_experts, dim, hidden, dw1, dw3, stream);
+  if (st) return st;
+  return moe_grouped_gemm_bwd_dw2(dy, h, counts, n_rows, n_experts, dim, hidden, dw2, stream);
 }

@@ -11,11 +11,11 @@
 //
 // Permute (moe.py:445-451) reads each token row once and writes its K copies
 // (scaled by the routing score when score_before_experts). Combine
-// (moe.py:465-475 via torchtitan/ops/scatter_add.py:10-20) reduces each
-// token's K rows in ascending sorted position, accumulating in fp32 and
-// rounding once onto the shared-expert output, which is how the reference's
-// deterministic scatter_add lowers on the GPU (index_put with accumulate,
-// duplicates summed in sorted order). All row traffic uses 128-bit accesses.
+// (moe.py:465-475 via torchtitan/ops/scatter_add.py:10-20) adds each
+// token's K rows onto its shared-expert output row in ascending sorted
+// position, rounding to the row type after every add, which is how the
+// reference's deterministic scatter_add lowers on the GPU (a sorted index_put
+// with accumulate). All row traffic uses 128-bit accesses.
 #include "common.h"
 
 namespace moe {
@@ -215,9 +215,12 @@ __global__ __launch_bounds__(256) void expand_rows_kernel(const T* __restrict__ 
   }
 }
 
-// out[t] = round( shared[t] + sum_k r_k ), the sum in fp32 from 0 in ascending
-// sorted position; r_k = routed[pos_k], or round(routed[pos_k] * score) when
-// the score is applied after the experts (moe.py:465-469).
+// out[t] = ( ... ((shared[t] + r_0) + r_1) ... + r_{K-1} ), rounding to the row
+// type after every add, the rows taken in ascending sorted position (the order
+// and rounding of the reference's deterministic scatter_add on the GPU, a
+// sorted index_put with accumulate); r_k = routed[pos_k], or
+// round(routed[pos_k] * score) when the score is applied after the experts
+// (moe.py:465-469). Without a shared expert the sum starts from zero.
 template <typename T>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shared_out,
                                                       const T* __restrict__ routed,
@@ -233,8 +236,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shar
     const int64_t t = c / cpr;
     const int ch = (int)(c - t * cpr);
     float a[n];
+    if (shared_out) {
+      Chunk<T>::unpack(*(const uint4*)(shared_out + t * D + ch * n), a);
+    } else {
 #pragma unroll
-    for (int i = 0; i < n; ++i) a[i] = 0.f;
+      for (int i = 0; i < n; ++i) a[i] = 0.f;
+    }
     for (int k = 0; k < K; ++k) {
       const int64_t pos = tok_pos[t * K + k];
       uint4 v = *(const uint4*)(routed + pos * D + ch * n);
@@ -242,18 +249,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shar
       float f[n];
       Chunk<T>::unpack(v, f);
 #pragma unroll
-      for (int i = 0; i < n; ++i) a[i] += f[i];
+      for (int i = 0; i < n; ++i) a[i] = Chunk<T>::round(a[i] + f[i]);
     }
-    float b[n];
-    if (shared_out) {
-      Chunk<T>::unpack(*(const uint4*)(shared_out + t * D + ch * n), b);
-    } else {
-#pragma unroll
-      for (int i = 0; i < n; ++i) b[i] = 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < n; ++i) b[i] = b[i] + a[i];
-    *(uint4*)(out + t * D + ch * n) = Chunk<T>::pack(b);
+    *(uint4*)(out + t * D + ch * n) = Chunk<T>::pack(a);
   }
 }
 

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from ._lib import check, lib, ptr, require_gpu, stream_of
+from ._lib import call, lib, ptr, require_gpu, stream_of
 
 SCORE_FUNCS = {"softmax": 0, "sigmoid": 1}
 DTYPE_CODES = {torch.bfloat16: 0, torch.float32: 1}
@@ -66,18 +66,14 @@ def router(
     idx = torch.empty(n, top_k, dtype=torch.int64, device=dev)
     counts = torch.empty(num_experts, dtype=torch.int64, device=dev)
     s = stream_of(logits)
-    check(
-        lib().moe_router_fwd(
-            ptr(logits), ptr(bias), n, num_experts, top_k, score_func, num_expert_groups,
+    call(
+        "moe_router_fwd", ptr(logits), ptr(bias), n, num_experts, top_k, score_func, num_expert_groups,
             num_limited_groups, int(route_norm), route_scale, int(force_load_balance),
             ptr(scores), ptr(top_scores), ptr(idx), s,
-        ),
-        "moe_router_fwd",
     )
     ws = _workspace(n, num_experts, dev)
-    check(
-        lib().moe_histogram(ptr(idx), n, top_k, num_experts, ptr(ws), ws.numel(), ptr(counts), None, s),
-        "moe_histogram",
+    call(
+        "moe_histogram", ptr(idx), n, top_k, num_experts, ptr(ws), ws.numel(), ptr(counts), None, s
     )
     return top_scores, idx, counts, scores
 
@@ -104,10 +100,9 @@ def router_backward(
     n, e = scores.shape
     k = selected_experts.shape[1]
     out = torch.empty_like(scores)
-    check(
-        lib().moe_router_bwd(ptr(g), ptr(scores), ptr(selected_experts), n, e, k, score_func,
-                             int(route_norm), route_scale, ptr(out), stream_of(scores)),
-        "moe_router_bwd",
+    call(
+        "moe_router_bwd", ptr(g), ptr(scores), ptr(selected_experts), n, e, k, score_func,
+                             int(route_norm), route_scale, ptr(out), stream_of(scores)
     )
     return out
 
@@ -159,11 +154,10 @@ def reorder(
     slot_pos = torch.empty(n, k, dtype=torch.int32, device=dev)
     tok_pos = torch.empty(n, k, dtype=torch.int32, device=dev)
     ws = _workspace(n, num_experts, dev)
-    check(
-        lib().moe_reorder(ptr(idx), ptr(ts), n, k, num_experts, ptr(ws), ws.numel(),
+    call(
+        "moe_reorder", ptr(idx), ptr(ts), n, k, num_experts, ptr(ws), ws.numel(),
                           ptr(scores_sorted), ptr(token_idx), ptr(counts), ptr(offsets),
-                          ptr(slot_pos), ptr(tok_pos), stream_of(idx)),
-        "moe_reorder",
+                          ptr(slot_pos), ptr(tok_pos), stream_of(idx)
     )
     return scores_sorted, token_idx, counts, offsets, slot_pos, tok_pos
 
@@ -188,7 +182,9 @@ def reorder_backward(grad_scores_sorted: Tensor, slot_pos: Tensor) -> Tensor:
     g = grad_scores_sorted.float().contiguous()
     n, k = slot_pos.shape
     out = torch.empty(n, k, dtype=torch.float32, device=g.device)
-    check(lib().moe_reorder_bwd(ptr(g), ptr(slot_pos), n, k, ptr(out), stream_of(g)), "moe_reorder_bwd")
+    call(
+        "moe_reorder_bwd", ptr(g), ptr(slot_pos), n, k, ptr(out), stream_of(g)
+    )
     return out
 
 
@@ -225,9 +221,8 @@ def permute(x: Tensor, slot_pos: Tensor, tok_pos: Tensor, scores_sorted: Tensor 
     k = slot_pos.shape[1]
     out = x.new_empty(n * k, d)
     sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
-    check(
-        lib().moe_permute(ptr(x), ptr(slot_pos), ptr(sc), n, d, k, _dtype_code(x), ptr(out), stream_of(x)),
-        "moe_permute",
+    call(
+        "moe_permute", ptr(x), ptr(slot_pos), ptr(sc), n, d, k, _dtype_code(x), ptr(out), stream_of(x)
     )
     return out
 
@@ -248,11 +243,10 @@ def permute_backward(
     grad_x = x.new_empty(n, d)
     grad_s = torch.empty(n * k if scores_sorted is not None else 0, dtype=torch.float32, device=x.device)
     sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
-    check(
-        lib().moe_permute_bwd(ptr(g), ptr(x), ptr(tok_pos), ptr(sc), n, d, k, _dtype_code(x),
+    call(
+        "moe_permute_bwd", ptr(g), ptr(x), ptr(tok_pos), ptr(sc), n, d, k, _dtype_code(x),
                               int(round_each), ptr(grad_x), ptr(grad_s) if sc is not None else None,
-                              stream_of(x)),
-        "moe_permute_bwd",
+                              stream_of(x)
     )
     return grad_x, grad_s
 
@@ -301,11 +295,10 @@ def grouped_swiglu(
     u = x.new_empty(r, h_dim)
     h = x.new_empty(r, h_dim)
     y = x.new_empty(r, d)
-    check(
-        lib().moe_grouped_swiglu_fwd(ptr(x), ptr(w1), ptr(w2), ptr(w3), ptr(counts), r, e, d, h_dim,
-                                     ptr(g), ptr(u), ptr(h), ptr(y), stream_of(x)),
-        "moe_grouped_swiglu_fwd",
-    )
+    s = stream_of(x)
+    call("moe_grouped_gemm_gate_up", ptr(x), ptr(w1), ptr(w3), ptr(counts), r, e, d, h_dim,
+         ptr(g), ptr(u), ptr(h), s)
+    call("moe_grouped_gemm_down", ptr(h), ptr(w2), ptr(counts), r, e, d, h_dim, ptr(y), s)
     return y, g, u, h
 
 
@@ -331,12 +324,13 @@ def grouped_swiglu_backward(
     dw1 = torch.empty_like(w1)
     dw2 = torch.empty_like(w2)
     dw3 = torch.empty_like(w3)
-    check(
-        lib().moe_grouped_swiglu_bwd(ptr(dy), ptr(x), ptr(w1), ptr(w2), ptr(w3), ptr(counts), ptr(g),
-                                     ptr(u), ptr(h), r, e, d, h_dim, ptr(dgu), ptr(dx), ptr(dw1),
-                                     ptr(dw2), ptr(dw3), stream_of(x)),
-        "moe_grouped_swiglu_bwd",
-    )
+    s = stream_of(x)
+    call("moe_grouped_gemm_bwd_dgu", ptr(dy), ptr(w2), ptr(g), ptr(u), ptr(counts), r, e, d, h_dim,
+         ptr(dgu), s)
+    call("moe_grouped_gemm_bwd_dx", ptr(dgu), ptr(w1), ptr(w3), ptr(counts), r, e, d, h_dim, ptr(dx), s)
+    call("moe_grouped_gemm_bwd_dw13", ptr(dgu), ptr(x), ptr(counts), r, e, d, h_dim, ptr(dw1),
+         ptr(dw3), s)
+    call("moe_grouped_gemm_bwd_dw2", ptr(dy), ptr(h), ptr(counts), r, e, d, h_dim, ptr(dw2), s)
     return dx, dw1, dw2, dw3
 
 
@@ -378,10 +372,9 @@ def combine(
     base = shared_out.to(routed.dtype).contiguous() if shared_out is not None else None
     out = routed.new_empty(n, d)
     sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
-    check(
-        lib().moe_combine(ptr(base), ptr(routed), ptr(tok_pos), ptr(sc), n, d, k, _dtype_code(routed),
-                          ptr(out), stream_of(routed)),
-        "moe_combine",
+    call(
+        "moe_combine", ptr(base), ptr(routed), ptr(tok_pos), ptr(sc), n, d, k, _dtype_code(routed),
+                          ptr(out), stream_of(routed)
     )
     return out
 
@@ -403,11 +396,10 @@ def combine_backward(
     grad_routed = g.new_empty(n * k, d)
     grad_s = torch.empty(n * k if scores_sorted is not None else 0, dtype=torch.float32, device=g.device)
     sc = scores_sorted.float().contiguous() if scores_sorted is not None else None
-    check(
-        lib().moe_combine_bwd(ptr(g), ptr(routed_output), ptr(slot_pos), ptr(tok_pos), ptr(sc), n, d, k,
+    call(
+        "moe_combine_bwd", ptr(g), ptr(routed_output), ptr(slot_pos), ptr(tok_pos), ptr(sc), n, d, k,
                               _dtype_code(g), ptr(grad_routed), ptr(grad_s) if sc is not None else None,
-                              stream_of(g)),
-        "moe_combine_bwd",
+                              stream_of(g)
     )
     return grad_routed, grad_s
 
