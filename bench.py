@@ -135,10 +135,11 @@ def make_layer(w: dict, device: torch.device, seed: int):
             p.data = torch.empty(p.shape, dtype=torch.bfloat16, device=device).normal_(0.0, w["std"], generator=gen)
         bias = (torch.rand(e, generator=gen, device=device) * 2 - 1) * w["bias"]
         if w["zipf"]:
-            # Zipf(s) per-expert boost on a random expert order: a few experts take
-            # most tokens and a tail of experts gets none.
+            # Zipf(s)-shaped per-expert boost over a random expert order, plus a
+            # tail of 20 experts pushed below every score: the top expert gets
+            # ~10x the mean load and those 20 experts get no tokens.
             ranks = torch.randperm(e, generator=gen, device=device).float() + 1.0
-            bias = bias + 0.35 * ranks.pow(-w["zipf"]) * e ** 0.0 - 0.35 * (ranks > e * 0.9).float()
+            bias = bias + 0.25 * ranks.pow(-w["zipf"]) - 1.0 * (ranks > e - 20).float()
         moe.expert_bias.copy_(bias)
         moe.tokens_per_expert.zero_()
     return moe
@@ -183,6 +184,7 @@ def cpu_baseline(moe, w: dict, x: torch.Tensor, g: torch.Tensor, n_tokens: int) 
         times.append(time.perf_counter() - t0)
         print(f"[bench] cpu baseline iteration {it}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
     t = statistics.median(times[1:])
+    print(f"[bench] cpu baseline: {n_tokens} tokens, {threads} threads, {t:.2f} s/iter", file=sys.stderr, flush=True)
     return {
         "value": n_tokens * w["top_k"] / t,
         "unit": "routed tokens/s",
@@ -202,7 +204,8 @@ def main() -> int:
     ap.add_argument("--workload", default="kimi", choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    ap.add_argument("--cpu-tokens", type=int, default=None,
+                    help="tokens in the CPU baseline sample (default: 8192, or 1024 for dsv3)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE layer runs with all experts resident on a single "
@@ -288,8 +291,8 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        print(f"[bench] cpu baseline on {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(moe, w, x, g, min(args.cpu_tokens, n))
+        cpu_tokens = args.cpu_tokens or (1024 if args.workload == "dsv3" else 8192)
+        cpu = cpu_baseline(moe, w, x, g, min(cpu_tokens, n))
 
     line = {
         "metric": "MoE layer fwd+bwd routed tokens/s; grouped-GEMM TFLOPS as % of MFMA peak",

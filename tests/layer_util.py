@@ -1,0 +1,114 @@
+"""Helpers shared by the GPU layer tests: build the drop-in MoE at a given shape
+with device-generated parameters, run it and the reference op sequence
+(oracle.moe_forward_reference_ops) on the same GPU, and compare."""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from oracle import moe_ref as R
+
+
+@dataclass
+class LayerShape:
+    bs: int
+    slen: int
+    dim: int
+    experts: int
+    top_k: int
+    hidden: int
+    shared_hidden: int
+    score_func: str = "sigmoid"
+    groups: tuple[int, int] | None = None
+    route_norm: bool = True
+    route_scale: float = 2.5
+    score_before: bool = True
+    std: float = 0.02
+    bias: float = 0.01
+    zipf: float | None = None
+
+
+def build_layer(sh: LayerShape, dev: torch.device, seed: int):
+    from torchtitan_amd import FeedForward, GroupedExperts, Linear, MoE, TokenChoiceTopKRouter
+
+    d, e, h, hs = sh.dim, sh.experts, sh.hidden, sh.shared_hidden
+    cfg = MoE.Config(
+        num_experts=e,
+        experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e),
+        router=TokenChoiceTopKRouter.Config(
+            num_experts=e, gate=Linear.Config(in_features=d, out_features=e), top_k=sh.top_k,
+            score_func=sh.score_func, route_norm=sh.route_norm, route_scale=sh.route_scale,
+            num_expert_groups=sh.groups[0] if sh.groups else None,
+            num_limited_groups=sh.groups[1] if sh.groups else None),
+        score_before_experts=sh.score_before,
+        shared_experts=FeedForward.Config(
+            w1=Linear.Config(in_features=d, out_features=hs), w2=Linear.Config(in_features=hs, out_features=d),
+            w3=Linear.Config(in_features=d, out_features=hs)) if hs else None,
+    )
+    with torch.device("meta"):
+        moe = cfg.build()
+    moe = moe.to_empty(device=dev)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    with torch.no_grad():
+        for p in moe.parameters():
+            p.data = torch.empty(p.shape, dtype=torch.bfloat16, device=dev).normal_(0.0, sh.std, generator=gen)
+        bias = (torch.rand(e, generator=gen, device=dev) * 2 - 1) * sh.bias
+        if sh.zipf:
+            ranks = torch.randperm(e, generator=gen, device=dev).float() + 1.0
+            bias = bias + 0.25 * ranks.pow(-sh.zipf) - 1.0 * (ranks > e - 20).float()
+        moe.expert_bias.copy_(bias)
+        moe.tokens_per_expert.zero_()
+    x = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
+    g = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
+    return moe, x, g
+
+
+def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.detach().float(), b.detach().float()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape) -> dict:
+    """Runs both sides forward + backward and returns {name: (rel_err, bit_identical)};
+    asserts that routing (indices, counts, top scores) is bit-exact."""
+    d = sh.dim
+    xa = x.clone().requires_grad_(True)
+    out = moe(xa)
+    out.backward(g)
+
+    sd = moe.state_dict()
+    names = {"gate": "router.gate.weight", "w1": "experts.w1", "w2": "experts.w2", "w3": "experts.w3",
+             "expert_bias": "expert_bias"}
+    if sh.shared_hidden:
+        names.update(sw1="shared_experts.w1.weight", sw2="shared_experts.w2.weight",
+                     sw3="shared_experts.w3.weight")
+    params = {k: sd[v].detach().clone().requires_grad_(k != "expert_bias") for k, v in names.items()}
+    rc = R.RouterCfg(num_experts=sh.experts, top_k=sh.top_k, score_func=sh.score_func,
+                     route_norm=sh.route_norm, route_scale=sh.route_scale,
+                     num_expert_groups=sh.groups[0] if sh.groups else None,
+                     num_limited_groups=sh.groups[1] if sh.groups else None)
+    mc = R.MoECfg(router=rc, dim=d, hidden_dim=sh.hidden, score_before_experts=sh.score_before,
+                  use_grouped_mm=True, has_shared=bool(sh.shared_hidden))
+    xb = x.clone().requires_grad_(True)
+    ref = R.moe_forward_reference_ops(params, xb, mc)
+    ref.backward(g)
+
+    x2 = x.view(-1, d)
+    with torch.no_grad():
+        top, idx, counts = moe.router(x2, moe.expert_bias)
+        with torch.autocast(device_type="cuda", dtype=torch.float32):
+            logits = torch.nn.functional.linear(x2, params["gate"].detach())
+        t_top, t_idx, t_counts, _ = R.router_forward_torch(logits, params["expert_bias"], rc)
+    assert torch.equal(idx, t_idx), "selected experts differ from the reference op sequence"
+    assert torch.equal(counts, t_counts), "tokens per expert differ"
+    assert torch.equal(top, t_top), "top scores differ"
+    pairs = {"out": (out, ref), "grad_x": (xa.grad, xb.grad),
+             "grad_gate": (moe.router.gate.weight.grad, params["gate"].grad),
+             "grad_w1": (moe.experts.w1.grad, params["w1"].grad),
+             "grad_w2": (moe.experts.w2.grad, params["w2"].grad),
+             "grad_w3": (moe.experts.w3.grad, params["w3"].grad)}
+    res = {k: (rel_err(a, b), bool(torch.equal(a, b))) for k, (a, b) in pairs.items()}
+    res["_counts"] = counts.cpu()
+    return res

@@ -1,0 +1,51 @@
+"""The drop-in layer at the benchmark shapes, against the reference op sequence
+run by torch on the same GPU (oracle.moe_forward_reference_ops):
+
+  kimi   Kimi-Linear-48B-A3B shape: 16384 tokens, dim 2304, 256 experts top-8
+         sigmoid + bias, route norm, scale 2.5, hidden 1024 + shared 1024;
+  zipf   the same with 32768 tokens and a Zipf(1.2)-shaped expert bias plus 20
+         experts that never win (heavily skewed and empty groups);
+  dsv3   DeepSeek-V3-style: 8192 tokens, dim 7168, 256 experts in 8 groups,
+         top-4 groups then top-8, hidden 2048 + shared 2048, scores applied
+         after the experts.
+
+Routing (indices, counts, top scores) must be bit-exact; the output and all
+gradients within 1e-2 normwise relative error (max |ours - ref| / max |ref|).
+"""
+
+import pytest
+import torch
+
+from tests.conftest import banner
+from tests.layer_util import LayerShape, build_layer, compare_with_reference
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {
+    "kimi": LayerShape(bs=4, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024),
+    "zipf": LayerShape(bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+                       zipf=1.2),
+    "dsv3": LayerShape(bs=1, slen=8192, dim=7168, experts=256, top_k=8, hidden=2048, shared_hidden=2048,
+                       groups=(8, 4), score_before=False, std=0.006),
+}
+
+TOL = 1e-2
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_layer_at_benchmark_shape(dev, name):
+    sh = SHAPES[name]
+    banner(f"full-size layer {name}")
+    moe, x, g = build_layer(sh, dev, seed=7)
+    res = compare_with_reference(moe, x, g, sh)
+    counts = res.pop("_counts")
+    print(f"[case] {name}: max load {int(counts.max())}, mean {counts.float().mean().item():.0f}, "
+          f"empty experts {int((counts == 0).sum())}", flush=True)
+    print(f"[case] {name}: " + ", ".join(f"{k} {v[0]:.2e}{' (bit-identical)' if v[1] else ''}"
+                                          for k, v in res.items()), flush=True)
+    if name == "zipf":
+        assert int((counts == 0).sum()) >= 20 and counts.max() > 5 * counts.float().mean()
+    bad = {k: v[0] for k, v in res.items() if not v[0] <= TOL}
+    assert not bad, bad
+    del moe, x, g
+    torch.cuda.empty_cache()

@@ -54,6 +54,10 @@ __global__ __launch_bounds__(256) void hist_kernel(const int64_t* __restrict__ i
 
 // Single block of 256 threads; thread t owns experts 4t..4t+3.
 // block_hist[b][e] -> block_base[b][e] = start[e] + sum_{b'<b} hist[b'][e]
+// The per-block counts are read in batches of kScanBatch independent loads so
+// their latencies overlap instead of adding up block after block.
+constexpr int kScanBatch = 16;
+
 __global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ block_hist, int n_blocks,
                                                    int E, int32_t* __restrict__ block_base,
                                                    int64_t* __restrict__ counts,
@@ -65,10 +69,16 @@ __global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ b
     const int e = threadIdx.x * 4 + i;
     int run = 0;
     if (e < E) {
-      for (int b = 0; b < n_blocks; ++b) {
-        const int v = block_hist[(int64_t)b * E + e];
-        if (block_base) block_base[(int64_t)b * E + e] = run;
-        run += v;
+      for (int b0 = 0; b0 < n_blocks; b0 += kScanBatch) {
+        int v[kScanBatch];
+#pragma unroll
+        for (int j = 0; j < kScanBatch; ++j)
+          v[j] = (b0 + j < n_blocks) ? block_hist[(int64_t)(b0 + j) * E + e] : 0;
+#pragma unroll
+        for (int j = 0; j < kScanBatch; ++j) {
+          if (block_base && b0 + j < n_blocks) block_base[(int64_t)(b0 + j) * E + e] = run;
+          run += v[j];
+        }
       }
     }
     tot[i] = run;
@@ -80,9 +90,19 @@ __global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ b
     if (e < E) {
       if (counts) counts[e] = tot[i];
       if (offsets) offsets[e] = start[i] + tot[i];
-      if (block_base)
-        for (int b = 0; b < n_blocks; ++b) block_base[(int64_t)b * E + e] += start[i];
     }
+  }
+  if (block_base) {
+    // add the expert starts to every block's base (coalesced over experts)
+    __shared__ int s_start[kMaxExperts];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = threadIdx.x * 4 + i;
+      if (e < E) s_start[e] = start[i];
+    }
+    __syncthreads();
+    const int64_t total = (int64_t)n_blocks * E;
+    for (int64_t i = threadIdx.x; i < total; i += blockDim.x) block_base[i] += s_start[i % E];
   }
 }
 
