@@ -34,6 +34,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 
 WORKLOADS = {
@@ -56,16 +57,16 @@ WORKLOADS = {
         score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
         score_before=True, std=0.02, bias=0.01, zipf=1.2,
     ),
+    "kimi_fp8": dict(
+        desc="Kimi-shape MoE layer with fp8 e4m3 grouped GEMMs",
+        bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+        score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.01, zipf=None, fp8=True,
+    ),
 }
 
-GEMM_ENTRIES = (
-    "moe_grouped_gemm_gate_up",
-    "moe_grouped_gemm_down",
-    "moe_grouped_gemm_bwd_dgu",
-    "moe_grouped_gemm_bwd_dx",
-    "moe_grouped_gemm_bwd_dw13",
-    "moe_grouped_gemm_bwd_dw2",
-)
+GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm")
+                     for m in ("gate_up", "down", "bwd_dgu", "bwd_dx", "bwd_dw13", "bwd_dw2"))
 
 
 def kernel_work(name: str, w: dict) -> tuple[str, float]:
@@ -76,16 +77,10 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
     d, e, k, h = w["dim"], w["experts"], w["top_k"], w["hidden"]
     r = n * k
     b = 2  # bf16 rows
-    flops = {
-        "moe_grouped_gemm_gate_up": 4 * r * d * h,
-        "moe_grouped_gemm_down": 2 * r * d * h,
-        "moe_grouped_gemm_bwd_dgu": 2 * r * d * h,
-        "moe_grouped_gemm_bwd_dx": 4 * r * d * h,
-        "moe_grouped_gemm_bwd_dw13": 4 * r * d * h,
-        "moe_grouped_gemm_bwd_dw2": 2 * r * d * h,
-    }
-    if name in flops:
-        return "mfma", float(flops[name])
+    flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw2": 2}
+    for kind in ("moe_grouped_gemm_", "moe_fp8_gemm_"):
+        if name.startswith(kind) and name[len(kind):] in flops:
+            return "mfma", float(flops[name[len(kind):]] * r * d * h)
     nbytes = {
         # logits [N,E] f32 read; scores [N,E] f32, top scores f32 and ids i64 [N,K] written
         "moe_router_fwd": 4 * n * e + 4 * n * e + 12 * n * k,
@@ -103,7 +98,8 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
         "moe_reorder_bwd": 4 * r + 4 * n * k + 4 * n * k,
         "moe_router_bwd": 4 * n * k + 8 * n * k + 4 * n * e + 4 * n * e,
     }
-    return "hbm", float(nbytes.get(name, 0))
+    # fp8 quantizers run on tensors of several sizes per step: time only
+    return "hbm", (float(nbytes[name]) if name in nbytes else None)
 
 
 def make_layer(w: dict, device: torch.device, seed: int):
@@ -142,6 +138,10 @@ def make_layer(w: dict, device: torch.device, seed: int):
             bias = bias + 0.25 * ranks.pow(-w["zipf"]) - 1.0 * (ranks > e - 20).float()
         moe.expert_bias.copy_(bias)
         moe.tokens_per_expert.zero_()
+    if w.get("fp8"):
+        from torchtitan_amd.quantization import Float8GroupedMMConverter
+
+        Float8GroupedMMConverter.Config(fqns=["experts"]).build().convert(moe)
     return moe
 
 
@@ -264,23 +264,29 @@ def main() -> int:
         avg = sum(ds) / len(ds)
         bound, work = kernel_work(name, w)
         if bound == "mfma":
-            achieved, peak, unit = work / (avg * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
-        else:
+            peak = PEAK_FP8_TFLOPS if name.startswith("moe_fp8_") else PEAK_BF16_TFLOPS
+            achieved, unit = work / (avg * 1e-3) / 1e12, "TFLOP/s"
+        elif work is not None:
             achieved, peak, unit = work / (avg * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+        else:
+            achieved, peak, unit = None, None, "GB/s"
         kernels[name] = {
             "launches_per_step": per_step, "avg_ms": round(avg, 4), "bound": bound,
-            "achieved": round(achieved, 1), "unit": unit, "frac": round(achieved / peak, 4),
+            "achieved": round(achieved, 1) if achieved is not None else None, "unit": unit,
+            "frac": round(achieved / peak, 4) if achieved is not None else None,
         }
     gemm_ms = sum(kernels[nm]["avg_ms"] * kernels[nm]["launches_per_step"] for nm in GEMM_ENTRIES if nm in kernels)
     gemm_flops = 18.0 * n * k * w["dim"] * w["hidden"]
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
     dom = max(kernels, key=lambda nm: kernels[nm]["avg_ms"] * kernels[nm]["launches_per_step"])
     dk = kernels[dom]
+    gemm_peak = PEAK_FP8_TFLOPS if w.get("fp8") else PEAK_BF16_TFLOPS
     roofline = {
         "kernel": dom,
         "bound": dk["bound"],
         "achieved": dk["achieved"],
-        "peak": PEAK_BF16_TFLOPS if dk["bound"] == "mfma" else PEAK_HBM_GBS,
+        "peak": (PEAK_FP8_TFLOPS if dom.startswith("moe_fp8_") else PEAK_BF16_TFLOPS) if dk["bound"] == "mfma"
+        else PEAK_HBM_GBS,
         "unit": dk["unit"],
         "frac": dk["frac"],
         "traffic": None,
@@ -305,7 +311,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8 e4m3 (grouped GEMMs), bf16 elsewhere" if w.get("fp8") else "bf16",
         "data": "synthetic (random-init weights, x ~ N(0,1), g ~ N(0,1))",
         "config": {
             "workload": f"{w['desc']}: N={n} tokens (bs {w['bs']} x seq {w['slen']}), dim {w['dim']}, "
@@ -320,7 +326,7 @@ def main() -> int:
         "grouped_gemm": {
             "ms_per_step": round(gemm_ms, 4),
             "tflops": round(gemm_tflops, 1),
-            "frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+            "frac_of_peak": round(gemm_tflops / gemm_peak, 4),
         },
         "permute_combine": {
             "ms_per_step": round(mover_ms, 4),

@@ -178,6 +178,70 @@ int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, const int64_
                              int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
                              uint16_t* dw2, moe_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * fp8 e4m3 (OCP e4m3fn) grouped SwiGLU experts. The reference's fp8 path is
+ * torchao's Float8TrainingOpConfig on the experts
+ * (torchtitan/components/quantization/float8.py:260-288): dynamic rowwise
+ * scales, fp32 accumulation, bf16 outputs, token groups padded to 16
+ * (quantization/__init__.py:37-40). Quantization: s = max(amax, 1e-12) / 448,
+ * q = e4m3fn(x / s) rounded to nearest even. fp8 tensors are uint8_t*.
+ * ------------------------------------------------------------------------- */
+
+/* Rows of the token-transposed fp8 tensors: n_rows + n_experts * 15 (every
+ * group starts at a multiple of 16); round it up to a multiple of 16. */
+int64_t moe_fp8_padded_rows(int64_t n_rows, int32_t n_experts);
+
+/* x [rows, cols] bf16 -> q [rows, cols] fp8, scale [rows] (one per row). */
+int moe_fp8_quant_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q, float* scale,
+                       moe_stream_t stream);
+
+/* x [E, a, b] bf16 -> per expert e and column j: scale[e*scale_expert_stride + j]
+ * = amax over a / 448, and the quantized column written as a row of a values
+ * at q + e*q_expert_stride + j*q_row_stride (a transposed copy). */
+int moe_fp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
+                         int64_t q_expert_stride, int64_t q_row_stride, float* scale,
+                         int64_t scale_expert_stride, moe_stream_t stream);
+
+/* x [n_rows, cols] bf16 in expert token groups (counts) -> q [cols, padded_rows]
+ * fp8 with group e at the 16-aligned offset sum_{e'<e} ceil16(count_e') and
+ * zero padding up to ceil16(count_e); scale [E, cols] over the group's tokens
+ * (not written for empty groups). */
+int moe_fp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                           int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
+                           moe_stream_t stream);
+
+/* fp8 forward of _run_experts_grouped_mm (moe.py:62-67): g = (qx.qw1^T)*sx*sw1,
+ * u likewise with w3, h = bf16(bf16(silu(g)) * u). sw1, sw3 [E, H]. */
+int moe_fp8_gemm_gate_up(const uint8_t* qx, const float* sx, const uint8_t* qw1, const float* sw1,
+                         const uint8_t* qw3, const float* sw3, const int64_t* counts, int64_t n_rows,
+                         int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* g, uint16_t* u,
+                         uint16_t* h, moe_stream_t stream);
+/* fp8 y = (qh.qw2^T)*sh*sw2 (moe.py:68); sw2 [E, D]. */
+int moe_fp8_gemm_down(const uint8_t* qh, const float* sh, const uint8_t* qw2, const float* sw2,
+                      const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                      uint16_t* y, moe_stream_t stream);
+/* fp8 dh = (qdy.qw2t^T)*sdy*sw2t with qw2t [E, H, D] (w2 quantized along D),
+ * then the SwiGLU backward -> dgu [R, 2H] bf16. */
+int moe_fp8_gemm_bwd_dgu(const uint8_t* qdy, const float* sdy, const uint8_t* qw2t, const float* sw2t,
+                         const uint16_t* g, const uint16_t* u, const int64_t* counts, int64_t n_rows,
+                         int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dgu, moe_stream_t stream);
+/* fp8 dx = bf16(dg.w1 scaled) + bf16(du.w3 scaled): qdgu [R, 2H] with sdgu [R, 2]
+ * (one scale per half), qw13t [E, D, 2H] with sw13t [E, 2, D]. */
+int moe_fp8_gemm_bwd_dx(const uint8_t* qdgu, const float* sdgu, const uint8_t* qw13t, const float* sw13t,
+                        const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                        uint16_t* dx, moe_stream_t stream);
+/* fp8 dw1[e], dw3[e] = dgu_e^T . x_e from the token-transposed fp8 tensors
+ * qdgut [2H, padded_rows] (sdgut [E, 2H]) and qxt [D, padded_rows] (sxt [E, D]);
+ * experts without tokens get zeros. */
+int moe_fp8_gemm_bwd_dw13(const uint8_t* qdgut, const float* sdgut, const uint8_t* qxt, const float* sxt,
+                          const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                          int32_t dim, int32_t hidden, uint16_t* dw1, uint16_t* dw3, moe_stream_t stream);
+/* fp8 dw2[e] = dy_e^T . h_e from qdyt [D, padded_rows] (sdyt [E, D]) and
+ * qht [H, padded_rows] (sht [E, H]). */
+int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const uint8_t* qht, const float* sht,
+                         const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                         int32_t dim, int32_t hidden, uint16_t* dw2, moe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -458,3 +458,104 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg) -> tor
         routed_output = (routed_output.to(torch.float32) * scores_sorted.reshape(-1, 1)).to(x2.dtype)
     out = _deterministic_scatter_add(out, token_idx.reshape(-1, 1).expand(-1, dim), routed_output)
     return out.reshape(bs, slen, dim)
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 grouped GEMMs (parity unpinned: the reference delegates to torchao's
+# Float8TrainingOpConfig, torchtitan/components/quantization/float8.py:260-288,
+# which is absent; this restates its published rowwise recipe)
+# ---------------------------------------------------------------------------
+
+FP8_MAX = 448.0  # largest finite float8_e4m3fn
+FP8_PAD = 16  # token-group alignment for fp8 grouped GEMMs (quantization/__init__.py:37-40)
+
+
+def quant_fp8_rows(x: torch.Tensor, dim: int = -1):
+    """Dynamic fp8 quantization with one scale per slice along `dim`:
+    s = max(amax, 1e-12) / 448 (fp32), q = e4m3fn(x / s) (round to nearest even).
+    Returns (q float8_e4m3fn, s fp32 with `dim` kept as size 1)."""
+    xf = x.float()
+    amax = xf.abs().amax(dim=dim, keepdim=True).clamp_min(1e-12)
+    s = amax / FP8_MAX
+    q = (xf / s).to(torch.float8_e4m3fn)
+    return q, s
+
+
+def _fp8_mm(qa, sa, qb, sb):
+    """(qa @ qb^T) accumulated in fp64 then scaled as (acc * sa) * sb in fp32."""
+    acc = (qa.double() @ qb.double().t()).float()
+    return (acc * sa) * sb.reshape(1, -1)
+
+
+def experts_fp8_forward(w1, w2, w3, x, counts):
+    """fp8 forward of _run_experts_grouped_mm (moe.py:53-70): x and h quantized
+    per token row, each weight per output row (per expert column), fp32
+    accumulate, outputs g, u, h, y rounded to bf16 at the reference's points."""
+    qx, sx = quant_fp8_rows(x)
+    qw1, sw1 = quant_fp8_rows(w1)
+    qw3, sw3 = quant_fp8_rows(w3)
+    qw2, sw2 = quant_fp8_rows(w2)
+    gs, us, hs = [], [], []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        g = _fp8_mm(qx[sl], sx[sl], qw1[e], sw1[e]).bfloat16()
+        u = _fp8_mm(qx[sl], sx[sl], qw3[e], sw3[e]).bfloat16()
+        gs.append(g); us.append(u); hs.append(F.silu(g) * u)
+        start += c
+    g, u, h = torch.cat(gs), torch.cat(us), torch.cat(hs)
+    qh, sh = quant_fp8_rows(h)
+    ys = []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        ys.append(_fp8_mm(qh[sl], sh[sl], qw2[e], sw2[e]).bfloat16())
+        start += c
+    return torch.cat(ys), g, u, h
+
+
+def experts_fp8_backward(w1, w2, w3, x, counts, g, u, h, dy):
+    """fp8 backward matching experts_fp8_forward: dh = dy . w2 with dy per row and
+    w2 per (expert, h) column over D; SwiGLU backward in bf16; dx = bf16(dg . w1)
+    + bf16(du . w3) with dg, du per row and w1, w3 per (expert, d) column over H;
+    dw = per-group products over the expert's tokens with both operands scaled
+    per (group, column) over those tokens."""
+    E, H, D = w1.shape
+    qdy, sdy = quant_fp8_rows(dy)
+    dgs, dus = [], []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        qw2t, sw2t = quant_fp8_rows(w2[e].t())  # [H, D] rows
+        dh = _fp8_mm(qdy[sl], sdy[sl], qw2t, sw2t).bfloat16()
+        gg, uu = g[sl], u[sl]
+        sl_g = F.silu(gg)
+        dsl = (dh * uu)  # bf16 op: grad of silu output
+        du = dh * sl_g
+        dg = torch.ops.aten.silu_backward(dsl, gg)
+        dgs.append(dg); dus.append(du)
+        start += c
+    dg, du = torch.cat(dgs), torch.cat(dus)
+    qdg, sdg = quant_fp8_rows(dg)
+    qdu, sdu = quant_fp8_rows(du)
+    dxs, dw1s, dw2s, dw3s = [], [], [], []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        qw1t, sw1t = quant_fp8_rows(w1[e].t())  # [D, H]
+        qw3t, sw3t = quant_fp8_rows(w3[e].t())
+        dx = (_fp8_mm(qdg[sl], sdg[sl], qw1t, sw1t).bfloat16() + _fp8_mm(qdu[sl], sdu[sl], qw3t, sw3t).bfloat16())
+        dxs.append(dx)
+        if c == 0:
+            dw1s.append(torch.zeros_like(w1[e])); dw3s.append(torch.zeros_like(w3[e])); dw2s.append(torch.zeros_like(w2[e]))
+        else:
+            qdgt, sdgt = quant_fp8_rows(dg[sl].t())  # [H, c]
+            qdut, sdut = quant_fp8_rows(du[sl].t())
+            qxt, sxt = quant_fp8_rows(x[sl].t())     # [D, c]
+            qdyt, sdyt = quant_fp8_rows(dy[sl].t())  # [D, c]
+            qht, sht = quant_fp8_rows(h[sl].t())     # [H, c]
+            dw1s.append(_fp8_mm(qdgt, sdgt, qxt, sxt).bfloat16())
+            dw3s.append(_fp8_mm(qdut, sdut, qxt, sxt).bfloat16())
+            dw2s.append(_fp8_mm(qdyt, sdyt, qht, sht).bfloat16())
+        start += c
+    return torch.cat(dxs), torch.stack(dw1s), torch.stack(dw2s), torch.stack(dw3s)

@@ -28,6 +28,7 @@ class LayerShape:
     std: float = 0.02
     bias: float = 0.01
     zipf: float | None = None
+    fp8: bool = False
 
 
 def build_layer(sh: LayerShape, dev: torch.device, seed: int):
@@ -60,6 +61,10 @@ def build_layer(sh: LayerShape, dev: torch.device, seed: int):
             bias = bias + 0.25 * ranks.pow(-sh.zipf) - 1.0 * (ranks > e - 20).float()
         moe.expert_bias.copy_(bias)
         moe.tokens_per_expert.zero_()
+    if sh.fp8:
+        from torchtitan_amd.quantization import Float8GroupedMMConverter
+
+        Float8GroupedMMConverter.Config(fqns=["experts"]).build().convert(moe)
     x = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
     g = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
     return moe, x, g

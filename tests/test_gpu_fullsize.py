@@ -7,10 +7,14 @@ run by torch on the same GPU (oracle.moe_forward_reference_ops):
          experts that never win (heavily skewed and empty groups);
   dsv3   DeepSeek-V3-style: 8192 tokens, dim 7168, 256 experts in 8 groups,
          top-4 groups then top-8, hidden 2048 + shared 2048, scores applied
-         after the experts.
+         after the experts;
+  kimi_fp8  the Kimi shape with 32768 tokens and fp8 e4m3 grouped GEMMs,
+         against the same bf16 reference (the reference's own fp8 path is
+         torchao's and absent, so fp8 parity is unpinned).
 
 Routing (indices, counts, top scores) must be bit-exact; the output and all
-gradients within 1e-2 normwise relative error (max |ours - ref| / max |ref|).
+gradients within 1e-2 normwise relative error (max |ours - ref| / max |ref|),
+0.1 for the fp8 layer against the bf16 reference.
 """
 
 import pytest
@@ -27,9 +31,11 @@ SHAPES = {
                        zipf=1.2),
     "dsv3": LayerShape(bs=1, slen=8192, dim=7168, experts=256, top_k=8, hidden=2048, shared_hidden=2048,
                        groups=(8, 4), score_before=False, std=0.006),
+    "kimi_fp8": LayerShape(bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+                           fp8=True),
 }
 
-TOL = 1e-2
+TOL = {"kimi_fp8": 0.1}
 
 
 @pytest.mark.parametrize("name", list(SHAPES))
@@ -45,7 +51,8 @@ def test_layer_at_benchmark_shape(dev, name):
                                           for k, v in res.items()), flush=True)
     if name == "zipf":
         assert int((counts == 0).sum()) >= 20 and counts.max() > 5 * counts.float().mean()
-    bad = {k: v[0] for k, v in res.items() if not v[0] <= TOL}
+    tol = TOL.get(name, 1e-2)
+    bad = {k: v[0] for k, v in res.items() if not v[0] <= tol}
     assert not bad, bad
     del moe, x, g
     torch.cuda.empty_cache()

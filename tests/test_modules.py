@@ -129,3 +129,16 @@ def test_kimi_init():
     init_kimi_moe_weights(layer, std=0.02)
     assert torch.count_nonzero(layer._moe.expert_bias) == 0
     assert 0.01 < layer._moe.experts.w1.std().item() < 0.03
+
+
+def test_float8_converter_selects_experts_by_fqn():
+    from torchtitan_amd.quantization import Float8GroupedMMConverter, find_pad_multiple
+
+    model = torch.nn.ModuleDict({"a": _cfg(hs=0).build(), "b": _cfg(hs=0).build()})
+    conv_cfg = Float8GroupedMMConverter.Config(fqns=["a.experts"])
+    names = conv_cfg.build().convert(model)
+    assert names == ["a.experts"]
+    assert model["a"].experts.float8 and not model["b"].experts.float8
+    assert set(model["a"].state_dict()) == set(model["b"].state_dict())
+    assert find_pad_multiple([conv_cfg]) == 16 and find_pad_multiple([]) is None
+    assert Float8GroupedMMConverter.Config(fqns="experts").build().fqns == ["experts"]

@@ -1,0 +1,777 @@
+// fp8 e4m3 grouped GEMMs for the SwiGLU experts on MI355X (CDNA4 fp8 MFMA).
+//
+// The reference's fp8 MoE path is torchao's Float8TrainingOpConfig applied to
+// the experts (torchtitan/components/quantization/float8.py:260-288): dynamic
+// rowwise scaling, fp8 grouped GEMMs with fp32 accumulation, bf16 outputs,
+// token groups padded to 16 (quantization/__init__.py:37-40). This file
+// restates that recipe for gfx950:
+//
+//  * quantizers (HBM-bound): x -> (q = e4m3fn(x / s), s = max(amax, 1e-12) / 448)
+//      - moe_fp8_quant_rows: one scale per row of a [rows, K] tensor;
+//      - moe_fp8_quant_cols_t: per expert, one scale per column b of an
+//        [E, A, B] tensor, written transposed as [E, B, A];
+//      - moe_fp8_quant_tokens_t: per expert token group, one scale per column c
+//        of a [R, C] tensor, written transposed as [C, Rpad] with every group
+//        starting at a multiple of 16 tokens (zero padded).
+//    so that every GEMM below reads both operands contiguous along k.
+//  * fp8 grouped GEMMs, C[m][n] = (sum_k qP[m][k] qQ[n][k]) * sP[m] * sQ[n],
+//    on v_mfma_scale_f32_16x16x128_f8f6f4 (unit MX scales): forward gate_up
+//    (with the SwiGLU epilogue) and down; backward dgu (dy . w2 with the
+//    SwiGLU backward), dx (dg . w1 + du . w3, two scaled products added in
+//    bf16), dw13 and dw2 (k = the expert's token group).
+//
+// Tiles: 256 threads, 2 x 2 waves, BM x BN output tile, 128 k per stage held
+// as two 64-byte half-tiles in the conflict-free chunk-major LDS layout of
+// the bf16 kernels; each lane's 32-byte MFMA fragment is chunk (lane >> 4) of
+// both halves (any k order is valid as long as both operands share it).
+#include "common.h"
+
+namespace moe {
+namespace fp8 {
+
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kFp8Max = 448.0f;
+constexpr int kPad = 16;
+constexpr int kMaxE = 1024;
+constexpr int kThreads = 256;
+
+// float -> float8_e4m3fn, round to nearest even, saturating at +-448.
+__device__ __forceinline__ uint32_t e4m3(float x) {
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  const float a = fabsf(x);
+  uint32_t q;
+  if (!(a < 448.0f)) {
+    q = (a == a) ? 0x7eu : 0x7fu;  // saturate; NaN stays NaN
+  } else if (a < 0.015625f) {        // below 2^-6: subnormal steps of 2^-9
+    q = (uint32_t)rintf(a * 512.0f);
+  } else {
+    uint32_t u = __float_as_uint(a);
+    u += 0x7ffffu + ((u >> 20) & 1u);  // round the mantissa to 3 bits, ties to even
+    q = (u >> 20) - ((127u - 7u) << 3);
+    q = q > 0x7eu ? 0x7eu : q;
+  }
+  return sign | q;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ float scale_of(float amax) { return fmaxf(amax, 1e-12f) / kFp8Max; }
+
+// ---------------------------------------------------------------------------
+// quantizers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float amax8(uint4 v) {
+  return fmaxf(fmaxf(fmaxf(fabsf(bf_lo(v.x)), fabsf(bf_hi(v.x))), fmaxf(fabsf(bf_lo(v.y)), fabsf(bf_hi(v.y)))),
+               fmaxf(fmaxf(fabsf(bf_lo(v.z)), fabsf(bf_hi(v.z))), fmaxf(fabsf(bf_lo(v.w)), fabsf(bf_hi(v.w)))));
+}
+
+__device__ __forceinline__ uint2 quant8(uint4 v, float s) {
+  const uint32_t lo = e4m3(bf_lo(v.x) / s) | (e4m3(bf_hi(v.x) / s) << 8) | (e4m3(bf_lo(v.y) / s) << 16) |
+                      (e4m3(bf_hi(v.y) / s) << 24);
+  const uint32_t hi = e4m3(bf_lo(v.z) / s) | (e4m3(bf_hi(v.z) / s) << 8) | (e4m3(bf_lo(v.w) / s) << 16) |
+                      (e4m3(bf_hi(v.w) / s) << 24);
+  return make_uint2(lo, hi);
+}
+
+// One wave per row of x [rows, K] (K % 8 == 0). With CPL > 0 the row (up to
+// 64 * CPL 16-byte chunks) stays in registers between the amax and the
+// quantize step, so it is read once; CPL == 0 reads it twice.
+template <int CPL>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int K,
+                                                         uint8_t* __restrict__ q, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int cpr = K / 8;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + wv; r < rows; r += (int64_t)gridDim.x * 4) {
+    const uint16_t* xr = x + r * K;
+    uint8_t* qr = q + r * K;
+    float amax = 0.f;
+    if constexpr (CPL > 0) {
+      uint4 v[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < cpr ? *(const uint4*)(xr + c * 8) : make_uint4(0, 0, 0, 0);
+        amax = fmaxf(amax, amax8(v[i]));
+      }
+      const float s = scale_of(wave_max(amax));
+      if (lane == 0) scale[r] = s;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < cpr) *(uint2*)(qr + c * 8) = quant8(v[i], s);
+      }
+    } else {
+      for (int c = lane; c < cpr; c += 64) amax = fmaxf(amax, amax8(*(const uint4*)(xr + c * 8)));
+      const float s = scale_of(wave_max(amax));
+      if (lane == 0) scale[r] = s;
+      for (int c = lane; c < cpr; c += 64) *(uint2*)(qr + c * 8) = quant8(*(const uint4*)(xr + c * 8), s);
+    }
+  }
+}
+
+// Column amax over `n_rows` rows of a 64-column slab (row stride ld elements)
+// -> s_amax[64]; every thread of the block calls it.
+__device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int64_t ld, int n_rows, float* s_red,
+                                          float* s_amax) {
+  const int t = threadIdx.x;
+  const int ch = t & 7, r0 = t >> 3;  // 8 chunks of 8 columns, 32 rows per pass
+  float m[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m[i] = 0.f;
+  for (int r = r0; r < n_rows; r += 32) {
+    const uint4 v = *(const uint4*)(base + (int64_t)r * ld + ch * 8);
+    m[0] = fmaxf(m[0], fabsf(bf_lo(v.x))); m[1] = fmaxf(m[1], fabsf(bf_hi(v.x)));
+    m[2] = fmaxf(m[2], fabsf(bf_lo(v.y))); m[3] = fmaxf(m[3], fabsf(bf_hi(v.y)));
+    m[4] = fmaxf(m[4], fabsf(bf_lo(v.z))); m[5] = fmaxf(m[5], fabsf(bf_hi(v.z)));
+    m[6] = fmaxf(m[6], fabsf(bf_lo(v.w))); m[7] = fmaxf(m[7], fabsf(bf_hi(v.w)));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s_red[(ch * 8 + i) * 33 + r0] = m[i];
+  __syncthreads();
+  if (t < 64) {
+    float a = 0.f;
+    for (int j = 0; j < 32; ++j) a = fmaxf(a, s_red[t * 33 + j]);
+    s_amax[t] = a;
+  }
+  __syncthreads();
+}
+
+// Transposes a [rows x 64] bf16 slab (64 rows per pass) into 64 output rows of
+// fp8 (one per slab column), quantized with that column's scale.
+// out row b starts at out + b * ldo; rows >= n_rows up to n_out are zero.
+__device__ __forceinline__ void slab_transpose_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows,
+                                                     int n_out, uint8_t* __restrict__ out, int64_t ldo,
+                                                     const float* s_scale, uint16_t (*s_tile)[66]) {
+  const int t = threadIdx.x;
+  for (int a0 = 0; a0 < n_out; a0 += 64) {
+    // load 64 rows x 64 columns (rows past n_rows are zero)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = t + i * 256;
+      const int r = c >> 3, ch = c & 7;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (a0 + r < n_rows) v = *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8);
+      const uint16_t* pv = (const uint16_t*)&v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_tile[ch * 8 + j][r] = pv[j];
+    }
+    __syncthreads();
+    // write: thread -> (column b, 16 rows)
+    const int b = t >> 2, seg = (t & 3) * 16;
+    if (a0 + seg < n_out) {
+      const float s = s_scale[b];
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        w[j] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[j] |= e4m3(bf2f(s_tile[b][seg + 4 * j + i]) / s) << (8 * i);
+      }
+      *(uint4*)(out + (int64_t)b * ldo + a0 + seg) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    __syncthreads();
+  }
+}
+
+// x [E][A][B] -> q rows (e, b) of A values at q + e * q_estride + b * q_ld, and
+// scale[e * s_estride + b] = amax over A. Block per (e, 64 columns).
+__global__ __launch_bounds__(256) void quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
+                                                           uint8_t* __restrict__ q, int64_t q_estride, int64_t q_ld,
+                                                           float* __restrict__ scale, int64_t s_estride) {
+  __shared__ float s_red[64 * 33];
+  __shared__ float s_amax[64];
+  __shared__ uint16_t s_tile[64][66];
+  const int nb = B / 64;
+  const int64_t e = blockIdx.x / nb;
+  const int b0 = (blockIdx.x % nb) * 64;
+  const uint16_t* base = x + e * A * (int64_t)B + b0;
+  slab_amax(base, B, A, s_red, s_amax);
+  if (threadIdx.x < 64) {
+    const float s = scale_of(s_amax[threadIdx.x]);
+    s_amax[threadIdx.x] = s;
+    scale[e * s_estride + b0 + threadIdx.x] = s;
+  }
+  __syncthreads();
+  slab_transpose_quant(base, B, A, A, q + e * q_estride + b0 * q_ld, q_ld, s_amax, s_tile);
+}
+
+// x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
+// 16-aligned offset pstart_e, zero padded to ceil16(count_e)), scale [E][C].
+// Block per (e, 64 columns); empty groups exit.
+__global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ counts,
+                                                             int64_t R, int E, int C, int64_t Rpad,
+                                                             uint8_t* __restrict__ q, float* __restrict__ scale) {
+  __shared__ float s_red[64 * 33];
+  __shared__ float s_amax[64];
+  __shared__ uint16_t s_tile[64][66];
+  __shared__ int s_tmp[8];
+  __shared__ int s_seg[2];
+  const int nc = C / 64;
+  const int e = blockIdx.x / nc;
+  const int c0 = (blockIdx.x % nc) * 64;
+  {
+    int cnt[4], pc[4], st[4], pst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ee = threadIdx.x * 4 + i;
+      const int64_t c = ee < E ? counts[ee] : 0;
+      cnt[i] = c < 0 ? 0 : (int)(c > R ? R : c);
+      pc[i] = (cnt[i] + kPad - 1) / kPad * kPad;
+    }
+    block_exclusive_scan4(cnt, st, s_tmp);
+    block_exclusive_scan4(pc, pst, s_tmp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (threadIdx.x * 4 + i == e) { s_seg[0] = st[i]; s_seg[1] = pst[i]; s_red[0] = __int_as_float(cnt[i]); }
+    __syncthreads();
+  }
+  const int seg0 = s_seg[0], pstart = s_seg[1];
+  int n = __float_as_int(s_red[0]);
+  __syncthreads();
+  if ((int64_t)seg0 + n > R) n = (int)(R - seg0 > 0 ? R - seg0 : 0);
+  const int n_out = (n + kPad - 1) / kPad * kPad;
+  if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
+  const uint16_t* base = x + (int64_t)seg0 * C + c0;
+  slab_amax(base, C, n, s_red, s_amax);
+  if (threadIdx.x < 64) {
+    const float s = scale_of(s_amax[threadIdx.x]);
+    s_amax[threadIdx.x] = s;
+    scale[(int64_t)e * C + c0 + threadIdx.x] = s;
+  }
+  __syncthreads();
+  slab_transpose_quant(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, s_amax, s_tile);
+}
+
+// ---------------------------------------------------------------------------
+// fp8 grouped GEMM
+// ---------------------------------------------------------------------------
+enum Mode : int { kGateUp = 0, kDown = 1, kDgu = 2, kDx = 3, kDw13 = 4, kDw2 = 5 };
+
+struct Params {
+  const int64_t* counts;
+  int64_t R, Rpad;
+  int E, D, H;
+  const uint8_t* qp;  // P operand (fp8, k-contiguous rows)
+  const uint8_t* qq;  // Q operand
+  const uint8_t* qq2; // second Q operand (w3 for gate_up)
+  const float* sp;    // P scales
+  const float* sq;    // Q scales
+  const float* sq2;   // second Q scales
+  const uint16_t* g;  // saved g, u for the SwiGLU backward
+  const uint16_t* u;
+  uint16_t* o0;  // outputs (mode dependent)
+  uint16_t* o1;
+  uint16_t* o2;
+};
+
+template <int ROWS>
+__device__ __forceinline__ int lds_off(int r, int kc) {
+  return (kc * ROWS + (r ^ (((2 * kc) ^ (r >> 3)) & 7))) * 16;  // bytes
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+template <int MODE, int BM, int BN, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
+  constexpr bool kRowGrouped = MODE <= kDx;
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+  constexpr int PCH = BM * 8 / kThreads;  // 16-byte chunks per thread per stage (128 k = 8 chunks per row)
+  constexpr int QCH = BN * 8 / kThreads;
+  constexpr int HALF_P = BM * 64, HALF_Q = BN * 64;  // bytes per 64-byte half-tile
+  __shared__ __attribute__((aligned(16))) uint8_t sP[2][2 * HALF_P];
+  __shared__ __attribute__((aligned(16))) uint8_t sQ[2][2 * HALF_Q];
+  __shared__ int s_seg[kMaxE + 1];
+  __shared__ int s_pst[kMaxE + 1];
+  __shared__ int s_tile[kMaxE + 1];
+  __shared__ int s_tmp[8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int E = p.E, D = p.D, H = p.H;
+  int Ntot = 0, Kfix = 0, Mfix = 0;
+  if (MODE == kGateUp) { Ntot = 2 * H; Kfix = D; }
+  if (MODE == kDown) { Ntot = D; Kfix = H; }
+  if (MODE == kDgu) { Ntot = H; Kfix = D; }
+  if (MODE == kDx) { Ntot = D; Kfix = 2 * H; }
+  if (MODE == kDw13) { Ntot = D; Mfix = 2 * H; }
+  if (MODE == kDw2) { Ntot = H; Mfix = D; }
+  const int NT = Ntot / BN;
+  const int MT = kRowGrouped ? 0 : Mfix / BM;
+  {
+    int cnt[4], tl[4], seg[4], pc[4], pst[4], tst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid * 4 + i;
+      const int64_t c = (e < E) ? p.counts[e] : 0;
+      cnt[i] = c < 0 ? 0 : (c > p.R ? (int)p.R : (int)c);
+    }
+    {
+      int pre[4];
+      block_exclusive_scan4(cnt, pre, s_tmp);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t lo = pre[i] < p.R ? pre[i] : p.R;
+        const int64_t hi = (int64_t)pre[i] + cnt[i] < p.R ? (int64_t)pre[i] + cnt[i] : p.R;
+        cnt[i] = (int)(hi - lo);
+        pc[i] = (cnt[i] + kPad - 1) / kPad * kPad;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid * 4 + i;
+      tl[i] = (e < E) ? (kRowGrouped ? ((cnt[i] + BM - 1) / BM) * NT : MT * NT) : 0;
+    }
+    const int rtot = block_exclusive_scan4(cnt, seg, s_tmp);
+    const int ptot = block_exclusive_scan4(pc, pst, s_tmp);
+    const int ttot = block_exclusive_scan4(tl, tst, s_tmp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid * 4 + i;
+      if (e < E) { s_seg[e] = seg[i]; s_pst[e] = pst[i]; s_tile[e] = tst[i]; }
+    }
+    if (tid == 0) { s_seg[E] = rtot; s_pst[E] = ptot; s_tile[E] = ttot; }
+    __syncthreads();
+  }
+  if (!kRowGrouped && (int64_t)s_pst[E] > p.Rpad) return;  // inconsistent padding: nothing is read out of bounds
+  const int total_tiles = s_tile[E];
+  const int G = gridDim.x;
+  const int lb = (G % 8 == 0) ? ((int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
+
+  for (int t = lb; t < total_tiles; t += G) {
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_tile[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int64_t e64 = e;
+    const int local = t - s_tile[e];
+    const int seg0 = s_seg[e], seg1 = s_seg[e + 1];
+    int mt, nt;
+    if (kRowGrouped) {
+      const int mtiles = (seg1 - seg0 + BM - 1) / BM;
+      nt = local / mtiles;
+      mt = local - nt * mtiles;
+    } else {
+      nt = local / MT;
+      mt = local - nt * MT;
+    }
+    const int pst0 = s_pst[e];
+    const int Klen = kRowGrouped ? Kfix : (s_pst[e + 1] - pst0);  // bytes of k
+    const int nk = (Klen + 127) / 128;
+    const int row0 = seg0 + mt * BM;
+
+    // P / Q row pointers (k-contiguous), row strides in bytes
+    auto p_row = [&](int m, bool& ok) -> const uint8_t* {
+      if (kRowGrouped) {
+        const int r = row0 + m;
+        ok = r < seg1;
+        return p.qp + (int64_t)r * Kfix;
+      }
+      ok = true;
+      return p.qp + (int64_t)(mt * BM + m) * p.Rpad + pst0;
+    };
+    auto q_row = [&](int n) -> const uint8_t* {
+      if (MODE == kGateUp) {
+        const int blk = n >> 4;
+        const int hc = nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
+        return ((blk & 1) ? p.qq2 : p.qq) + (e64 * H + hc) * (int64_t)D;
+      }
+      if (MODE == kDown) return p.qq + (e64 * D + nt * BN + n) * (int64_t)H;
+      if (MODE == kDgu) return p.qq + (e64 * H + nt * BN + n) * (int64_t)D;
+      if (MODE == kDx) return p.qq + (e64 * D + nt * BN + n) * (int64_t)(2 * H);
+      return p.qq + (int64_t)(nt * BN + n) * p.Rpad + pst0;
+    };
+
+    uint4 rp[PCH], rq[QCH], np[PCH], nq[QCH];
+    auto load = [&](uint4 (&dp)[PCH], uint4 (&dq)[QCH], int kt) {
+      const int k0 = kt * 128;
+#pragma unroll
+      for (int i = 0; i < PCH; ++i) {
+        const int c = tid + i * kThreads;
+        const int half = c / (BM * 4), w = c % (BM * 4);
+        const int m = w >> 2, kc = w & 3;
+        const int kb = k0 + half * 64 + kc * 16;
+        bool ok;
+        const uint8_t* rowp = p_row(m, ok);
+        dp[i] = (ok && kb < Klen) ? *(const uint4*)(rowp + kb) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < QCH; ++i) {
+        const int c = tid + i * kThreads;
+        const int half = c / (BN * 4), w = c % (BN * 4);
+        const int n = w >> 2, kc = w & 3;
+        const int kb = k0 + half * 64 + kc * 16;
+        dq[i] = (kb < Klen) ? *(const uint4*)(q_row(n) + kb) : make_uint4(0, 0, 0, 0);
+      }
+    };
+    auto store = [&](const uint4 (&dp)[PCH], const uint4 (&dq)[QCH], int s) {
+#pragma unroll
+      for (int i = 0; i < PCH; ++i) {
+        const int c = tid + i * kThreads;
+        const int half = c / (BM * 4), w = c % (BM * 4);
+        *(uint4*)(&sP[s][half * HALF_P + lds_off<BM>(w >> 2, w & 3)]) = dp[i];
+      }
+#pragma unroll
+      for (int i = 0; i < QCH; ++i) {
+        const int c = tid + i * kThreads;
+        const int half = c / (BN * 4), w = c % (BN * 4);
+        *(uint4*)(&sQ[s][half * HALF_Q + lds_off<BN>(w >> 2, w & 3)]) = dq[i];
+      }
+    };
+
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int ml = lane & 15, nql = (lane >> 4) * 4, g4 = lane >> 4;
+    auto compute = [&](int s) {
+      v8i_t af[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = wm * WM + i * 16 + ml;
+        const uint4 a0 = *(const uint4*)(&sP[s][lds_off<BM>(m, g4)]);
+        const uint4 a1 = *(const uint4*)(&sP[s][HALF_P + lds_off<BM>(m, g4)]);
+        af[i] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = wn * WN + j * 16 + ml;
+        const uint4 b0 = *(const uint4*)(&sQ[s][lds_off<BN>(n, g4)]);
+        const uint4 b1 = *(const uint4*)(&sQ[s][HALF_Q + lds_off<BN>(n, g4)]);
+        const v8i_t bq = v8i_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq, af[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+      }
+    };
+
+    // dx = dg.w1 + du.w3: the w1 half (k < H) is scaled, rounded and parked in
+    // the output rows, then added (in bf16) to the scaled w3 half at the end.
+    auto park_dx_half = [&]() {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = row0 + wm * WM + i * 16 + ml;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (r < seg1) {
+            const int n = nt * BN + wn * WN + j * 16 + nql;
+            const float sp = p.sp[(int64_t)r * 2];
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * p.sq[e64 * 2 * D + n + q];
+            *(uint2*)(p.o0 + (int64_t)r * D + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+          }
+          acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    };
+    const int kt_half = (MODE == kDx) ? H / 128 : -1;
+
+    __syncthreads();
+    if (nk > 0) {
+      load(rp, rq, 0);
+      store(rp, rq, 0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load(np, nq, kt + 1);
+      if (MODE == kDx && kt == kt_half) park_dx_half();
+      compute(cur);
+      if (kt + 1 < nk) store(np, nq, cur ^ 1);
+      __syncthreads();
+    }
+
+    // ---- epilogues: lane holds C[m = .. + ml][n = .. + nql + 0..3] ----
+    if (MODE == kGateUp) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = row0 + wm * WM + i * 16 + ml;
+        if (r < seg1) {
+          const float sx = p.sp[r];
+#pragma unroll
+          for (int jj = 0; jj < TN / 2; ++jj) {
+            const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nql;
+            float gv[4], uv[4], hv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              gv[q] = round_bf((acc[i][2 * jj][q] * sx) * p.sq[e64 * H + hc + q]);
+              uv[q] = round_bf((acc[i][2 * jj + 1][q] * sx) * p.sq2[e64 * H + hc + q]);
+              hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+            }
+            const int64_t off = (int64_t)r * H + hc;
+            *(uint2*)(p.o0 + off) = make_uint2(pack_bf2(gv[0], gv[1]), pack_bf2(gv[2], gv[3]));
+            *(uint2*)(p.o1 + off) = make_uint2(pack_bf2(uv[0], uv[1]), pack_bf2(uv[2], uv[3]));
+            *(uint2*)(p.o2 + off) = make_uint2(pack_bf2(hv[0], hv[1]), pack_bf2(hv[2], hv[3]));
+          }
+        }
+      }
+    } else if (MODE == kDown || MODE == kDx) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = row0 + wm * WM + i * 16 + ml;
+        if (r < seg1) {
+          const float sp = (MODE == kDx) ? p.sp[(int64_t)r * 2 + 1] : p.sp[r];
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int n = nt * BN + wn * WN + j * 16 + nql;
+            uint16_t* dst = p.o0 + (int64_t)r * D + n;
+            const float* sq = (MODE == kDx) ? p.sq + e64 * 2 * D + D + n : p.sq + e64 * D + n;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * sq[q];
+            if (MODE == kDx) {
+              const uint2 pw = *(const uint2*)dst;
+              v[0] = bf_lo(pw.x) + round_bf(v[0]);
+              v[1] = bf_hi(pw.x) + round_bf(v[1]);
+              v[2] = bf_lo(pw.y) + round_bf(v[2]);
+              v[3] = bf_hi(pw.y) + round_bf(v[3]);
+            }
+            *(uint2*)dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+          }
+        }
+      }
+    } else if (MODE == kDgu) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = row0 + wm * WM + i * 16 + ml;
+        if (r < seg1) {
+          const float sp = p.sp[r];
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int hh = nt * BN + wn * WN + j * 16 + nql;
+            const int64_t off = (int64_t)r * H + hh;
+            const uint2 gw = *(const uint2*)(p.g + off);
+            const uint2 uw = *(const uint2*)(p.u + off);
+            const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
+            const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
+            float dg[4], du[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float dh = round_bf((acc[i][j][q] * sp) * p.sq[e64 * H + hh + q]);
+              const float sl = round_bf(silu_f(gv[q]));
+              const float dsl = round_bf(dh * uv[q]);
+              du[q] = dh * sl;
+              const float sg = 1.0f / (1.0f + expf(-gv[q]));
+              dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
+            }
+            const int64_t o2 = (int64_t)r * (2 * H) + hh;
+            *(uint2*)(p.o0 + o2) = make_uint2(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]));
+            *(uint2*)(p.o0 + o2 + H) = make_uint2(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]));
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = mt * BM + wm * WM + i * 16 + ml;
+        // an expert without tokens gets zero gradients (its scales are never written)
+        const float sp = (nk > 0) ? p.sp[e64 * Mfix + m] : 0.f;
+        uint16_t* rowp;
+        if (MODE == kDw13)
+          rowp = (m < H) ? p.o0 + (e64 * H + m) * (int64_t)D : p.o1 + (e64 * H + (m - H)) * (int64_t)D;
+        else
+          rowp = p.o0 + (e64 * D + m) * (int64_t)H;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = nt * BN + wn * WN + j * 16 + nql;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = (nk > 0) ? (acc[i][j][q] * sp) * p.sq[e64 * Ntot + n + q] : 0.f;
+          *(uint2*)(rowp + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+        }
+      }
+    }
+  }
+}
+
+static int g_cus[64];
+static int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!g_cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_cus[dev] = n;
+  }
+  return g_cus[dev];
+}
+
+constexpr int kBM = 128, kBN = 128, kOcc = 2;
+
+template <int MODE>
+static void launch(const Params& p, hipStream_t stream) {
+  int64_t max_tiles;
+  if (MODE == kGateUp) max_tiles = (p.R / kBM + p.E) * (2 * p.H / kBN);
+  else if (MODE == kDown || MODE == kDx) max_tiles = (p.R / kBM + p.E) * (p.D / kBN);
+  else if (MODE == kDgu) max_tiles = (p.R / kBM + p.E) * (p.H / kBN);
+  else if (MODE == kDw13) max_tiles = (int64_t)p.E * (2 * p.H / kBM) * (p.D / kBN);
+  else max_tiles = (int64_t)p.E * (p.D / kBM) * (p.H / kBN);
+  int64_t g = (int64_t)cu_count() * kOcc;
+  if (g > max_tiles) g = max_tiles;
+  if (g >= 8) g -= g % 8;
+  if (g < 1) g = 1;
+  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, kBM, kBN, kOcc>), dim3((int)g), dim3(kThreads), 0, stream, p);
+}
+
+static int check_shape(int64_t R, int E, int D, int H) {
+  if (R < 0 || E < 1 || E > kMaxE || D < 256 || H < 256) return kErrInvalidArgument;
+  if (D % 256 || H % 256) return kErrUnsupportedShape;
+  if (R >= (int64_t)INT32_MAX / 2) return kErrUnsupportedShape;
+  return kOk;
+}
+
+}  // namespace fp8
+}  // namespace moe
+
+using namespace moe;
+using namespace moe::fp8;
+
+MOE_API int64_t moe_fp8_padded_rows(int64_t n_rows, int32_t n_experts) {
+  return n_rows + (int64_t)n_experts * (kPad - 1);
+}
+
+MOE_API int moe_fp8_quant_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q, float* scale,
+                               hipStream_t stream) {
+  if (rows < 0 || cols < 8 || cols % 8) return kErrInvalidArgument;
+  if (rows == 0) return kOk;
+  if (!x || !q || !scale) return kErrInvalidArgument;
+  int64_t g = (rows + 3) / 4;
+  if (g > 16384) g = 16384;
+  const int chunks = cols / 8;
+  if (chunks <= 64 * 2)
+    hipLaunchKernelGGL(quant_rows_kernel<2>, dim3((int)g), dim3(256), 0, stream, x, rows, cols, q, scale);
+  else if (chunks <= 64 * 4)
+    hipLaunchKernelGGL(quant_rows_kernel<4>, dim3((int)g), dim3(256), 0, stream, x, rows, cols, q, scale);
+  else if (chunks <= 64 * 8)
+    hipLaunchKernelGGL(quant_rows_kernel<8>, dim3((int)g), dim3(256), 0, stream, x, rows, cols, q, scale);
+  else if (chunks <= 64 * 16)
+    hipLaunchKernelGGL(quant_rows_kernel<16>, dim3((int)g), dim3(256), 0, stream, x, rows, cols, q, scale);
+  else
+    hipLaunchKernelGGL(quant_rows_kernel<0>, dim3((int)g), dim3(256), 0, stream, x, rows, cols, q, scale);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
+                                 int64_t q_expert_stride, int64_t q_row_stride, float* scale,
+                                 int64_t scale_expert_stride, hipStream_t stream) {
+  if (n_experts < 1 || a < 16 || a % 16 || b < 64 || b % 64) return kErrInvalidArgument;
+  if (q_row_stride < a || q_row_stride % 16 || q_expert_stride < (int64_t)(b - 1) * q_row_stride + a ||
+      scale_expert_stride < b)
+    return kErrInvalidArgument;
+  if (!x || !q || !scale) return kErrInvalidArgument;
+  hipLaunchKernelGGL(quant_cols_t_kernel, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
+                     q_expert_stride, q_row_stride, scale, scale_expert_stride);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                   int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
+                                   hipStream_t stream) {
+  if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
+  if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
+  if (!x || !counts || !q || !scale) return kErrInvalidArgument;
+  hipLaunchKernelGGL(quant_tokens_t_kernel, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts, n_rows,
+                     n_experts, cols, padded_rows, q, scale);
+  return launch_status();
+}
+
+static int fp8_params(Params& p, const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                      int32_t hidden) {
+  const int st = check_shape(n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (!counts) return kErrInvalidArgument;
+  p = Params{};
+  p.counts = counts; p.R = n_rows; p.E = n_experts; p.D = dim; p.H = hidden;
+  return kOk;
+}
+
+MOE_API int moe_fp8_gemm_gate_up(const uint8_t* qx, const float* sx, const uint8_t* qw1, const float* sw1,
+                                 const uint8_t* qw3, const float* sw3, const int64_t* counts, int64_t n_rows,
+                                 int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* g, uint16_t* u,
+                                 uint16_t* h, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qx || !sx || !qw1 || !sw1 || !qw3 || !sw3 || !g || !u || !h) return kErrInvalidArgument;
+  p.qp = qx; p.sp = sx; p.qq = qw1; p.sq = sw1; p.qq2 = qw3; p.sq2 = sw3; p.o0 = g; p.o1 = u; p.o2 = h;
+  launch<kGateUp>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_gemm_down(const uint8_t* qh, const float* sh, const uint8_t* qw2, const float* sw2,
+                              const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                              int32_t hidden, uint16_t* y, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qh || !sh || !qw2 || !sw2 || !y) return kErrInvalidArgument;
+  p.qp = qh; p.sp = sh; p.qq = qw2; p.sq = sw2; p.o0 = y;
+  launch<kDown>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_gemm_bwd_dgu(const uint8_t* qdy, const float* sdy, const uint8_t* qw2t, const float* sw2t,
+                                 const uint16_t* g, const uint16_t* u, const int64_t* counts, int64_t n_rows,
+                                 int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dgu,
+                                 hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qdy || !sdy || !qw2t || !sw2t || !g || !u || !dgu) return kErrInvalidArgument;
+  p.qp = qdy; p.sp = sdy; p.qq = qw2t; p.sq = sw2t; p.g = g; p.u = u; p.o0 = dgu;
+  launch<kDgu>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_gemm_bwd_dx(const uint8_t* qdgu, const float* sdgu, const uint8_t* qw13t, const float* sw13t,
+                                const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                int32_t hidden, uint16_t* dx, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qdgu || !sdgu || !qw13t || !sw13t || !dx) return kErrInvalidArgument;
+  p.qp = qdgu; p.sp = sdgu; p.qq = qw13t; p.sq = sw13t; p.o0 = dx;
+  launch<kDx>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_gemm_bwd_dw13(const uint8_t* qdgut, const float* sdgut, const uint8_t* qxt, const float* sxt,
+                                  const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                                  int32_t dim, int32_t hidden, uint16_t* dw1, uint16_t* dw3, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
+  if (!dw1 || !dw3 || (n_rows > 0 && (!qdgut || !sdgut || !qxt || !sxt))) return kErrInvalidArgument;
+  p.Rpad = padded_rows; p.qp = qdgut; p.sp = sdgut; p.qq = qxt; p.sq = sxt; p.o0 = dw1; p.o1 = dw3;
+  launch<kDw13>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const uint8_t* qht, const float* sht,
+                                 const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                                 int32_t dim, int32_t hidden, uint16_t* dw2, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
+  if (!dw2 || (n_rows > 0 && (!qdyt || !sdyt || !qht || !sht))) return kErrInvalidArgument;
+  p.Rpad = padded_rows; p.qp = qdyt; p.sp = sdyt; p.qq = qht; p.sq = sht; p.o0 = dw2;
+  launch<kDw2>(p, stream);
+  return launch_status();
+}

@@ -32,6 +32,7 @@ __all__ = [
     "TokenReorderer",
     "_run_experts_for_loop",
     "_run_experts_grouped_mm",
+    "_run_experts_grouped_mm_fp8",
 ]
 
 
@@ -67,6 +68,19 @@ def _run_experts_grouped_mm(
     return y.type_as(x)
 
 
+def _run_experts_grouped_mm_fp8(
+    w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor, x: torch.Tensor,
+    num_tokens_per_expert: torch.Tensor,
+) -> torch.Tensor:
+    """The fp8 grouped GEMMs the reference gets from torchao's
+    Float8TrainingOpConfig (torchtitan/components/quantization/float8.py:260-288):
+    dynamic rowwise e4m3 scaling, fp32 accumulation, bf16 outputs."""
+    y, _, _, _ = ops.grouped_swiglu_fp8(
+        x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16(), num_tokens_per_expert
+    )
+    return y.type_as(x)
+
+
 class GroupedExperts(Module):
     @dataclass(kw_only=True, slots=True)
     class Config(Module.Config):
@@ -82,9 +96,13 @@ class GroupedExperts(Module):
         self.w2 = nn.Parameter(torch.empty(config.num_experts, config.dim, config.hidden_dim))
         self.w3 = nn.Parameter(torch.empty(config.num_experts, config.hidden_dim, config.dim))
         self.use_grouped_mm = config.use_grouped_mm
+        # set by quantization.Float8GroupedMMConverter.convert
+        self.float8 = False
 
     def forward(self, x: torch.Tensor, num_tokens_per_expert: torch.Tensor) -> torch.Tensor:
         w1, w2, w3 = _local(self.w1), _local(self.w2), _local(self.w3)
+        if self.float8:
+            return _run_experts_grouped_mm_fp8(w1, w2, w3, x, num_tokens_per_expert)
         if self.use_grouped_mm:
             return _run_experts_grouped_mm(w1, w2, w3, x, num_tokens_per_expert)
         return _run_experts_for_loop(w1, w2, w3, x, num_tokens_per_expert)

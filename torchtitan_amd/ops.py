@@ -432,3 +432,132 @@ def _combine_bwd(ctx, g):
 
 
 combine.register_autograd(_combine_bwd, setup_context=_combine_setup)
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 grouped SwiGLU experts (dynamic rowwise scaling, fp32 accumulate)
+# ---------------------------------------------------------------------------
+FP8 = torch.uint8  # fp8 e4m3fn bytes as produced by the quantizers
+
+
+def _quant_rows(x: Tensor, cols: int) -> tuple[Tensor, Tensor]:
+    """x viewed as [rows, cols] bf16 -> (q uint8 [rows, cols], scale f32 [rows])."""
+    rows = x.numel() // cols
+    q = torch.empty(rows, cols, dtype=FP8, device=x.device)
+    s = torch.empty(rows, dtype=torch.float32, device=x.device)
+    call("moe_fp8_quant_rows", ptr(x), rows, cols, ptr(q), ptr(s), stream_of(x))
+    return q, s
+
+
+def _padded_rows(r: int, e: int) -> int:
+    n = lib().moe_fp8_padded_rows(r, e)
+    return (n + 15) // 16 * 16
+
+
+def _quant_tokens_t(x: Tensor, counts: Tensor, e: int, rpad: int) -> tuple[Tensor, Tensor]:
+    """x [R, C] bf16 in expert token groups -> (q [C, rpad], scale [E, C])."""
+    r, c = x.shape
+    q = torch.empty(c, rpad, dtype=FP8, device=x.device)
+    s = torch.empty(e, c, dtype=torch.float32, device=x.device)
+    call("moe_fp8_quant_tokens_t", ptr(x), ptr(counts), r, e, c, rpad, ptr(q), ptr(s), stream_of(x))
+    return q, s
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_fp8", mutates_args=())
+def grouped_swiglu_fp8(
+    x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """fp8 e4m3 grouped SwiGLU: x, h quantized per token row, weights per
+    output row; fp32 accumulate; bf16 outputs (y, g, u, h)."""
+    require_gpu(x, w1, w2, w3, num_tokens_per_expert)
+    for t, name in ((x, "x"), (w1, "w1"), (w2, "w2"), (w3, "w3")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"grouped_swiglu_fp8 expects bfloat16 {name}, got {t.dtype}")
+    x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    s = stream_of(x)
+    qx, sx = _quant_rows(x, d)
+    qw1, sw1 = _quant_rows(w1, d)
+    qw3, sw3 = _quant_rows(w3, d)
+    qw2, sw2 = _quant_rows(w2, h_dim)
+    g = x.new_empty(r, h_dim)
+    u = x.new_empty(r, h_dim)
+    h = x.new_empty(r, h_dim)
+    y = x.new_empty(r, d)
+    call("moe_fp8_gemm_gate_up", ptr(qx), ptr(sx), ptr(qw1), ptr(sw1), ptr(qw3), ptr(sw3), ptr(counts), r, e, d,
+         h_dim, ptr(g), ptr(u), ptr(h), s)
+    qh, sh = _quant_rows(h, h_dim)
+    call("moe_fp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
+    return y, g, u, h
+
+
+@grouped_swiglu_fp8.register_fake
+def _(x, w1, w2, w3, num_tokens_per_expert):
+    r, d = x.shape
+    h_dim = w1.shape[1]
+    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_fp8_backward", mutates_args=())
+def grouped_swiglu_fp8_backward(
+    dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
+    g: Tensor, u: Tensor, h: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
+    dy = dy.to(torch.bfloat16).contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    dev = x.device
+    s = stream_of(x)
+    # dh = dy . w2 (contraction over D): dy per row, w2 per (e, h) column over D
+    qdy, sdy = _quant_rows(dy, d)
+    qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
+    sw2t = torch.empty(e, h_dim, dtype=torch.float32, device=dev)
+    call("moe_fp8_quant_cols_t", ptr(w2), e, d, h_dim, ptr(qw2t), h_dim * d, d, ptr(sw2t), h_dim, s)
+    dgu = x.new_empty(r, 2 * h_dim)
+    call("moe_fp8_gemm_bwd_dgu", ptr(qdy), ptr(sdy), ptr(qw2t), ptr(sw2t), ptr(g), ptr(u), ptr(counts), r, e, d,
+         h_dim, ptr(dgu), s)
+    # dx = dg . w1 + du . w3 (contraction over H): one scale per dg / du row half,
+    # w1 and w3 per (e, d) column over H, written side by side as [E, D, 2H]
+    qdgu, sdgu = _quant_rows(dgu, h_dim)
+    qw13t = torch.empty(e, d, 2 * h_dim, dtype=FP8, device=dev)
+    sw13t = torch.empty(e, 2, d, dtype=torch.float32, device=dev)
+    call("moe_fp8_quant_cols_t", ptr(w1), e, h_dim, d, ptr(qw13t), d * 2 * h_dim, 2 * h_dim, ptr(sw13t), 2 * d, s)
+    call("moe_fp8_quant_cols_t", ptr(w3), e, h_dim, d, qw13t.data_ptr() + h_dim, d * 2 * h_dim, 2 * h_dim,
+         sw13t.data_ptr() + 4 * d, 2 * d, s)
+    dx = x.new_empty(r, d)
+    call("moe_fp8_gemm_bwd_dx", ptr(qdgu), ptr(sdgu), ptr(qw13t), ptr(sw13t), ptr(counts), r, e, d, h_dim,
+         ptr(dx), s)
+    # weight gradients: contraction over each expert's tokens (per-group scales)
+    rpad = _padded_rows(r, e)
+    qdgut, sdgut = _quant_tokens_t(dgu, counts, e, rpad)
+    qxt, sxt = _quant_tokens_t(x, counts, e, rpad)
+    dw1 = torch.empty_like(w1)
+    dw3 = torch.empty_like(w3)
+    call("moe_fp8_gemm_bwd_dw13", ptr(qdgut), ptr(sdgut), ptr(qxt), ptr(sxt), ptr(counts), r, rpad, e, d, h_dim,
+         ptr(dw1), ptr(dw3), s)
+    qdyt, sdyt = _quant_tokens_t(dy, counts, e, rpad)
+    qht, sht = _quant_tokens_t(h, counts, e, rpad)
+    dw2 = torch.empty_like(w2)
+    call("moe_fp8_gemm_bwd_dw2", ptr(qdyt), ptr(sdyt), ptr(qht), ptr(sht), ptr(counts), r, rpad, e, d, h_dim,
+         ptr(dw2), s)
+    return dx, dw1, dw2, dw3
+
+
+@grouped_swiglu_fp8_backward.register_fake
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h):
+    return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
+
+
+def _gs8_bwd(ctx, dy, _dg, _du, _dh):
+    x, w1, w2, w3, counts, g, u, h = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None, None
+    dx, dw1, dw2, dw3 = grouped_swiglu_fp8_backward(dy, x, w1, w2, w3, counts, g, u, h)
+    return dx, dw1, dw2, dw3, None
+
+
+grouped_swiglu_fp8.register_autograd(_gs8_bwd, setup_context=_gs_setup)
