@@ -16,28 +16,37 @@
 //   bwd_dw2     dw2 D x H            dy^T             h^T                   tokens
 //
 // Design (gfx950, 64-wide waves):
-//  * 256 threads = 4 waves in 2 x 2; block tile BM x BN x BK (128 x 256 x 32);
-//    wave tile 64 x 128 of v_mfma_f32_16x16x32_bf16 (fp32 accumulate); two
-//    workgroups per CU.
-//  * Two LDS stages. Stage k+1 is loaded from HBM into registers while stage k
-//    feeds the MFMAs, then stored to the other LDS buffer; one barrier per K
-//    step. The LDS tile is chunk-major (each 16-byte k-chunk of all rows is
-//    contiguous, rows XOR-permuted inside 8-row groups), which on gfx950
-//    measures free of bank conflicts for both the 16-byte fragment reads and
-//    the 16-byte tile stores; a row-major tile costs ~4 conflict cycles per read.
-//  * Operands that are contiguous along m/n in HBM (the weights in dgu/dx,
-//    the token-major activations in dW) are transposed in registers while
-//    staging: each thread loads KB k-rows of 8 contiguous elements and writes
-//    8 LDS rows of KB elements.
+//  * 256 threads = 4 waves in 2 x 2; block tile 128 x 256 x 32; wave tile
+//    64 x 128 of v_mfma_f32_16x16x32_bf16 (fp32 accumulate); two workgroups
+//    per CU (two waves per SIMD hide each other's LDS latency).
+//  * Operands go HBM/L2 -> LDS with direct-to-LDS copies
+//    (global_load_lds_dwordx4: each wave instruction fills 1 KB of LDS), so no
+//    VGPRs stage the tiles and no ds_write is issued. Two LDS stages: the copy
+//    of stage k+1 is in flight while stage k feeds the MFMAs; one barrier per
+//    k-step. The copies are issued as inline asm and waited for with explicit
+//    vmcnt, so the compiler neither serialises them against the LDS reads nor
+//    adds waits of its own.
+//  * LDS layouts, both conflict-free for their fragment reads (measured on
+//    gfx950, where a 16-byte read is served 8 lanes = 128 bytes at a time):
+//      - K-contiguous operands: row-major 64-byte rows, 16-byte chunk kc of
+//        row r at chunk kc ^ ((r >> 1) & 3); a copy instruction fills 16 rows,
+//        four lanes per row (coalesced);
+//      - M/N-contiguous operands (transposed weights, the dW operands):
+//        k-major rows, 16-byte chunk c of k-row k at c ^ kswz(k); fragments
+//        come from pairs of ds_read_b64_tr_b16 transposing reads.
 //  * Persistent grid. Each workgroup derives the expert segments and
 //    per-expert tile counts from num_tokens_per_expert in LDS (atomics-free
 //    scan), so empty and heavily loaded experts need no host sync and no
 //    padding. Workgroup ids are remapped so each XCD works on a contiguous
-//    window of tiles (neighbouring tiles share an operand in its L2).
+//    window of tiles (neighbouring tiles share an operand in its L2). In the
+//    last m-tile of an expert, waves skip the MFMAs of 16-row blocks that hold
+//    no routed rows.
 //  * The K loop runs in ascending k in steps of 32 and each output element is
 //    rounded to bf16 once, at the points the reference's bf16 autograd rounds;
 //    the outputs are bit-identical to torch._grouped_mm and its autograd on
 //    this GPU.
+#include <type_traits>
+
 #include "common.h"
 
 namespace moe {
@@ -81,16 +90,6 @@ struct GemmParams {
   uint16_t* out_dw3;
 };
 
-// LDS tile layout (measured conflict-free on gfx950 for 16-byte fragment reads
-// of 16 consecutive rows and for 16-byte tile stores of 4 lanes per row):
-// chunk-major, i.e. the 16-byte k-chunk kc of all ROWS rows is contiguous,
-// with rows permuted inside each 8-row group by an XOR of the chunk index and
-// the group index. Returns the element offset of (row r, chunk kc).
-template <int ROWS>
-__device__ __forceinline__ int lds_off(int r, int kc) {
-  return (kc * ROWS + (r ^ (((2 * kc) ^ (r >> 3)) & 7))) * 8;
-}
-
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
 template <int MODE>
@@ -108,36 +107,61 @@ __device__ __forceinline__ const uint16_t* gate_up_row(const GemmParams& p, int6
   return ((blk & 1) ? p.w3 : p.w1) + (e * p.H + hc) * (int64_t)p.D;
 }
 
-template <int MODE, int BM, int BN, int BK, int STAGES, int OCC, bool PD>
-__global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams p) {
-  using T = ModeTraits<MODE>;
-  // PD: the K-contiguous P operand (token rows) bypasses LDS: each lane loads
-  // its MFMA fragment (16 contiguous bytes of one row) straight from HBM.
-  static_assert(!PD || (!T::kPT && BK == 32), "direct P fragments need K-contiguous P and BK = 32");
-  constexpr int CPR = BK / 8;  // 16-byte chunks per LDS row
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int TM = WM / 16, TN = WN / 16;
-  // staging shapes
-  constexpr int PK_CH = BM * BK / 8 / kThreads;  // 16-byte chunks per thread, K-contiguous P
-  constexpr int QK_CH = BN * BK / 8 / kThreads;
-  constexpr int PT_KB = BM * BK / 8 / kThreads;  // k-rows per thread, m-contiguous P (8 m each)
-  constexpr int QT_KB = BN * BK / 8 / kThreads;
-  static_assert(PK_CH >= 1 && QK_CH >= 1, "tile too small for 256 threads");
-  static_assert(!T::kPT || PT_KB == 2 || PT_KB == 4 || PT_KB == 8, "transposed P staging: 2, 4 or 8 k-rows");
-  static_assert(!T::kQT || QT_KB == 2 || QT_KB == 4 || QT_KB == 8, "transposed Q staging: 2, 4 or 8 k-rows");
-  static_assert(BK % 32 == 0 && (CPR == 4 || CPR == 8), "BK must be 32 or 64");
+#define LDSP __attribute__((address_space(3)))
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+typedef short v8s_t __attribute__((ext_vector_type(8)));
 
-  constexpr int LDS_STAGES = STAGES == 1 ? 1 : 2;
-  __shared__ __attribute__((aligned(16))) uint16_t sP[LDS_STAGES][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[LDS_STAGES][BN * BK];
+// One wave-wide direct-to-LDS copy: lane i's 16 bytes at g land at LDS byte
+// address lds + 16 i. Issued as inline asm so the compiler neither waits on it
+// before unrelated LDS reads nor reorders it; the kernel waits with vmcnt.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" :: "v"(g), "{m0}"(lds) : "memory");
+}
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T* ptr) { return (uint32_t)(size_t)((LDSP T*)ptr); }
+
+// Row-major LDS tile with 64-byte rows (32 bf16 of k): element offset of chunk kc of row r.
+__device__ __forceinline__ int rm_off(int r, int kc) { return (r * 4 + (kc ^ ((r >> 1) & 3))) * 8; }
+
+// 16-byte chunk swizzle of a k-major tile row k (rows of 16 or more chunks):
+// conflict-free for transposed fragment reads (32 lanes per LDS pass read 8 k-rows).
+__device__ __forceinline__ int kswz(int k) { return 2 * ((k & 3) | ((k >> 1) & 4)); }
+template <int ROWE>
+__device__ __forceinline__ int km_off(int k, int n) { return k * ROWE + ((((n >> 3) ^ kswz(k)) << 3) | (n & 7)); }
+
+// MFMA fragment (16 rows x 32 k, lane l: row l % 16, k 8 (l / 16) .. + 7) from a
+// K-contiguous tile (row-major 64-byte rows).
+__device__ __forceinline__ bf16x8_t frag_rm(const uint16_t* tile, int row, int lane) {
+  return *(const bf16x8_t*)(tile + rm_off(row, lane >> 4));
+}
+// the same fragment from a k-major tile of ROWE elements per k-row, with two
+// transposing reads (each lane supplies 4 consecutive rows of one k)
+template <int ROWE>
+__device__ __forceinline__ bf16x8_t frag_km(const uint16_t* tile, int row0, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const int k = 8 * g + (j >> 2), n = row0 + 4 * (j & 3);
+  const v4s_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDSP v4s_t*)(tile + km_off<ROWE>(k, n)));
+  const v4s_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDSP v4s_t*)(tile + km_off<ROWE>(k + 4, n)));
+  const v8s_t c = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8_t, c);
+}
+
+__device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a dW segment
+
+template <int MODE, bool SKIP>
+__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmParams p) {
+  using T = ModeTraits<MODE>;
+  constexpr int BM = 128, BN = 256, BK = 32;
+  constexpr int WM = 64, WN = 128, TM = 4, TN = 8;
+  __shared__ __attribute__((aligned(1024))) uint16_t sP[2][BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sQ[2][BN * BK];
   __shared__ int s_seg[kGemmMaxE + 1];
   __shared__ int s_tile[kGemmMaxE + 1];
   __shared__ int s_tmp[8];
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wv >> 1, wn = wv & 1;
   const int E = p.E, D = p.D, H = p.H;
-
   int Ntot = 0, Kfix = 0, Mfix = 0;
   if (MODE == kFwdGateUp) { Ntot = 2 * H; Kfix = D; }
   if (MODE == kFwdDown) { Ntot = D; Kfix = H; }
@@ -148,7 +172,6 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
   const int NT = Ntot / BN;
   const int MT = T::kRowGrouped ? 0 : Mfix / BM;
 
-  // ---- expert segments and tile table (LDS) ----
   {
     int cnt[4], tl[4], seg[4], tst[4];
 #pragma unroll
@@ -158,7 +181,6 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
       cnt[i] = c < 0 ? 0 : (c > p.R ? (int)p.R : (int)c);
     }
     {
-      // clamp the running segment ends to R so inconsistent counts never read past the rows
       int pre[4];
       block_exclusive_scan4(cnt, pre, s_tmp);
 #pragma unroll
@@ -178,20 +200,20 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid * 4 + i;
-      if (e < E) {
-        s_seg[e] = seg[i];
-        s_tile[e] = tst[i];
-      }
+      if (e < E) { s_seg[e] = seg[i]; s_tile[e] = tst[i]; }
     }
-    if (tid == 0) {
-      s_seg[E] = rtot;
-      s_tile[E] = ttot;
-    }
+    if (tid == 0) { s_seg[E] = rtot; s_tile[E] = ttot; }
     __syncthreads();
   }
   const int total_tiles = s_tile[E];
   const int G = gridDim.x;
   const int lb = (G % 8 == 0) ? ((int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
+  const int ml = lane & 15, nq = (lane >> 4) * 4;
+  // copy-lane maps. K-contiguous tile: one copy = 16 rows x 64 B, lane i -> row i >> 2,
+  // chunk (i & 3) ^ ((row >> 1) & 3). k-major tile: one copy = 1 KB of k-rows, lane i ->
+  // k-row i / (ROWB / 16), chunk (i % (ROWB / 16)) ^ kswz(k).
+  const int dr = lane >> 2;
+  const int dc = (lane & 3) ^ ((dr >> 1) & 3);
 
   for (int t = lb; t < total_tiles; t += G) {
     int lo = 0, hi = E - 1;
@@ -214,142 +236,87 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
     }
     const int Ktot = T::kRowGrouped ? Kfix : (seg1 - seg0);
     const int nk = (Ktot + BK - 1) / BK;
-    const int row0 = seg0 + mt * BM;  // first token row of a row-grouped tile
+    const int row0 = seg0 + mt * BM;
 
-    struct Regs {
-      uint4 p[PD ? TM : (T::kPT ? PT_KB : PK_CH)];
-      uint4 q[T::kQT ? QT_KB : QK_CH];
-    };
-    Regs ra, rb;
+    // ---- per-lane copy sources ----
+    const uint16_t* srcP[2];
+    const uint16_t* srcQ[4];
+    const uint16_t* srcQ3[4];  // dx: the w3 half of the k range
+    int64_t stepP = BK, stepQ = BK;  // element advance per k-step
+    if constexpr (!T::kPT) {
+      const uint16_t* pb;
+      int ldp;
+      if (MODE == kFwdGateUp) { pb = p.x; ldp = D; }
+      else if (MODE == kFwdDown) { pb = p.h; ldp = H; }
+      else if (MODE == kBwdDgu) { pb = p.dy; ldp = D; }
+      else { pb = p.dgu; ldp = 2 * H; }
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        int r = row0 + (wv * 2 + b) * 16 + dr;
+        r = r < (int)p.R ? r : (int)p.R - 1;  // rows past the segment are computed, never stored
+        srcP[b] = pb + (int64_t)r * ldp + dc * 8;
+      }
+    } else {
+      // dW: P = dgu^T (m over 2H) or dy^T (m over D); k-rows = the expert's tokens
+      const uint16_t* pb = (MODE == kBwdDw13) ? p.dgu : p.dy;
+      const int ldp = (MODE == kBwdDw13) ? 2 * H : D;
+      stepP = (int64_t)BK * ldp;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int kl = (wv * 2 + b) * 4 + (lane >> 4);
+        const int c = (lane & 15) ^ kswz(kl);
+        srcP[b] = pb + (int64_t)(seg0 + kl) * ldp + mt * BM + c * 8;
+      }
+    }
+    if constexpr (!T::kQT) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int n = (wv * 4 + b) * 16 + dr;
+        const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, nt, n, BN)
+                                                     : p.w2 + (e64 * D + nt * BN + n) * (int64_t)H;
+        srcQ[b] = rowp + dc * 8;
+      }
+    } else {
+      const uint16_t* qb;
+      int ldq;
+      if (MODE == kBwdDgu) { qb = p.w2 + e64 * D * (int64_t)H; ldq = H; }        // rows k of w2[e] (D x H)
+      else if (MODE == kBwdDx) { qb = p.w1 + e64 * H * (int64_t)D; ldq = D; }    // rows k of w1[e], then w3[e]
+      else if (MODE == kBwdDw13) { qb = p.x + (int64_t)seg0 * D; ldq = D; }
+      else { qb = p.h + (int64_t)seg0 * H; ldq = H; }
+      stepQ = (int64_t)BK * ldq;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int kl = (wv * 4 + b) * 2 + (lane >> 5);
+        const int c = (lane & 31) ^ kswz(kl);
+        const int64_t off = (int64_t)kl * ldq + nt * BN + c * 8;
+        srcQ[b] = qb + off;
+        if (MODE == kBwdDx) srcQ3[b] = p.w3 + e64 * H * (int64_t)D + off;
+      }
+    }
+    const int kl_p = T::kPT ? (wv * 2) * 4 + (lane >> 4) : 0;   // first k-row of this lane's P copies
+    const int kl_q = T::kQT ? (wv * 4) * 2 + (lane >> 5) : 0;
 
-    // ---- global -> registers for K step kt ----
-    auto load_stage = [&](Regs& rr, int kt) {
-      uint4* rp = rr.p;
-      uint4* rq = rr.q;
+    auto issue = [&](int kt) {
+      const int s = kt & 1;
       const int k0 = kt * BK;
-      // P
-      if constexpr (!T::kPT) {
-        const uint16_t* pb;
-        int ldp;
-        if (MODE == kFwdGateUp) { pb = p.x; ldp = D; }
-        else if (MODE == kFwdDown) { pb = p.h; ldp = H; }
-        else if (MODE == kBwdDgu) { pb = p.dy; ldp = D; }
-        else { pb = p.dgu; ldp = 2 * H; }
-        if constexpr (PD) {
 #pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            const int r = row0 + wm * WM + i * 16 + (lane & 15);
-            rp[i] = (r < seg1) ? *(const uint4*)(pb + (int64_t)r * ldp + k0 + (lane >> 4) * 8) : make_uint4(0, 0, 0, 0);
-          }
-        } else
-#pragma unroll
-        for (int i = 0; i < PK_CH; ++i) {
-          const int c = tid + i * kThreads;
-          const int m = c / CPR, kc = c % CPR;
-          const int r = row0 + m;
-          rp[i] = (r < seg1) ? *(const uint4*)(pb + (int64_t)r * ldp + k0 + kc * 8) : make_uint4(0, 0, 0, 0);
+      for (int b = 0; b < 2; ++b) {
+        const uint16_t* src = srcP[b] + kt * stepP;
+        if constexpr (T::kPT) {
+          if (seg0 + k0 + kl_p + b * 4 >= seg1) src = (const uint16_t*)kZeroRow;
         }
-      } else {
-        const uint16_t* pb = (MODE == kBwdDw13) ? p.dgu : p.dy;
-        const int ldp = (MODE == kBwdDw13) ? 2 * H : D;
-        constexpr int MB = BM / 8;
-        const int mb = tid % MB, kb = tid / MB;
-#pragma unroll
-        for (int kk = 0; kk < PT_KB; ++kk) {
-          const int r = seg0 + k0 + kb * PT_KB + kk;
-          rp[kk] = (r < seg1) ? *(const uint4*)(pb + (int64_t)r * ldp + mt * BM + mb * 8) : make_uint4(0, 0, 0, 0);
-        }
+        dma16(src, lds_addr(&sP[s][(wv * 2 + b) * 512]));
       }
-      // Q
-      if constexpr (!T::kQT) {
 #pragma unroll
-        for (int i = 0; i < QK_CH; ++i) {
-          const int c = tid + i * kThreads;
-          const int n = c / CPR, kc = c % CPR;
-          const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, nt, n, BN)
-                                                       : p.w2 + (e64 * D + nt * BN + n) * (int64_t)H;
-          rq[i] = *(const uint4*)(rowp + k0 + kc * 8);
+      for (int b = 0; b < 4; ++b) {
+        const uint16_t* src = srcQ[b] + kt * stepQ;
+        if constexpr (MODE == kBwdDx) {
+          if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * D;
         }
-      } else {
-        constexpr int NB = BN / 8;
-        const int nb = tid % NB, kb = tid / NB;
-#pragma unroll
-        for (int kk = 0; kk < QT_KB; ++kk) {
-          const int k = k0 + kb * QT_KB + kk;
-          const uint16_t* src;
-          bool ok = true;
-          if (MODE == kBwdDgu) {
-            src = p.w2 + (e64 * D + k) * (int64_t)H;
-          } else if (MODE == kBwdDx) {
-            src = (k < H) ? p.w1 + (e64 * H + k) * (int64_t)D : p.w3 + (e64 * H + (k - H)) * (int64_t)D;
-          } else {
-            const int r = seg0 + k;
-            ok = r < seg1;
-            src = (MODE == kBwdDw13) ? p.x + (int64_t)r * D : p.h + (int64_t)r * H;
-          }
-          rq[kk] = ok ? *(const uint4*)(src + nt * BN + nb * 8) : make_uint4(0, 0, 0, 0);
+        if constexpr (MODE >= kBwdDw13) {
+          if (seg0 + k0 + kl_q + b * 2 >= seg1) src = (const uint16_t*)kZeroRow;
         }
-      }
-    };
-
-    // ---- registers -> LDS stage s ----
-    auto store_stage = [&](const Regs& rr, int s) {
-      const uint4* rp = rr.p;
-      const uint4* rq = rr.q;
-      uint16_t* dP = sP[s];
-      uint16_t* dQ = sQ[s];
-      if constexpr (PD) {
-      } else if constexpr (!T::kPT) {
-#pragma unroll
-        for (int i = 0; i < PK_CH; ++i) {
-          const int c = tid + i * kThreads;
-          const int m = c / CPR, kc = c % CPR;
-          *(uint4*)(dP + lds_off<BM>(m, kc)) = rp[i];
-        }
-      } else {
-        constexpr int MB = BM / 8;
-        const int mb = tid % MB, kb = tid / MB;
-        const int kl = kb * PT_KB;  // first k of this thread's rows
-#pragma unroll
-        for (int mm = 0; mm < 8; ++mm) {
-          const int m = mb * 8 + mm;
-          uint32_t o[PT_KB / 2];
-#pragma unroll
-          for (int j = 0; j < PT_KB / 2; ++j) {
-            const uint32_t a = (&rp[2 * j].x)[mm >> 1], b = (&rp[2 * j + 1].x)[mm >> 1];
-            o[j] = (mm & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-          }
-          uint16_t* dst = dP + lds_off<BM>(m, kl >> 3) + (kl & 7);
-          if constexpr (PT_KB == 8) *(uint4*)dst = make_uint4(o[0], o[1 % (PT_KB / 2)], o[2 % (PT_KB / 2)], o[3 % (PT_KB / 2)]);
-          else if constexpr (PT_KB == 4) *(uint2*)dst = make_uint2(o[0], o[1 % (PT_KB / 2)]);
-          else *(uint32_t*)dst = o[0];
-        }
-      }
-      if constexpr (!T::kQT) {
-#pragma unroll
-        for (int i = 0; i < QK_CH; ++i) {
-          const int c = tid + i * kThreads;
-          const int n = c / CPR, kc = c % CPR;
-          *(uint4*)(dQ + lds_off<BN>(n, kc)) = rq[i];
-        }
-      } else {
-        constexpr int NB = BN / 8;
-        const int nb = tid % NB, kb = tid / NB;
-        const int kl = kb * QT_KB;
-#pragma unroll
-        for (int nn = 0; nn < 8; ++nn) {
-          const int n = nb * 8 + nn;
-          uint32_t o[QT_KB / 2];
-#pragma unroll
-          for (int j = 0; j < QT_KB / 2; ++j) {
-            const uint32_t a = (&rq[2 * j].x)[nn >> 1], b = (&rq[2 * j + 1].x)[nn >> 1];
-            o[j] = (nn & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-          }
-          uint16_t* dst = dQ + lds_off<BN>(n, kl >> 3) + (kl & 7);
-          if constexpr (QT_KB == 8) *(uint4*)dst = make_uint4(o[0], o[1 % (QT_KB / 2)], o[2 % (QT_KB / 2)], o[3 % (QT_KB / 2)]);
-          else if constexpr (QT_KB == 4) *(uint2*)dst = make_uint2(o[0], o[1 % (QT_KB / 2)]);
-          else *(uint32_t*)dst = o[0];
-        }
+        dma16(src, lds_addr(&sQ[s][(wv * 4 + b) * 512]));
       }
     };
 
@@ -358,11 +325,7 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    const int ml = lane & 15, nq = (lane >> 4) * 4;
-    // dx = dg.w1 + du.w3: the reference's autograd forms the two products as
-    // separate bf16 GEMM outputs and adds them in bf16. The w1 half is rounded
-    // and parked in the output rows (read back by the same lanes at the end).
+    const int tmv = T::kRowGrouped ? min(TM, max(0, (seg1 - (row0 + wm * WM) + 15) >> 4)) : TM;
     const int kt_half = (MODE == kBwdDx) ? H / BK : -1;
 
     auto park_dx_half = [&]() {
@@ -381,88 +344,42 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
       }
     };
 
-    auto compute_stage = [&](int s, const Regs& cur) {
-      const uint16_t* cP = sP[s];
-      const uint16_t* cQ = sQ[s];
-#pragma unroll
-      for (int ks = 0; ks < BK / 32; ++ks) {
-        const int kc = ks * 4 + (lane >> 4);
+    auto run = [&](auto full) {
+      auto compute = [&](int s) {
+        const uint16_t* cP = sP[s];
+        const uint16_t* cQ = sQ[s];
         bf16x8_t af[TM];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-          const int m = wm * WM + i * 16 + ml;
-          if constexpr (PD) af[i] = __builtin_bit_cast(bf16x8_t, cur.p[i]);
-          else af[i] = *(const bf16x8_t*)(cP + lds_off<BM>(m, kc));
+          if (!decltype(full)::value && i >= tmv) continue;
+          if constexpr (T::kPT) af[i] = frag_km<BM>(cP, wm * WM + i * 16, lane);
+          else af[i] = frag_rm(cP, wm * WM + i * 16 + ml, lane);
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const int n = wn * WN + j * 16 + ml;
-          const bf16x8_t bq = *(const bf16x8_t*)(cQ + lds_off<BN>(n, kc));
+          bf16x8_t bq;
+          if constexpr (T::kQT) bq = frag_km<BN>(cQ, wn * WN + j * 16, lane);
+          else bq = frag_rm(cQ, wn * WN + j * 16 + ml, lane);
 #pragma unroll
-          for (int i = 0; i < TM; ++i)
+          for (int i = 0; i < TM; ++i) {
+            if (!decltype(full)::value && i >= tmv) continue;
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq, af[i], acc[i][j], 0, 0, 0);
+          }
         }
+      };
+      // the previous tile's LDS reads are done in every wave
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (nk > 0) issue(0);
+      for (int kt = 0; kt < nk; ++kt) {
+        // stage kt has landed in every wave; the reads of the other buffer are retired
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + 1 < nk) issue(kt + 1);
+        if (MODE == kBwdDx && kt == kt_half) park_dx_half();
+        if (decltype(full)::value || tmv > 0) compute(kt & 1);
       }
     };
-
-    if constexpr (STAGES == 3) {
-      // two LDS stages and two register sets: stage kt+2 is in flight to
-      // registers while stage kt feeds the MFMAs and stage kt+1 (loaded one
-      // step earlier) is stored to the other LDS buffer; one barrier per step
-      __syncthreads();  // the previous tile's last stage reads are done
-      if (nk > 0) {
-        load_stage(ra, 0);
-        store_stage(ra, 0);
-      }
-      if (nk > 1) load_stage(ra, 1);
-      __syncthreads();
-      for (int kt = 0; kt < nk; kt += 2) {
-        if (kt + 2 < nk) load_stage(rb, kt + 2);
-        if (MODE == kBwdDx && kt == kt_half) park_dx_half();
-        compute_stage(0, ra);
-        if (kt + 1 < nk) store_stage(ra, 1);
-        __syncthreads();
-        if (kt + 1 >= nk) break;
-        if (kt + 3 < nk) load_stage(ra, kt + 3);
-        if (MODE == kBwdDx && kt + 1 == kt_half) park_dx_half();
-        compute_stage(1, rb);
-        if (kt + 2 < nk) store_stage(rb, 0);
-        __syncthreads();
-      }
-    } else if constexpr (STAGES == 2) {
-      // two LDS stages: stage kt+1 is loaded to registers during the MFMAs of
-      // stage kt and stored to the other buffer; one barrier per K step
-      __syncthreads();  // the previous tile's last stage reads are done
-      if (nk > 0) {
-        load_stage(ra, 0);
-        store_stage(ra, 0);
-      }
-      __syncthreads();
-      for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) load_stage(rb, kt + 1);
-        if (MODE == kBwdDx && kt == kt_half) park_dx_half();
-        compute_stage(cur, ra);
-        if (kt + 1 < nk) store_stage(rb, cur ^ 1);
-        if constexpr (PD) {
-#pragma unroll
-          for (int i = 0; i < TM; ++i) ra.p[i] = rb.p[i];
-        }
-        __syncthreads();
-      }
-    } else {
-      // one LDS stage shared by two resident workgroups per CU: stage kt+1 is
-      // loaded to registers during the MFMAs of stage kt
-      if (nk > 0) load_stage(ra, 0);
-      for (int kt = 0; kt < nk; ++kt) {
-        __syncthreads();
-        store_stage(ra, 0);
-        __syncthreads();
-        if (kt + 1 < nk) load_stage(ra, kt + 1);
-        if (MODE == kBwdDx && kt == kt_half) park_dx_half();
-        compute_stage(0, ra);
-      }
-    }
+    if (!SKIP || tmv == TM) run(std::true_type{});
+    else run(std::false_type{});
 
     // ---- epilogue: lane holds C[m = .. + ml][n = .. + nq + 0..3] ----
     if (MODE == kFwdGateUp) {
@@ -526,11 +443,11 @@ __global__ __launch_bounds__(kThreads, OCC) void grouped_gemm_kernel(GemmParams 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const float dh = round_bf(acc[i][j][q]);
-              const float sl = round_bf(silu_f(gv[q]));         // saved silu(g) (bf16)
-              const float dsl = round_bf(dh * uv[q]);           // d silu(g)
-              du[q] = dh * sl;                                  // d u
+              const float sl = round_bf(silu_f(gv[q]));
+              const float dsl = round_bf(dh * uv[q]);
+              du[q] = dh * sl;
               const float sg = 1.0f / (1.0f + expf(-gv[q]));
-              dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));  // silu backward
+              dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
             }
             const int64_t o2 = (int64_t)r * (2 * H) + hh;
             *(uint2*)(p.out_dgu + o2) = make_uint2(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]));
@@ -574,10 +491,6 @@ static int cu_count() {
   return g_cu_count[dev];
 }
 
-// Tile shape per mode (BM x BN x BK, LDS stages). D and H are multiples of 256
-// (check_gemm_shape), so every BM and BN here divides the fixed dimensions.
-template <int MODE> struct Tile { static constexpr int BM = 128, BN = 256, BK = 32, STAGES = 2, OCC = 2; };
-
 static int persistent_grid(int64_t max_tiles, int per_cu) {
   int64_t g = (int64_t)cu_count() * per_cu;
   if (g > max_tiles) g = max_tiles;
@@ -585,22 +498,20 @@ static int persistent_grid(int64_t max_tiles, int per_cu) {
   return (int)(g < 1 ? 1 : g);
 }
 
-template <int MODE, int BM, int BN, int BK, int ST, int OCC, bool PD>
-static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
+// Tile 128 x 256 (D and H are multiples of 256: check_gemm_shape). The tail
+// skip is compiled into the row-grouped modes except dx, where the second copy
+// of its K loop costs more registers than the skip saves.
+template <int MODE>
+static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
+  constexpr int BM = 128, BN = 256;
   int64_t max_tiles;
   if (MODE == kFwdGateUp) max_tiles = (R / BM + p.E) * (2 * p.H / BN);
   else if (MODE == kFwdDown || MODE == kBwdDx) max_tiles = (R / BM + p.E) * (p.D / BN);
   else if (MODE == kBwdDgu) max_tiles = (R / BM + p.E) * (p.H / BN);
   else if (MODE == kBwdDw13) max_tiles = (int64_t)p.E * (2 * p.H / BM) * (p.D / BN);
   else max_tiles = (int64_t)p.E * (p.D / BM) * (p.H / BN);
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, BM, BN, BK, ST, OCC, PD>), dim3(persistent_grid(max_tiles, OCC)),
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, (MODE <= kBwdDgu)>), dim3(persistent_grid(max_tiles, 2)),
                      dim3(kThreads), 0, stream, p);
-}
-
-template <int MODE>
-static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
-  using C = Tile<MODE>;
-  launch_cfg<MODE, C::BM, C::BN, C::BK, C::STAGES, C::OCC, false>(p, R, stream);
 }
 
 static int check_gemm_shape(int64_t R, int32_t E, int32_t D, int32_t H) {
