@@ -16,16 +16,20 @@
 //   bwd_dw2     dw2 D x H            dy^T             h^T                   tokens
 //
 // Design (gfx950, 64-wide waves):
-//  * 256 threads = 4 waves in 2 x 2; block tile 128 x 256 x 32; wave tile
-//    64 x 128 of v_mfma_f32_16x16x32_bf16 (fp32 accumulate); two workgroups
-//    per CU (two waves per SIMD hide each other's LDS latency).
+//  * Wave tiles of 64 x 128 (or 64 x 96) of v_mfma_f32_16x16x32_bf16 (fp32
+//    accumulate), two waves per SIMD so each hides the other's LDS latency:
+//    forward modes 4 waves / 128 x 256 block / two workgroups per CU, backward
+//    modes 8 waves / 128 x 512, 128 x 384 or 256 x 256 block / one workgroup
+//    per CU (wider blocks copy fewer bytes per flop). k-step 32.
 //  * Operands go HBM/L2 -> LDS with direct-to-LDS copies
 //    (global_load_lds_dwordx4: each wave instruction fills 1 KB of LDS), so no
-//    VGPRs stage the tiles and no ds_write is issued. Two LDS stages: the copy
-//    of stage k+1 is in flight while stage k feeds the MFMAs; one barrier per
-//    k-step. The copies are issued as inline asm and waited for with explicit
-//    vmcnt, so the compiler neither serialises them against the LDS reads nor
-//    adds waits of its own.
+//    VGPRs stage the tiles and no ds_write is issued. Two or three LDS stages:
+//    the copies of the next stages are in flight while stage k feeds the
+//    MFMAs; one barrier per k-step. The copies are issued as inline asm and
+//    waited for with explicit vmcnt, so the compiler neither serialises them
+//    against the LDS reads nor adds waits of its own. Measured: the kernels
+//    are bound by the latency of these copies (HBM and L2 round trips), not
+//    by LDS or MFMA throughput.
 //  * LDS layouts, both conflict-free for their fragment reads (measured on
 //    gfx950, where a 16-byte read is served 8 lanes = 128 bytes at a time):
 //      - K-contiguous operands: row-major 64-byte rows, 16-byte chunk kc of
@@ -55,7 +59,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmMaxE = 1024;
-constexpr int kThreads = 256;
 
 enum GemmMode : int {
   kFwdGateUp = 0,
@@ -148,19 +151,25 @@ __device__ __forceinline__ bf16x8_t frag_km(const uint16_t* tile, int row0, int 
 
 __device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a dW segment
 
-template <int MODE, bool SKIP>
-__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmParams p) {
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p) {
   using T = ModeTraits<MODE>;
-  constexpr int BM = 128, BN = 256, BK = 32;
-  constexpr int WM = 64, WN = 128, TM = 4, TN = 8;
-  __shared__ __attribute__((aligned(1024))) uint16_t sP[2][BM * BK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sQ[2][BN * BK];
+  constexpr int WGN = NW / WGM;
+  constexpr int WM = TM * 16, WN = TN * 16;
+  constexpr int BM = WGM * WM, BN = WGN * WN, BK = 32;
+  constexpr int CPW_P = BM / 16 / NW, CPW_Q = BN / 16 / NW;  // 1 KB copies per wave and stage
+  static_assert(CPW_P * 16 * NW == BM && CPW_Q * 16 * NW == BN, "copies per wave");
+  constexpr int CPW = CPW_P + CPW_Q;
+  constexpr int CHP = BM / 8, CHQ = BN / 8;          // 16-byte chunks per k-row (k-major tiles)
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && CPW <= 30, "tile");
+  __shared__ __attribute__((aligned(1024))) uint16_t sP[NS][BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sQ[NS][BN * BK];
   __shared__ int s_seg[kGemmMaxE + 1];
   __shared__ int s_tile[kGemmMaxE + 1];
   __shared__ int s_tmp[8];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv / WGN, wn = wv % WGN;
   const int E = p.E, D = p.D, H = p.H;
   int Ntot = 0, Kfix = 0, Mfix = 0;
   if (MODE == kFwdGateUp) { Ntot = 2 * H; Kfix = D; }
@@ -238,10 +247,11 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmParams p)
     const int nk = (Ktot + BK - 1) / BK;
     const int row0 = seg0 + mt * BM;
 
-    // ---- per-lane copy sources ----
-    const uint16_t* srcP[2];
-    const uint16_t* srcQ[4];
-    const uint16_t* srcQ3[4];  // dx: the w3 half of the k range
+    // ---- per-lane copy sources (copy c of this wave covers LDS bytes [1 KB (wv CPW_X + c), +1 KB)) ----
+    const uint16_t* srcP[CPW_P];
+    const uint16_t* srcQ[CPW_Q];
+    const uint16_t* srcQ3[CPW_Q];  // dx: the w3 half of the k range
+    int klP[CPW_P], klQ[CPW_Q];    // k-major copies: the k-row this lane fills
     int64_t stepP = BK, stepQ = BK;  // element advance per k-step
     if constexpr (!T::kPT) {
       const uint16_t* pb;
@@ -251,30 +261,33 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmParams p)
       else if (MODE == kBwdDgu) { pb = p.dy; ldp = D; }
       else { pb = p.dgu; ldp = 2 * H; }
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        int r = row0 + (wv * 2 + b) * 16 + dr;
+      for (int b = 0; b < CPW_P; ++b) {
+        int r = row0 + (wv * CPW_P + b) * 16 + dr;
         r = r < (int)p.R ? r : (int)p.R - 1;  // rows past the segment are computed, never stored
         srcP[b] = pb + (int64_t)r * ldp + dc * 8;
+        klP[b] = 0;
       }
     } else {
-      // dW: P = dgu^T (m over 2H) or dy^T (m over D); k-rows = the expert's tokens
       const uint16_t* pb = (MODE == kBwdDw13) ? p.dgu : p.dy;
       const int ldp = (MODE == kBwdDw13) ? 2 * H : D;
       stepP = (int64_t)BK * ldp;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int kl = (wv * 2 + b) * 4 + (lane >> 4);
-        const int c = (lane & 15) ^ kswz(kl);
+      for (int b = 0; b < CPW_P; ++b) {
+        const int slot = (wv * CPW_P + b) * 64 + lane;
+        const int kl = slot / CHP;
+        const int c = (slot % CHP) ^ kswz(kl);
         srcP[b] = pb + (int64_t)(seg0 + kl) * ldp + mt * BM + c * 8;
+        klP[b] = kl;
       }
     }
     if constexpr (!T::kQT) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int n = (wv * 4 + b) * 16 + dr;
+      for (int b = 0; b < CPW_Q; ++b) {
+        const int n = (wv * CPW_Q + b) * 16 + dr;
         const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, nt, n, BN)
                                                      : p.w2 + (e64 * D + nt * BN + n) * (int64_t)H;
         srcQ[b] = rowp + dc * 8;
+        klQ[b] = 0;
       }
     } else {
       const uint16_t* qb;
@@ -285,38 +298,38 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmParams p)
       else { qb = p.h + (int64_t)seg0 * H; ldq = H; }
       stepQ = (int64_t)BK * ldq;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int kl = (wv * 4 + b) * 2 + (lane >> 5);
-        const int c = (lane & 31) ^ kswz(kl);
+      for (int b = 0; b < CPW_Q; ++b) {
+        const int slot = (wv * CPW_Q + b) * 64 + lane;
+        const int kl = slot / CHQ;
+        const int c = (slot % CHQ) ^ kswz(kl);
         const int64_t off = (int64_t)kl * ldq + nt * BN + c * 8;
         srcQ[b] = qb + off;
         if (MODE == kBwdDx) srcQ3[b] = p.w3 + e64 * H * (int64_t)D + off;
+        klQ[b] = kl;
       }
     }
-    const int kl_p = T::kPT ? (wv * 2) * 4 + (lane >> 4) : 0;   // first k-row of this lane's P copies
-    const int kl_q = T::kQT ? (wv * 4) * 2 + (lane >> 5) : 0;
 
     auto issue = [&](int kt) {
-      const int s = kt & 1;
+      const int s = kt % NS;
       const int k0 = kt * BK;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < CPW_P; ++b) {
         const uint16_t* src = srcP[b] + kt * stepP;
         if constexpr (T::kPT) {
-          if (seg0 + k0 + kl_p + b * 4 >= seg1) src = (const uint16_t*)kZeroRow;
+          if (seg0 + k0 + klP[b] >= seg1) src = (const uint16_t*)kZeroRow;
         }
-        dma16(src, lds_addr(&sP[s][(wv * 2 + b) * 512]));
+        dma16(src, lds_addr(&sP[s][(wv * CPW_P + b) * 512]));
       }
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < CPW_Q; ++b) {
         const uint16_t* src = srcQ[b] + kt * stepQ;
         if constexpr (MODE == kBwdDx) {
           if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * D;
         }
         if constexpr (MODE >= kBwdDw13) {
-          if (seg0 + k0 + kl_q + b * 2 >= seg1) src = (const uint16_t*)kZeroRow;
+          if (seg0 + k0 + klQ[b] >= seg1) src = (const uint16_t*)kZeroRow;
         }
-        dma16(src, lds_addr(&sQ[s][(wv * 4 + b) * 512]));
+        dma16(src, lds_addr(&sQ[s][(wv * CPW_Q + b) * 512]));
       }
     };
 
@@ -369,13 +382,17 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmParams p)
       };
       // the previous tile's LDS reads are done in every wave
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (nk > 0) issue(0);
+#pragma unroll
+      for (int i = 0; i < NS - 1; ++i)
+        if (i < nk) issue(i);
       for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed in every wave; the reads of the other buffer are retired
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (kt + 1 < nk) issue(kt + 1);
+        // stage kt has landed in every wave once at most the later stages' copies are
+        // outstanding; the barrier also retires every wave's reads of the buffer refilled next
+        if (NS == 3 && kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(CPW) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + NS - 1 < nk) issue(kt + NS - 1);
         if (MODE == kBwdDx && kt == kt_half) park_dx_half();
-        if (decltype(full)::value || tmv > 0) compute(kt & 1);
+        if (decltype(full)::value || tmv > 0) compute(kt % NS);
       }
     };
     if (!SKIP || tmv == TM) run(std::true_type{});
@@ -498,20 +515,43 @@ static int persistent_grid(int64_t max_tiles, int per_cu) {
   return (int)(g < 1 ? 1 : g);
 }
 
-// Tile 128 x 256 (D and H are multiples of 256: check_gemm_shape). The tail
-// skip is compiled into the row-grouped modes except dx, where the second copy
-// of its K loop costs more registers than the skip saves.
-template <int MODE>
-static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
-  constexpr int BM = 128, BN = 256;
+// One launch of grouped_gemm_kernel with NW waves in WGM x (NW / WGM), wave
+// tiles (16 TM) x (16 TN), NS LDS stages and OCC workgroups per CU.
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC>
+static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
+  constexpr int BM = WGM * TM * 16, BN = (NW / WGM) * TN * 16;
   int64_t max_tiles;
   if (MODE == kFwdGateUp) max_tiles = (R / BM + p.E) * (2 * p.H / BN);
   else if (MODE == kFwdDown || MODE == kBwdDx) max_tiles = (R / BM + p.E) * (p.D / BN);
   else if (MODE == kBwdDgu) max_tiles = (R / BM + p.E) * (p.H / BN);
   else if (MODE == kBwdDw13) max_tiles = (int64_t)p.E * (2 * p.H / BM) * (p.D / BN);
   else max_tiles = (int64_t)p.E * (p.D / BM) * (p.H / BN);
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, (MODE <= kBwdDgu)>), dim3(persistent_grid(max_tiles, 2)),
-                     dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC>), dim3(persistent_grid(max_tiles, OCC)),
+                     dim3(NW * 64), 0, stream, p);
+}
+
+// Tile per mode (measured at the Kimi and DSv3 shapes). The forward modes run
+// 128 x 256 tiles, four waves, two workgroups per CU. The backward modes run
+// one eight-wave workgroup per CU with three LDS stages and wider tiles, which
+// halves the copy traffic per flop of the dW operands: 128 x 512 (dgu, and dx
+// when D is a multiple of 512), 128 x 384 (dx, D a multiple of 384), 256 x 256
+// (dW). D and H are multiples of 256 (check_gemm_shape). The tail skip is
+// compiled into the row-grouped modes except dx, whose second copy of the K
+// loop costs more registers than the skip saves.
+template <int MODE>
+static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
+  if constexpr (MODE == kFwdGateUp || MODE == kFwdDown) {
+    launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2>(p, R, stream);
+  } else if constexpr (MODE == kBwdDgu) {
+    if (p.H % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, true, 1>(p, R, stream);
+    else launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2>(p, R, stream);
+  } else if constexpr (MODE == kBwdDx) {
+    if (p.D % 384 == 0) launch_cfg<MODE, 8, 2, 4, 6, 3, false, 1>(p, R, stream);
+    else if (p.D % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, false, 1>(p, R, stream);
+    else launch_cfg<MODE, 4, 2, 4, 8, 2, false, 2>(p, R, stream);
+  } else {
+    launch_cfg<MODE, 8, 4, 4, 8, 3, false, 1>(p, R, stream);
+  }
 }
 
 static int check_gemm_shape(int64_t R, int32_t E, int32_t D, int32_t H) {
