@@ -149,7 +149,7 @@ __device__ __forceinline__ bf16x8_t frag_km(const uint16_t* tile, int row0, int 
   return __builtin_bit_cast(bf16x8_t, c);
 }
 
-__device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a dW segment
+__device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a segment
 
 template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p) {
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     const uint16_t* srcP[CPW_P];
     const uint16_t* srcQ[CPW_Q];
     const uint16_t* srcQ3[CPW_Q];  // dx: the w3 half of the k range
-    int klP[CPW_P], klQ[CPW_Q];    // k-major copies: the k-row this lane fills
+    int klP[CPW_P], klQ[CPW_Q];    // k-major copies: the k-row this lane fills (P rows: the token row)
     int64_t stepP = BK, stepQ = BK;  // element advance per k-step
     if constexpr (!T::kPT) {
       const uint16_t* pb;
@@ -262,10 +262,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       else { pb = p.dgu; ldp = 2 * H; }
 #pragma unroll
       for (int b = 0; b < CPW_P; ++b) {
-        int r = row0 + (wv * CPW_P + b) * 16 + dr;
-        r = r < (int)p.R ? r : (int)p.R - 1;  // rows past the segment are computed, never stored
+        const int r = row0 + (wv * CPW_P + b) * 16 + dr;
         srcP[b] = pb + (int64_t)r * ldp + dc * 8;
-        klP[b] = 0;
+        klP[b] = r;  // rows past the segment copy the zero row
       }
     } else {
       const uint16_t* pb = (MODE == kBwdDw13) ? p.dgu : p.dy;
@@ -317,6 +316,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const uint16_t* src = srcP[b] + kt * stepP;
         if constexpr (T::kPT) {
           if (seg0 + k0 + klP[b] >= seg1) src = (const uint16_t*)kZeroRow;
+        } else {
+          if (klP[b] >= seg1) src = (const uint16_t*)kZeroRow;
         }
         dma16(src, lds_addr(&sP[s][(wv * CPW_P + b) * 512]));
       }

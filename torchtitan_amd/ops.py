@@ -118,6 +118,7 @@ def _router_setup(ctx, inputs, output):
     ctx.save_for_backward(scores, idx)
     ctx.cfg = (score_func, route_norm, route_scale)
     ctx.mark_non_differentiable(idx, counts, scores)
+    ctx.set_materialize_grads(False)  # no zero-filled grads for the index / saved outputs
 
 
 def _router_bwd(ctx, g_top, _g_idx, _g_counts, _g_scores):
@@ -198,6 +199,7 @@ def _reorder_setup(ctx, inputs, output):
     _ss, token_idx, counts, offsets, slot_pos, tok_pos = output
     ctx.save_for_backward(slot_pos)
     ctx.mark_non_differentiable(token_idx, counts, offsets, slot_pos, tok_pos)
+    ctx.set_materialize_grads(False)  # no zero-filled grads for the index / saved outputs
 
 
 def _reorder_bwd(ctx, g_sorted, *_ignored):
@@ -344,6 +346,7 @@ def _gs_setup(ctx, inputs, output):
     _y, g, u, h = output
     ctx.save_for_backward(x, w1, w2, w3, counts, g, u, h)
     ctx.mark_non_differentiable(g, u, h)
+    ctx.set_materialize_grads(False)  # no zero-filled grads for the index / saved outputs
 
 
 def _gs_bwd(ctx, dy, _dg, _du, _dh):
