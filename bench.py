@@ -196,6 +196,24 @@ def cpu_baseline(moe, w: dict, x: torch.Tensor, g: torch.Tensor, n_tokens: int) 
     }
 
 
+TRAFFIC_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def measured_traffic(workload: str, entry: str) -> int | None:
+    """HBM bytes per launch of `entry` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (profiles/hbm_traffic_<workload>.txt, already
+    scaled by the copy-kernel calibration), or None when that workload was not profiled."""
+    path = os.path.join(TRAFFIC_DIR, f"hbm_traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if parts and not line.startswith("#") and parts[0] == entry and len(parts) == 5:
+                return int(parts[4])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,6 +309,7 @@ def main() -> int:
         "frac": dk["frac"],
         "traffic": None,
     }
+    roofline["traffic"] = measured_traffic(args.workload, dom)
     mover = ("moe_permute", "moe_combine", "moe_combine_bwd", "moe_permute_bwd")
     mover_ms = sum(kernels[m]["avg_ms"] for m in mover if m in kernels)
     mover_bytes = sum(kernel_work(m, w)[1] for m in mover if m in kernels)
