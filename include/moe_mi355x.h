@@ -242,6 +242,44 @@ int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const uint8_t* 
                          const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
                          int32_t dim, int32_t hidden, uint16_t* dw2, moe_stream_t stream);
 
+/* ---- auxiliary-loss-free load balancing (optimizer step pre-hook) ---- */
+
+/* For every MoE layer l < n_layers (<= 64), with t = tokens_per_expert[l]
+ * ([E] fp32, integer-valued; floor(t / 2) first when halve[l], the blocks that
+ * recompute their forward): expert_bias[l] += d - mean(d) with
+ * d = coeff[l] * sign(mean(t) - t); then tokens_per_expert[l] = 0.
+ * tokens_per_expert, expert_bias, coeff and halve are HOST arrays (the first
+ * two of device pointers). E <= 1024. One launch for all layers.
+ * Replaces _update_expert_bias of register_moe_load_balancing_hook,
+ * torchtitan/components/optimizer.py:366-437 (the count all-reduce at
+ * :400-414 belongs to the caller). */
+int moe_expert_bias_update(float* const* tokens_per_expert, float* const* expert_bias, const float* coeff,
+                           const int32_t* halve, int32_t n_layers, int32_t n_experts, moe_stream_t stream);
+
+/* ---- expert parallelism: rank-major -> expert-major local permute ---- */
+
+/* tokens_per_expert_group [num_ranks * experts_per_rank] int64 (rank-major)
+ * -> permuted_indices [total] int64: output row p of the expert-major layout
+ * reads input row permuted_indices[p]; num_tokens_per_expert [experts_per_rank]
+ * int64 (nullable) = the counts summed over ranks. total is the number of
+ * received rows (the sum of the counts, known to the caller from the
+ * all-to-all splits); positions past that sum get -1.
+ * num_ranks * experts_per_rank <= 2048.
+ * Replaces _generate_permute_indices, torchtitan/distributed/expert_parallel.py:26-67. */
+int moe_ep_permute_indices(const int64_t* tokens_per_expert_group, int32_t experts_per_rank, int32_t num_ranks,
+                           int64_t total, int64_t* permuted_indices, int64_t* num_tokens_per_expert,
+                           moe_stream_t stream);
+/* dst[i, :] = src[idx[i], :] for i < n_rows (rows with idx < 0 or >= n_src_rows
+ * are skipped); rows of `dim` elements of `dtype` (MOE_DTYPE_*), 16-byte
+ * multiples. Replaces x[permuted_indices, :] of _permute, expert_parallel.py:70-74. */
+int moe_gather_rows(const void* src, int64_t n_src_rows, const int64_t* idx, int64_t n_rows, int32_t dim,
+                    int32_t dtype, void* dst, moe_stream_t stream);
+/* dst[idx[i], :] = src[i, :] (idx a permutation; rows with idx outside
+ * [0, n_dst_rows) are skipped). Replaces out_unpermuted[permuted_indices, :] = out
+ * of _unpermute, expert_parallel.py:77-80. */
+int moe_scatter_rows(const void* src, const int64_t* idx, int64_t n_rows, int32_t dim, int32_t dtype, void* dst,
+                     int64_t n_dst_rows, moe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -190,6 +190,20 @@ def generate_permute_indices(tokens_per_expert_group, experts_per_rank: int, num
     return out, mat.sum(axis=0)
 
 
+def expert_bias_update(tokens_per_expert, expert_bias, coeffs, halve) -> None:
+    """_update_expert_bias, torchtitan/components/optimizer.py:386-431, per layer
+    with the same torch ops: t = tokens_per_expert (// 2 for recomputing blocks),
+    delta = coeff * sign(mean(t) - t), delta -= mean(delta), expert_bias += delta,
+    tokens_per_expert = 0. Updates the tensors in place."""
+    with torch.no_grad():
+        for t, b, c, hv in zip(tokens_per_expert, expert_bias, coeffs, halve):
+            tt = (t // 2 if hv else t).float()
+            delta = c * torch.sign(tt.mean() - tt)
+            delta = delta - delta.mean()
+            b.add_(delta)
+            t.zero_()
+
+
 # ---------------------------------------------------------------------------
 # row movement with the GPU accumulation semantics
 # ---------------------------------------------------------------------------

@@ -142,3 +142,35 @@ def test_float8_converter_selects_experts_by_fqn():
     assert set(model["a"].state_dict()) == set(model["b"].state_dict())
     assert find_pad_multiple([conv_cfg]) == 16 and find_pad_multiple([]) is None
     assert Float8GroupedMMConverter.Config(fqns="experts").build().fqns == ["experts"]
+
+
+def test_load_balancing_hook_registration_follows_reference_rules():
+    """register_moe_load_balancing_hook registers only when the MoE layers have a
+    coefficient (optimizer.py:352-362, 439-444); the walk goes layers -> block.moe."""
+    from torchtitan_amd.load_balancing import _moe_blocks, register_moe_load_balancing_hook
+
+    class Block(torch.nn.Module):
+        def __init__(self, coeff):
+            super().__init__()
+            self.moe_enabled = True
+            self.moe = _cfg(hs=0, coeff=coeff).build()
+
+    class Model(torch.nn.Module):
+        def __init__(self, coeff):
+            super().__init__()
+            self.layers = torch.nn.ModuleDict({"0": Block(coeff), "1": Block(coeff)})
+
+    class Recorder:
+        def __init__(self):
+            self.hooks = []
+
+        def register_step_pre_hook(self, fn):
+            self.hooks.append(fn)
+
+    with_coeff, without = Recorder(), Recorder()
+    register_moe_load_balancing_hook(with_coeff, [Model(1e-3)])
+    register_moe_load_balancing_hook(without, [Model(None)])
+    assert len(with_coeff.hooks) == 1 and without.hooks == []
+    assert len(_moe_blocks([Model(1e-3)])) == 2
+    # a model without a `layers` dict: every MoE module
+    assert len(_moe_blocks([torch.nn.Sequential(_cfg(hs=0).build())])) == 1

@@ -15,7 +15,9 @@ What fixes each function, independently of the formula being checked:
   * experts_grouped_mm / experts_for_loop: torch._grouped_mm on the CPU (the
     reference's third-party call) and a float64 textbook loop;
   * router gradients: float64 finite differences;
-  * moe_forward: the reference op sequence (moe_forward_reference_ops) on the CPU.
+  * moe_forward: the reference op sequence (moe_forward_reference_ops) on the CPU;
+  * expert_bias_update: closed forms on hand-worked loads (balanced, one hot
+    expert, ties with the mean, the recomputation halving).
 The GPU-lowering rules the oracle states (top-k tie order, deterministic
 scatter-add order, index-backward rounding, short-row sum order) are pinned
 against torch on the device in tests/test_gpu_oracle_pins.py.
@@ -392,3 +394,40 @@ def test_moe_forward_matches_reference_op_sequence(score_before, grouped):
     torch.testing.assert_close(outs[0], outs[1], **tol)
     for a, b in zip(grads[0], grads[1]):
         torch.testing.assert_close(a, b, **tol)
+
+
+# ---------------------------------------------------------------------------
+# aux-loss-free bias update: hand-worked closed forms (optimizer.py:416-431)
+# ---------------------------------------------------------------------------
+
+
+def _bias_case(t, coeff=1e-3, halve=False, bias=None):
+    tt = torch.tensor(t, dtype=torch.float32)
+    b = torch.zeros(len(t)) if bias is None else torch.tensor(bias, dtype=torch.float32)
+    R.expert_bias_update([tt], [b], [coeff], [halve])
+    assert torch.count_nonzero(tt) == 0
+    return b
+
+
+def test_bias_update_balanced_is_noop():
+    assert torch.equal(_bias_case([7.0, 7.0, 7.0, 7.0], bias=[0.5, -0.5, 0.25, 0.0]),
+                       torch.tensor([0.5, -0.5, 0.25, 0.0]))
+
+
+def test_bias_update_one_hot_expert():
+    # mean 4: signs (-1, 1, 1, 1); mean of delta = coeff / 2
+    c = torch.tensor(0.125)  # a power of two keeps every step exact
+    b = _bias_case([10.0, 2.0, 2.0, 2.0], coeff=float(c))
+    assert torch.equal(b, torch.tensor([-1.5, 0.5, 0.5, 0.5]) * c)
+
+
+def test_bias_update_ties_with_mean_get_zero_sign():
+    # mean 3: signs (1, 0, -1, 0) -> mean 0
+    b = _bias_case([2.0, 3.0, 4.0, 3.0], coeff=0.25)
+    assert torch.equal(b, torch.tensor([0.25, 0.0, -0.25, 0.0]))
+
+
+def test_bias_update_recompute_halves_with_floor():
+    # [9, 3, 3, 1] // 2 = [4, 1, 1, 0], mean 1.5: signs (-1, 1, 1, 1)
+    b = _bias_case([9.0, 3.0, 3.0, 1.0], coeff=0.5, halve=True)
+    assert torch.equal(b, torch.tensor([-0.75, 0.25, 0.25, 0.25]))

@@ -564,3 +564,61 @@ def _gs8_bwd(ctx, dy, _dg, _du, _dh):
 
 
 grouped_swiglu_fp8.register_autograd(_gs8_bwd, setup_context=_gs_setup)
+
+
+# ---------------------------------------------------------------------------
+# row gather / scatter by an index (expert-parallel permute and unpermute)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::gather_rows", mutates_args=())
+def gather_rows(src: Tensor, idx: Tensor) -> Tensor:
+    """dst = src[idx, :] (expert_parallel.py:70-74)."""
+    require_gpu(src, idx)
+    s = src.contiguous()
+    ix = idx.to(torch.int64).contiguous()
+    n, d = ix.shape[0], s.shape[1]
+    out = s.new_empty(n, d)
+    call("moe_gather_rows", ptr(s), s.shape[0], ptr(ix), n, d, _dtype_code(s), ptr(out), stream_of(s))
+    return out
+
+
+@gather_rows.register_fake
+def _(src, idx):
+    return src.new_empty(idx.shape[0], src.shape[1])
+
+
+@torch.library.custom_op("moe_mi355x::scatter_rows", mutates_args=())
+def scatter_rows(src: Tensor, idx: Tensor, n_rows: int) -> Tensor:
+    """dst = empty(n_rows, d); dst[idx, :] = src (expert_parallel.py:77-80). Rows of
+    dst that idx does not name are left uninitialised, as in the reference."""
+    require_gpu(src, idx)
+    s = src.contiguous()
+    ix = idx.to(torch.int64).contiguous()
+    out = s.new_empty(n_rows, s.shape[1])
+    call("moe_scatter_rows", ptr(s), ptr(ix), ix.shape[0], s.shape[1], _dtype_code(s), ptr(out), n_rows,
+         stream_of(s))
+    return out
+
+
+@scatter_rows.register_fake
+def _(src, idx, n_rows):
+    return src.new_empty(n_rows, src.shape[1])
+
+
+def _rows_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[1])
+    ctx.n_src = inputs[0].shape[0]
+
+
+def _gather_rows_bwd(ctx, g):
+    # a permutation: every source row receives exactly one gradient row
+    (idx,) = ctx.saved_tensors
+    return scatter_rows(g, idx, ctx.n_src), None
+
+
+def _scatter_rows_bwd(ctx, g):
+    (idx,) = ctx.saved_tensors
+    return gather_rows(g, idx), None, None
+
+
+gather_rows.register_autograd(_gather_rows_bwd, setup_context=_rows_setup)
+scatter_rows.register_autograd(_scatter_rows_bwd, setup_context=_rows_setup)
