@@ -20,10 +20,15 @@
 //    SwiGLU backward), dx (dg . w1 + du . w3, two scaled products added in
 //    bf16), dw13 and dw2 (k = the expert's token group).
 //
-// Tiles: 256 threads, 2 x 2 waves, BM x BN output tile, 128 k per stage held
-// as two 64-byte half-tiles in the conflict-free chunk-major LDS layout of
-// the bf16 kernels; each lane's 32-byte MFMA fragment is chunk (lane >> 4) of
-// both halves (any k order is valid as long as both operands share it).
+// Tiles: 256 threads, 2 x 2 waves, BM x BN output tile, 128 k per stage.
+// Operands reach LDS by direct-to-LDS copies (global_load_lds_dwordx4, one
+// wave instruction = 8 rows x 128 bytes, coalesced) into row-major 128-byte
+// rows with 16-byte chunk c of row r at c ^ ((r >> 1) & 7), which is
+// conflict-free for the fragment reads; two stages, one barrier per k-step,
+// copies waited for with explicit vmcnt. Each lane's 32-byte MFMA fragment is
+// chunks (lane >> 4) and 4 + (lane >> 4) of its row (any k order is valid as
+// long as both operands share it). Rows past a segment and k past a padded
+// token group are copied from a zero row.
 #include "common.h"
 
 namespace moe {
@@ -271,10 +276,19 @@ struct Params {
   uint16_t* o2;
 };
 
-template <int ROWS>
-__device__ __forceinline__ int lds_off(int r, int kc) {
-  return (kc * ROWS + (r ^ (((2 * kc) ^ (r >> 3)) & 7))) * 16;  // bytes
+#define LDSP __attribute__((address_space(3)))
+// One wave-wide direct-to-LDS copy: lane i's 16 bytes at g land at LDS byte
+// address lds + 16 i; issued as inline asm and waited for with vmcnt.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" :: "v"(g), "{m0}"(lds) : "memory");
 }
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* ptr) { return (uint32_t)(size_t)((LDSP const uint8_t*)ptr); }
+
+// Row-major LDS tile with 128-byte rows (one 128-k stage of fp8): byte offset of
+// 16-byte chunk c of row r; conflict-free for fragment reads of 16 rows.
+__device__ __forceinline__ int rm_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+
+__device__ const uint4 kZeroRow[64] = {};  // source of zero rows and k past a segment
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
@@ -282,17 +296,15 @@ template <int MODE, int BM, int BN, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
   constexpr bool kRowGrouped = MODE <= kDx;
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
-  constexpr int PCH = BM * 8 / kThreads;  // 16-byte chunks per thread per stage (128 k = 8 chunks per row)
-  constexpr int QCH = BN * 8 / kThreads;
-  constexpr int HALF_P = BM * 64, HALF_Q = BN * 64;  // bytes per 64-byte half-tile
-  __shared__ __attribute__((aligned(16))) uint8_t sP[2][2 * HALF_P];
-  __shared__ __attribute__((aligned(16))) uint8_t sQ[2][2 * HALF_Q];
+  constexpr int CPW_P = BM / 8 / 4, CPW_Q = BN / 8 / 4;  // 1 KB copies (8 rows x 128 B) per wave and stage
+  __shared__ __attribute__((aligned(1024))) uint8_t sP[2][BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ[2][BN * 128];
   __shared__ int s_seg[kMaxE + 1];
   __shared__ int s_pst[kMaxE + 1];
   __shared__ int s_tile[kMaxE + 1];
   __shared__ int s_tmp[8];
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wv >> 1, wn = wv & 1;
   const int E = p.E, D = p.D, H = p.H;
   int Ntot = 0, Kfix = 0, Mfix = 0;
@@ -368,62 +380,58 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
     const int nk = (Klen + 127) / 128;
     const int row0 = seg0 + mt * BM;
 
-    // P / Q row pointers (k-contiguous), row strides in bytes
-    auto p_row = [&](int m, bool& ok) -> const uint8_t* {
+    // copy sources: lane i of copy c fills row 8 c + i / 8, 16-byte chunk (i % 8),
+    // loading global chunk (i % 8) ^ ((row >> 1) & 7) of that row
+    const int cr = lane >> 3;
+    const uint8_t* srcP[CPW_P];
+    const uint8_t* srcQ[CPW_Q];
+    bool okP[CPW_P];
+    int chP[CPW_P], chQ[CPW_Q];
+#pragma unroll
+    for (int b = 0; b < CPW_P; ++b) {
+      const int m = (wv * CPW_P + b) * 8 + cr;
+      chP[b] = ((lane & 7) ^ ((m >> 1) & 7)) * 16;
       if (kRowGrouped) {
         const int r = row0 + m;
-        ok = r < seg1;
-        return p.qp + (int64_t)r * Kfix;
+        okP[b] = r < seg1;
+        srcP[b] = p.qp + (int64_t)r * Kfix + chP[b];
+      } else {
+        okP[b] = true;
+        srcP[b] = p.qp + (int64_t)(mt * BM + m) * p.Rpad + pst0 + chP[b];
       }
-      ok = true;
-      return p.qp + (int64_t)(mt * BM + m) * p.Rpad + pst0;
-    };
-    auto q_row = [&](int n) -> const uint8_t* {
+    }
+#pragma unroll
+    for (int b = 0; b < CPW_Q; ++b) {
+      const int n = (wv * CPW_Q + b) * 8 + cr;
+      chQ[b] = ((lane & 7) ^ ((n >> 1) & 7)) * 16;
+      const uint8_t* rowp;
       if (MODE == kGateUp) {
         const int blk = n >> 4;
         const int hc = nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
-        return ((blk & 1) ? p.qq2 : p.qq) + (e64 * H + hc) * (int64_t)D;
+        rowp = ((blk & 1) ? p.qq2 : p.qq) + (e64 * H + hc) * (int64_t)D;
+      } else if (MODE == kDown) {
+        rowp = p.qq + (e64 * D + nt * BN + n) * (int64_t)H;
+      } else if (MODE == kDgu) {
+        rowp = p.qq + (e64 * H + nt * BN + n) * (int64_t)D;
+      } else if (MODE == kDx) {
+        rowp = p.qq + (e64 * D + nt * BN + n) * (int64_t)(2 * H);
+      } else {
+        rowp = p.qq + (int64_t)(nt * BN + n) * p.Rpad + pst0;
       }
-      if (MODE == kDown) return p.qq + (e64 * D + nt * BN + n) * (int64_t)H;
-      if (MODE == kDgu) return p.qq + (e64 * H + nt * BN + n) * (int64_t)D;
-      if (MODE == kDx) return p.qq + (e64 * D + nt * BN + n) * (int64_t)(2 * H);
-      return p.qq + (int64_t)(nt * BN + n) * p.Rpad + pst0;
-    };
-
-    uint4 rp[PCH], rq[QCH], np[PCH], nq[QCH];
-    auto load = [&](uint4 (&dp)[PCH], uint4 (&dq)[QCH], int kt) {
+      srcQ[b] = rowp + chQ[b];
+    }
+    auto issue = [&](int kt) {
+      const int s = kt & 1;
       const int k0 = kt * 128;
 #pragma unroll
-      for (int i = 0; i < PCH; ++i) {
-        const int c = tid + i * kThreads;
-        const int half = c / (BM * 4), w = c % (BM * 4);
-        const int m = w >> 2, kc = w & 3;
-        const int kb = k0 + half * 64 + kc * 16;
-        bool ok;
-        const uint8_t* rowp = p_row(m, ok);
-        dp[i] = (ok && kb < Klen) ? *(const uint4*)(rowp + kb) : make_uint4(0, 0, 0, 0);
+      for (int b = 0; b < CPW_P; ++b) {
+        const bool ok = okP[b] && k0 + chP[b] < Klen;
+        dma16(ok ? (const void*)(srcP[b] + k0) : (const void*)kZeroRow, lds_addr(&sP[s][(wv * CPW_P + b) * 1024]));
       }
 #pragma unroll
-      for (int i = 0; i < QCH; ++i) {
-        const int c = tid + i * kThreads;
-        const int half = c / (BN * 4), w = c % (BN * 4);
-        const int n = w >> 2, kc = w & 3;
-        const int kb = k0 + half * 64 + kc * 16;
-        dq[i] = (kb < Klen) ? *(const uint4*)(q_row(n) + kb) : make_uint4(0, 0, 0, 0);
-      }
-    };
-    auto store = [&](const uint4 (&dp)[PCH], const uint4 (&dq)[QCH], int s) {
-#pragma unroll
-      for (int i = 0; i < PCH; ++i) {
-        const int c = tid + i * kThreads;
-        const int half = c / (BM * 4), w = c % (BM * 4);
-        *(uint4*)(&sP[s][half * HALF_P + lds_off<BM>(w >> 2, w & 3)]) = dp[i];
-      }
-#pragma unroll
-      for (int i = 0; i < QCH; ++i) {
-        const int c = tid + i * kThreads;
-        const int half = c / (BN * 4), w = c % (BN * 4);
-        *(uint4*)(&sQ[s][half * HALF_Q + lds_off<BN>(w >> 2, w & 3)]) = dq[i];
+      for (int b = 0; b < CPW_Q; ++b) {
+        const bool ok = k0 + chQ[b] < Klen;
+        dma16(ok ? (const void*)(srcQ[b] + k0) : (const void*)kZeroRow, lds_addr(&sQ[s][(wv * CPW_Q + b) * 1024]));
       }
     };
 
@@ -439,15 +447,15 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int m = wm * WM + i * 16 + ml;
-        const uint4 a0 = *(const uint4*)(&sP[s][lds_off<BM>(m, g4)]);
-        const uint4 a1 = *(const uint4*)(&sP[s][HALF_P + lds_off<BM>(m, g4)]);
+        const uint4 a0 = *(const uint4*)(&sP[s][rm_off(m, g4)]);
+        const uint4 a1 = *(const uint4*)(&sP[s][rm_off(m, 4 + g4)]);
         af[i] = v8i_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = wn * WN + j * 16 + ml;
-        const uint4 b0 = *(const uint4*)(&sQ[s][lds_off<BN>(n, g4)]);
-        const uint4 b1 = *(const uint4*)(&sQ[s][HALF_Q + lds_off<BN>(n, g4)]);
+        const uint4 b0 = *(const uint4*)(&sQ[s][rm_off(n, g4)]);
+        const uint4 b1 = *(const uint4*)(&sQ[s][rm_off(n, 4 + g4)]);
         const v8i_t bq = v8i_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -477,19 +485,15 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
     };
     const int kt_half = (MODE == kDx) ? H / 128 : -1;
 
-    __syncthreads();
-    if (nk > 0) {
-      load(rp, rq, 0);
-      store(rp, rq, 0);
-    }
-    __syncthreads();
+    // the previous tile's LDS reads are done in every wave
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (nk > 0) issue(0);
     for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load(np, nq, kt + 1);
+      // stage kt has landed in every wave; the reads of the other buffer are retired
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (kt + 1 < nk) issue(kt + 1);
       if (MODE == kDx && kt == kt_half) park_dx_half();
-      compute(cur);
-      if (kt + 1 < nk) store(np, nq, cur ^ 1);
-      __syncthreads();
+      compute(kt & 1);
     }
 
     // ---- epilogues: lane holds C[m = .. + ml][n = .. + nql + 0..3] ----
