@@ -122,20 +122,27 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
 }
 
 // Column amax over `n_rows` rows of a 64-column slab (row stride ld elements)
-// -> s_amax[64]; every thread of the block calls it.
+// -> s_amax[64]; every thread of the block calls it. Four independent 16-byte
+// loads per thread are in flight per iteration.
 __device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int64_t ld, int n_rows, float* s_red,
                                           float* s_amax) {
   const int t = threadIdx.x;
-  const int ch = t & 7, r0 = t >> 3;  // 8 chunks of 8 columns, 32 rows per pass
+  const int ch = t & 7, r0 = t >> 3;  // 8 chunks of 8 columns, 32 rows per sweep
   float m[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) m[i] = 0.f;
-  for (int r = r0; r < n_rows; r += 32) {
-    const uint4 v = *(const uint4*)(base + (int64_t)r * ld + ch * 8);
-    m[0] = fmaxf(m[0], fabsf(bf_lo(v.x))); m[1] = fmaxf(m[1], fabsf(bf_hi(v.x)));
-    m[2] = fmaxf(m[2], fabsf(bf_lo(v.y))); m[3] = fmaxf(m[3], fabsf(bf_hi(v.y)));
-    m[4] = fmaxf(m[4], fabsf(bf_lo(v.z))); m[5] = fmaxf(m[5], fabsf(bf_hi(v.z)));
-    m[6] = fmaxf(m[6], fabsf(bf_lo(v.w))); m[7] = fmaxf(m[7], fabsf(bf_hi(v.w)));
+  for (int r = r0; r < n_rows; r += 128) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      v[u] = (r + 32 * u < n_rows) ? *(const uint4*)(base + (int64_t)(r + 32 * u) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      m[0] = fmaxf(m[0], fabsf(bf_lo(v[u].x))); m[1] = fmaxf(m[1], fabsf(bf_hi(v[u].x)));
+      m[2] = fmaxf(m[2], fabsf(bf_lo(v[u].y))); m[3] = fmaxf(m[3], fabsf(bf_hi(v[u].y)));
+      m[4] = fmaxf(m[4], fabsf(bf_lo(v[u].z))); m[5] = fmaxf(m[5], fabsf(bf_hi(v[u].z)));
+      m[6] = fmaxf(m[6], fabsf(bf_lo(v[u].w))); m[7] = fmaxf(m[7], fabsf(bf_hi(v[u].w)));
+    }
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) s_red[(ch * 8 + i) * 33 + r0] = m[i];
@@ -148,38 +155,49 @@ __device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int
   __syncthreads();
 }
 
-// Transposes a [rows x 64] bf16 slab (64 rows per pass) into 64 output rows of
-// fp8 (one per slab column), quantized with that column's scale.
-// out row b starts at out + b * ldo; rows >= n_rows up to n_out are zero.
+constexpr int kSlabRows = 128;  // rows transposed per pass
+
+// Transposes a [rows x 64] bf16 slab (128 rows per pass, four loads in flight
+// per thread) into 64 output rows of fp8 (one per slab column), quantized with
+// that column's scale. out row b starts at out + b * ldo; rows >= n_rows up to
+// n_out (a multiple of 16) are zero.
 __device__ __forceinline__ void slab_transpose_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows,
                                                      int n_out, uint8_t* __restrict__ out, int64_t ldo,
-                                                     const float* s_scale, uint16_t (*s_tile)[66]) {
+                                                     const float* s_scale, uint16_t (*s_tile)[kSlabRows + 2]) {
   const int t = threadIdx.x;
-  for (int a0 = 0; a0 < n_out; a0 += 64) {
-    // load 64 rows x 64 columns (rows past n_rows are zero)
+  for (int a0 = 0; a0 < n_out; a0 += kSlabRows) {
+    uint4 v[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int c = t + i * 256;
       const int r = c >> 3, ch = c & 7;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (a0 + r < n_rows) v = *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8);
-      const uint16_t* pv = (const uint16_t*)&v;
+      v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = t + i * 256;
+      const int r = c >> 3, ch = c & 7;
+      const uint16_t* pv = (const uint16_t*)&v[i];
 #pragma unroll
       for (int j = 0; j < 8; ++j) s_tile[ch * 8 + j][r] = pv[j];
     }
     __syncthreads();
-    // write: thread -> (column b, 16 rows)
-    const int b = t >> 2, seg = (t & 3) * 16;
-    if (a0 + seg < n_out) {
-      const float s = s_scale[b];
-      uint32_t w[4];
+    // write: thread -> (column b, 32 rows as two 16-byte stores)
+    const int b = t >> 2, seg = (t & 3) * 32;
+    const float s = s_scale[b];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        w[j] = 0;
+    for (int h = 0; h < 2; ++h) {
+      const int rr = seg + 16 * h;
+      if (a0 + rr < n_out) {
+        uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[j] |= e4m3(bf2f(s_tile[b][seg + 4 * j + i]) / s) << (8 * i);
+        for (int j = 0; j < 4; ++j) {
+          w[j] = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[j] |= e4m3(bf2f(s_tile[b][rr + 4 * j + i]) / s) << (8 * i);
+        }
+        *(uint4*)(out + (int64_t)b * ldo + a0 + rr) = make_uint4(w[0], w[1], w[2], w[3]);
       }
-      *(uint4*)(out + (int64_t)b * ldo + a0 + seg) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     __syncthreads();
   }
@@ -192,7 +210,7 @@ __global__ __launch_bounds__(256) void quant_cols_t_kernel(const uint16_t* __res
                                                            float* __restrict__ scale, int64_t s_estride) {
   __shared__ float s_red[64 * 33];
   __shared__ float s_amax[64];
-  __shared__ uint16_t s_tile[64][66];
+  __shared__ uint16_t s_tile[64][kSlabRows + 2];
   const int nb = B / 64;
   const int64_t e = blockIdx.x / nb;
   const int b0 = (blockIdx.x % nb) * 64;
@@ -215,7 +233,7 @@ __global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __r
                                                              uint8_t* __restrict__ q, float* __restrict__ scale) {
   __shared__ float s_red[64 * 33];
   __shared__ float s_amax[64];
-  __shared__ uint16_t s_tile[64][66];
+  __shared__ uint16_t s_tile[64][kSlabRows + 2];
   __shared__ int s_tmp[8];
   __shared__ int s_seg[2];
   const int nc = C / 64;
