@@ -269,8 +269,20 @@ int moe_expert_bias_update(float* const* tokens_per_expert, float* const* expert
 int moe_ep_permute_indices(const int64_t* tokens_per_expert_group, int32_t experts_per_rank, int32_t num_ranks,
                            int64_t total, int64_t* permuted_indices, int64_t* num_tokens_per_expert,
                            moe_stream_t stream);
-/* dst[i, :] = src[idx[i], :] for i < n_rows (rows with idx < 0 or >= n_src_rows
- * are skipped); rows of `dim` elements of `dtype` (MOE_DTYPE_*), 16-byte
+/* The permute of moe_ep_permute_indices with every expert's group padded by
+ * zero rows to a multiple of pad_multiple (16 for fp8, 32 for MXFP8): padding
+ * positions get index sum(counts) (a zero row appended after the input rows),
+ * padded_tokens_per_expert [experts_per_rank] int64 (nullable) the padded group
+ * sizes and group_offsets [experts_per_rank] int32 (nullable) their inclusive
+ * ends; total_padded = the sum of the padded sizes.
+ * Replaces torchao's permute_and_pad as called by TorchAOExpertParallel,
+ * torchtitan/distributed/expert_parallel.py:537-551. */
+int moe_ep_permute_pad_indices(const int64_t* tokens_per_expert_group, int32_t experts_per_rank, int32_t num_ranks,
+                               int32_t pad_multiple, int64_t total_padded, int64_t* permuted_indices,
+                               int64_t* padded_tokens_per_expert, int32_t* group_offsets, moe_stream_t stream);
+/* dst[i, :] = src[idx[i], :] for i < n_rows; idx == n_src_rows writes a zero row
+ * (the appended padding row); rows with other idx outside [0, n_src_rows) are
+ * left untouched. Rows of `dim` elements of `dtype` (MOE_DTYPE_*), 16-byte
  * multiples. Replaces x[permuted_indices, :] of _permute, expert_parallel.py:70-74. */
 int moe_gather_rows(const void* src, int64_t n_src_rows, const int64_t* idx, int64_t n_rows, int32_t dim,
                     int32_t dtype, void* dst, moe_stream_t stream);

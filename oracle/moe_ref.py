@@ -190,6 +190,27 @@ def generate_permute_indices(tokens_per_expert_group, experts_per_rank: int, num
     return out, mat.sum(axis=0)
 
 
+def generate_permute_pad_indices(tokens_per_expert_group, experts_per_rank: int, num_ranks: int, pad: int):
+    """The permute_and_pad layout TorchAOExpertParallel relies on
+    (expert_parallel.py:537-562; torchao's permute_and_pad itself is absent, so this
+    is fixed by its call site): the rows of generate_permute_indices, each expert's
+    group followed by zero rows up to a multiple of `pad`; padding rows index the
+    extra zero row appended after the input (index sum(counts), dropped again by
+    _unpermute's [:-1]). Returns (indices, padded counts, inclusive group ends)."""
+    idx, per_expert = generate_permute_indices(tokens_per_expert_group, experts_per_rank, num_ranks)
+    n_in = int(np.asarray(tokens_per_expert_group).sum())
+    out, padded, ends, pos = [], [], [], 0
+    for e in range(experts_per_rank):
+        g = int(per_expert[e])
+        gp = (g + pad - 1) // pad * pad
+        out.extend(idx[pos : pos + g].tolist())
+        out.extend([n_in] * (gp - g))
+        pos += g
+        padded.append(gp)
+        ends.append((ends[-1] if ends else 0) + gp)
+    return np.asarray(out, dtype=np.int64), np.asarray(padded, dtype=np.int64), np.asarray(ends, dtype=np.int64)
+
+
 def expert_bias_update(tokens_per_expert, expert_bias, coeffs, halve) -> None:
     """_update_expert_bias, torchtitan/components/optimizer.py:386-431, per layer
     with the same torch ops: t = tokens_per_expert (// 2 for recomputing blocks),

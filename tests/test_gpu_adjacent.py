@@ -159,3 +159,33 @@ def test_ep_permute_unpermute_round_trip_and_grad(dev, dtype):
     xr = x.detach().clone().requires_grad_(True)
     xr[idx].backward(g)
     assert torch.equal(x.grad, xr.grad)
+
+
+@pytest.mark.parametrize("pad", [16, 32])
+def test_ep_permute_and_pad(dev, pad):
+    """Padded expert-major layout for quantized grouped GEMMs (torchao's permute_and_pad
+    as TorchAOExpertParallel calls it; torchao itself is absent, so the layout is the
+    one its call site fixes): indices vs the oracle, zero padding rows, round trip."""
+    from torchtitan_amd.expert_parallel import _permute_and_pad, _unpermute_padded
+
+    rng = np.random.default_rng(pad)
+    ranks, experts, d = 4, 8, 256
+    counts_np = rng.integers(0, 50, ranks * experts)
+    counts_np[3] = 0
+    counts = torch.from_numpy(counts_np).to(dev)
+    total = int(counts_np.sum())
+    x = torch.randn(total, d, device=dev).bfloat16().requires_grad_(True)
+    shape, xp, idx, padded, offsets = _permute_and_pad(x, counts, ranks, experts, pad)
+    ref_idx, ref_padded, ref_ends = R.generate_permute_pad_indices(counts_np, experts, ranks, pad)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    assert np.array_equal(padded.cpu().numpy(), ref_padded)
+    assert np.array_equal(offsets.cpu().numpy(), ref_ends)
+    assert tuple(shape) == (total + 1, d)
+    x_ext = torch.cat([x.detach(), torch.zeros(1, d, device=dev, dtype=x.dtype)])
+    assert torch.equal(xp, x_ext[idx])
+    assert torch.equal(_unpermute_padded(xp, shape, idx), x.detach())
+    g = torch.randn_like(xp)
+    xp.backward(g)
+    xr = x_ext.clone().requires_grad_(True)
+    xr[idx].backward(g)
+    assert torch.equal(x.grad, xr.grad[:-1])

@@ -431,3 +431,25 @@ def test_bias_update_recompute_halves_with_floor():
     # [9, 3, 3, 1] // 2 = [4, 1, 1, 0], mean 1.5: signs (-1, 1, 1, 1)
     b = _bias_case([9.0, 3.0, 3.0, 1.0], coeff=0.5, halve=True)
     assert torch.equal(b, torch.tensor([-0.75, 0.25, 0.25, 0.25]))
+
+
+@pytest.mark.parametrize("pad", [1, 16, 32])
+def test_permute_pad_layout_reduces_to_the_unpadded_permute(pad):
+    """The padded layout (fixed by TorchAOExpertParallel's call site) holds the
+    unpadded permutation's rows in order, each expert group padded to a multiple of
+    pad with the appended zero row's index, and is the unpadded one for pad = 1."""
+    rng = np.random.default_rng(pad)
+    for ranks, experts in [(1, 4), (3, 5), (8, 2)]:
+        counts = rng.integers(0, 40, ranks * experts)
+        idx, ntok = R.generate_permute_indices(counts, experts, ranks)
+        pidx, padded, ends = R.generate_permute_pad_indices(counts, experts, ranks, pad)
+        n_in = int(counts.sum())
+        assert np.array_equal(pidx[pidx != n_in], idx)
+        assert all(p % pad == 0 and p >= g for p, g in zip(padded, ntok))
+        assert np.array_equal(ends, np.cumsum(padded)) and len(pidx) == ends[-1]
+        starts = np.concatenate([[0], ends[:-1]])
+        for e in range(experts):
+            grp = pidx[starts[e]:ends[e]]
+            assert np.all(grp[ntok[e]:] == n_in) and np.all(grp[:ntok[e]] != n_in)
+        if pad == 1:
+            assert np.array_equal(pidx, idx)

@@ -54,6 +54,7 @@ SIGNATURES: dict[str, list] = {
     "moe_fp8_gemm_bwd_dw2": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P],
     "moe_expert_bias_update": [P, P, P, P, I32, I32, P],
     "moe_ep_permute_indices": [P, I32, I32, I64, P, P, P],
+    "moe_ep_permute_pad_indices": [P, I32, I32, I32, I64, P, P, P, P],
     "moe_gather_rows": [P, I64, P, I64, I32, I32, P, P],
     "moe_scatter_rows": [P, P, I64, I32, I32, P, I64, P],
 }

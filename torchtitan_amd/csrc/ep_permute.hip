@@ -14,6 +14,9 @@
 // and fills the positions grid-stride; the reference's host sync on the total
 // (torch.arange(total)) becomes the caller's `total` argument. Positions past
 // the sum of the counts (a `total` larger than it) are set to -1.
+// With a pad multiple (torchao's permute_and_pad, called at
+// expert_parallel.py:537-551 for the fp8 / MXFP8 grouped GEMMs), every
+// expert's group is followed by zero rows up to a multiple of it.
 #include "common.h"
 
 namespace moe {
@@ -35,11 +38,17 @@ __device__ __forceinline__ int64_t block_inclusive_scan_i64(int64_t v, int64_t* 
   return r;
 }
 
+// pad > 1 (permute_and_pad): every expert's group is padded with zero rows to a
+// multiple of pad; padding positions read the zero row appended after the
+// n_in input rows (index n_in), tokens_per_expert gets the padded counts and
+// group_offsets (nullable) the inclusive int32 ends of the padded groups.
 __global__ __launch_bounds__(256) void ep_permute_indices_kernel(const int64_t* __restrict__ counts, int R, int E,
-                                                                 int64_t total, int64_t* __restrict__ out_idx,
-                                                                 int64_t* __restrict__ tokens_per_expert) {
+                                                                 int pad, int64_t total, int64_t* __restrict__ out_idx,
+                                                                 int64_t* __restrict__ tokens_per_expert,
+                                                                 int32_t* __restrict__ group_offsets) {
   __shared__ int64_t s_in[kMaxEpSegments];    // input start of expert-major segment s
   __shared__ int64_t s_out[kMaxEpSegments + 1];
+  __shared__ int64_t s_len[kMaxEpSegments];
   __shared__ int64_t tmp[256];
   const int n = R * E;
   constexpr int PER = kMaxEpSegments / 256;
@@ -64,22 +73,34 @@ __global__ __launch_bounds__(256) void ep_permute_indices_kernel(const int64_t* 
       base += v[i];
     }
   }
-  // expert-major exclusive scan of the lengths -> output starts
+  // expert-major exclusive scan of the lengths (each expert's last segment
+  // carrying its group's padding) -> output starts
+  int64_t n_in = 0;
   {
     int64_t v[PER];
-    int64_t run = 0;
+    int64_t run = 0, run_in = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int s = threadIdx.x * PER + i;
-      int64_t len = 0;
+      int64_t len = 0, padded = 0;
       if (s < n) {
         const int e = s / R, r = s - e * R;
         len = counts[r * E + e];
+        padded = len;
+        if (pad > 1 && r == R - 1) {  // the group's padding follows its last segment
+          int64_t g = 0;
+          for (int rr = 0; rr < R; ++rr) g += counts[rr * E + e];
+          padded += (g + pad - 1) / pad * pad - g;
+        }
+        s_len[s] = len;
       }
-      v[i] = len;
-      run += len;
+      v[i] = padded;
+      run += padded;
+      run_in += len;
     }
     const int64_t incl = block_inclusive_scan_i64(run, tmp);
+    n_in = block_inclusive_scan_i64(run_in, tmp);
+    if (threadIdx.x == 255) tmp[0] = n_in;
     int64_t base = incl - run;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -87,14 +108,18 @@ __global__ __launch_bounds__(256) void ep_permute_indices_kernel(const int64_t* 
       if (s < n) s_out[s] = base;
       base += v[i];
     }
-    if (threadIdx.x == 255) s_out[n] = incl;  // the sum of every count
+    if (threadIdx.x == 255) s_out[n] = incl;  // the padded total
+    __syncthreads();
+    n_in = tmp[0];  // the sum of every count (the zero row's index)
     __syncthreads();
   }
-  if (blockIdx.x == 0 && tokens_per_expert) {
+  if (blockIdx.x == 0 && (tokens_per_expert || group_offsets)) {
     for (int e = threadIdx.x; e < E; e += 256) {
-      int64_t s = 0;
-      for (int r = 0; r < R; ++r) s += counts[r * E + e];
-      tokens_per_expert[e] = s;
+      int64_t g = 0;
+      for (int r = 0; r < R; ++r) g += counts[r * E + e];
+      if (pad > 1) g = (g + pad - 1) / pad * pad;
+      if (tokens_per_expert) tokens_per_expert[e] = g;
+      if (group_offsets) group_offsets[e] = (int32_t)(s_out[e * R] + g);  // the group's segments are contiguous
     }
   }
   const int64_t sum = s_out[n];
@@ -108,7 +133,8 @@ __global__ __launch_bounds__(256) void ep_permute_indices_kernel(const int64_t* 
       const int mid = (lo + hi + 1) >> 1;
       if (s_out[mid] <= p) lo = mid; else hi = mid - 1;
     }
-    out_idx[p] = s_in[lo] + (p - s_out[lo]);
+    const int64_t off = p - s_out[lo];
+    out_idx[p] = off < s_len[lo] ? s_in[lo] + off : n_in;  // past the rows: the group's padding
   }
 }
 
@@ -123,9 +149,13 @@ __global__ __launch_bounds__(256) void move_rows_kernel(const uint4* __restrict_
     const int64_t i = c / cpr;
     const int ch = (int)(c - i * cpr);
     const int64_t j = idx[i];
-    if (j < 0 || j >= n_src_rows) continue;  // -1 marks positions past the counts
-    if (SCATTER) dst[j * cpr + ch] = src[i * cpr + ch];
-    else dst[i * cpr + ch] = src[j * cpr + ch];
+    if (SCATTER) {
+      if (j >= 0 && j < n_src_rows) dst[j * cpr + ch] = src[i * cpr + ch];
+    } else if (j == n_src_rows) {
+      dst[i * cpr + ch] = make_uint4(0, 0, 0, 0);  // the zero row appended after the source rows
+    } else if (j >= 0 && j < n_src_rows) {
+      dst[i * cpr + ch] = src[j * cpr + ch];
+    }                                               // -1 (positions past the counts): untouched
   }
 }
 
@@ -143,7 +173,24 @@ MOE_API int moe_ep_permute_indices(const int64_t* tokens_per_expert_group, int32
   if (g > 1024) g = 1024;
   if (g < 1) g = 1;
   hipLaunchKernelGGL(ep_permute_indices_kernel, dim3((int)g), dim3(256), 0, stream, tokens_per_expert_group,
-                     num_ranks, experts_per_rank, total, permuted_indices, num_tokens_per_expert);
+                     num_ranks, experts_per_rank, 1, total, permuted_indices, num_tokens_per_expert,
+                     (int32_t*)nullptr);
+  return launch_status();
+}
+
+MOE_API int moe_ep_permute_pad_indices(const int64_t* tokens_per_expert_group, int32_t experts_per_rank,
+                                       int32_t num_ranks, int32_t pad_multiple, int64_t total_padded,
+                                       int64_t* permuted_indices, int64_t* padded_tokens_per_expert,
+                                       int32_t* group_offsets, hipStream_t stream) {
+  if (experts_per_rank < 1 || num_ranks < 1 || total_padded < 0 || pad_multiple < 1) return kErrInvalidArgument;
+  if ((int64_t)experts_per_rank * num_ranks > kMaxEpSegments) return kErrUnsupportedShape;
+  if (!tokens_per_expert_group || (total_padded > 0 && !permuted_indices)) return kErrInvalidArgument;
+  int64_t g = (total_padded + 255) / 256;
+  if (g > 1024) g = 1024;
+  if (g < 1) g = 1;
+  hipLaunchKernelGGL(ep_permute_indices_kernel, dim3((int)g), dim3(256), 0, stream, tokens_per_expert_group,
+                     num_ranks, experts_per_rank, (int)pad_multiple, total_padded, permuted_indices,
+                     padded_tokens_per_expert, group_offsets);
   return launch_status();
 }
 
