@@ -14,7 +14,7 @@ timings taken inside the timed steps, the roofline of the dominant kernel, and
 the reference's CPU MoE path (the oracle's op-for-op restatement) timed on a
 bounded token sample on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload kimi|dsv3|zipf]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload kimi|dsv3|zipf|kimi_fp8|kimi_mxfp8]
                        [--no-cpu-baseline] [--cpu-tokens N]
 """
 
@@ -63,9 +63,15 @@ WORKLOADS = {
         score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
         score_before=True, std=0.02, bias=0.01, zipf=None, fp8=True,
     ),
+    "kimi_mxfp8": dict(
+        desc="Kimi-shape MoE layer with MXFP8 (block-32 e8m0, RCEIL) grouped GEMMs",
+        bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+        score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.01, zipf=None, mxfp8=True,
+    ),
 }
 
-GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm")
+GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm", "mxfp8_gemm")
                      for m in ("gate_up", "down", "bwd_dgu", "bwd_dx", "bwd_dw13", "bwd_dw2"))
 
 
@@ -78,7 +84,7 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
     r = n * k
     b = 2  # bf16 rows
     flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw2": 2}
-    for kind in ("moe_grouped_gemm_", "moe_fp8_gemm_"):
+    for kind in ("moe_grouped_gemm_", "moe_fp8_gemm_", "moe_mxfp8_gemm_"):
         if name.startswith(kind) and name[len(kind):] in flops:
             return "mfma", float(flops[name[len(kind):]] * r * d * h)
     nbytes = {
@@ -142,6 +148,10 @@ def make_layer(w: dict, device: torch.device, seed: int):
         from torchtitan_amd.quantization import Float8GroupedMMConverter
 
         Float8GroupedMMConverter.Config(fqns=["experts"]).build().convert(moe)
+    if w.get("mxfp8"):
+        from torchtitan_amd.quantization import MXFP8Converter
+
+        MXFP8Converter.Config(fqns=["experts"]).build().convert(moe)
     return moe
 
 
@@ -282,7 +292,7 @@ def main() -> int:
         avg = sum(ds) / len(ds)
         bound, work = kernel_work(name, w)
         if bound == "mfma":
-            peak = PEAK_FP8_TFLOPS if name.startswith("moe_fp8_") else PEAK_BF16_TFLOPS
+            peak = PEAK_FP8_TFLOPS if name.startswith(("moe_fp8_", "moe_mxfp8_")) else PEAK_BF16_TFLOPS
             achieved, unit = work / (avg * 1e-3) / 1e12, "TFLOP/s"
         elif work is not None:
             achieved, peak, unit = work / (avg * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
@@ -298,12 +308,13 @@ def main() -> int:
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
     dom = max(kernels, key=lambda nm: kernels[nm]["avg_ms"] * kernels[nm]["launches_per_step"])
     dk = kernels[dom]
-    gemm_peak = PEAK_FP8_TFLOPS if w.get("fp8") else PEAK_BF16_TFLOPS
+    gemm_peak = PEAK_FP8_TFLOPS if (w.get("fp8") or w.get("mxfp8")) else PEAK_BF16_TFLOPS
     roofline = {
         "kernel": dom,
         "bound": dk["bound"],
         "achieved": dk["achieved"],
-        "peak": (PEAK_FP8_TFLOPS if dom.startswith("moe_fp8_") else PEAK_BF16_TFLOPS) if dk["bound"] == "mfma"
+        "peak": (PEAK_FP8_TFLOPS if dom.startswith(("moe_fp8_", "moe_mxfp8_")) else PEAK_BF16_TFLOPS)
+        if dk["bound"] == "mfma"
         else PEAK_HBM_GBS,
         "unit": dk["unit"],
         "frac": dk["frac"],
@@ -330,7 +341,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8 e4m3 (grouped GEMMs), bf16 elsewhere" if w.get("fp8") else "bf16",
+        "dtype": ("fp8 e4m3 (grouped GEMMs), bf16 elsewhere" if w.get("fp8") else
+                  "MXFP8 e4m3 + e8m0 block-32 scales (grouped GEMMs), bf16 elsewhere" if w.get("mxfp8") else "bf16"),
         "data": "synthetic (random-init weights, x ~ N(0,1), g ~ N(0,1))",
         "config": {
             "workload": f"{w['desc']}: N={n} tokens (bs {w['bs']} x seq {w['slen']}), dim {w['dim']}, "

@@ -242,6 +242,73 @@ int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const uint8_t* 
                          const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
                          int32_t dim, int32_t hidden, uint16_t* dw2, moe_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * MXFP8 grouped SwiGLU experts: torchao's MXFP8TrainingOpConfig with recipe
+ * "mxfp8_rceil", applied by MXFP8Converter
+ * (torchtitan/components/quantization/mx.py:25-128), token groups padded to
+ * 32 (quantization/__init__.py:36-40). Every row is quantized in blocks of
+ * 32 consecutive elements along the contraction: e8m0 scale byte
+ * e = clamp(ceil(log2(amax / 448)), -127, 127) + 127 (255 for NaN), elements
+ * e4m3fn(clamp(x * 2^(127 - e), +-448)) (x * 1 when e == 0). The GEMMs apply
+ * both scales in the MFMA (fp32 accumulation, bf16 outputs). Scales of
+ * row-quantized tensors are [rows, cols / 32]; of token-transposed ones
+ * k-block major, [padded_rows / 32, cols].
+ * ------------------------------------------------------------------------- */
+
+/* Rows of the token-transposed MXFP8 tensors: n_rows + n_experts * 31 rounded
+ * up to a multiple of 32 (every group starts at a multiple of 32). */
+int64_t moe_mxfp8_padded_rows(int64_t n_rows, int32_t n_experts);
+
+/* x [rows, cols] bf16 (cols % 32 == 0) -> q [rows, cols], scale [rows, cols / 32]. */
+int moe_mxfp8_quant_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q, uint8_t* scale,
+                         moe_stream_t stream);
+
+/* x [E, a, b] bf16 -> per expert e and column j the column quantized along a
+ * (blocks of 32) and written as a row of a values at
+ * q + e*q_expert_stride + j*q_row_stride, its a / 32 scales at
+ * scale + e*scale_expert_stride + j*scale_row_stride. */
+int moe_mxfp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
+                           int64_t q_expert_stride, int64_t q_row_stride, uint8_t* scale,
+                           int64_t scale_expert_stride, int64_t scale_row_stride, moe_stream_t stream);
+
+/* x [n_rows, cols] bf16 in expert token groups -> q [cols, padded_rows] with
+ * group e at the 32-aligned offset sum_{e'<e} ceil32(count_e') (zero padded),
+ * quantized along the tokens in blocks of 32; scale [padded_rows / 32, cols]
+ * (blocks of empty groups and past the groups are not written). */
+int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                             int32_t cols, int64_t padded_rows, uint8_t* q, uint8_t* scale,
+                             moe_stream_t stream);
+
+/* MXFP8 g, u, h as moe_fp8_gemm_gate_up; sx [R, D/32], sw1 and sw3 [E, H, D/32]. */
+int moe_mxfp8_gemm_gate_up(const uint8_t* qx, const uint8_t* sx, const uint8_t* qw1, const uint8_t* sw1,
+                           const uint8_t* qw3, const uint8_t* sw3, const int64_t* counts, int64_t n_rows,
+                           int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* g, uint16_t* u,
+                           uint16_t* h, moe_stream_t stream);
+/* MXFP8 y = qh.qw2^T; sh [R, H/32], sw2 [E, D, H/32]. */
+int moe_mxfp8_gemm_down(const uint8_t* qh, const uint8_t* sh, const uint8_t* qw2, const uint8_t* sw2,
+                        const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                        uint16_t* y, moe_stream_t stream);
+/* MXFP8 dh = qdy.qw2t^T (sdy [R, D/32], qw2t [E, H, D], sw2t [E, H, D/32]),
+ * then the SwiGLU backward -> dgu [R, 2H] bf16. */
+int moe_mxfp8_gemm_bwd_dgu(const uint8_t* qdy, const uint8_t* sdy, const uint8_t* qw2t, const uint8_t* sw2t,
+                           const uint16_t* g, const uint16_t* u, const int64_t* counts, int64_t n_rows,
+                           int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dgu, moe_stream_t stream);
+/* MXFP8 dx = bf16(dg.w1) + bf16(du.w3): qdgu [R, 2H] with sdgu [R, 2H/32],
+ * qw13t [E, D, 2H] with sw13t [E, D, 2H/32] (w1 half first). */
+int moe_mxfp8_gemm_bwd_dx(const uint8_t* qdgu, const uint8_t* sdgu, const uint8_t* qw13t, const uint8_t* sw13t,
+                          const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                          uint16_t* dx, moe_stream_t stream);
+/* MXFP8 dw1[e], dw3[e] = dgu_e^T . x_e from qdgut [2H, padded_rows]
+ * (sdgut [padded_rows/32, 2H]) and qxt [D, padded_rows] (sxt [padded_rows/32, D]). */
+int moe_mxfp8_gemm_bwd_dw13(const uint8_t* qdgut, const uint8_t* sdgut, const uint8_t* qxt, const uint8_t* sxt,
+                            const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                            int32_t dim, int32_t hidden, uint16_t* dw1, uint16_t* dw3, moe_stream_t stream);
+/* MXFP8 dw2[e] = dy_e^T . h_e from qdyt [D, padded_rows] (sdyt [padded_rows/32, D])
+ * and qht [H, padded_rows] (sht [padded_rows/32, H]). */
+int moe_mxfp8_gemm_bwd_dw2(const uint8_t* qdyt, const uint8_t* sdyt, const uint8_t* qht, const uint8_t* sht,
+                           const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                           int32_t dim, int32_t hidden, uint16_t* dw2, moe_stream_t stream);
+
 /* ---- auxiliary-loss-free load balancing (optimizer step pre-hook) ---- */
 
 /* For every MoE layer l < n_layers (<= 64), with t = tokens_per_expert[l]

@@ -594,3 +594,124 @@ def experts_fp8_backward(w1, w2, w3, x, counts, g, u, h, dy):
             dw2s.append(_fp8_mm(qdyt, sdyt, qht, sht).bfloat16())
         start += c
     return torch.cat(dxs), torch.stack(dw1s), torch.stack(dw2s), torch.stack(dw3s)
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 grouped GEMMs (parity unpinned: the reference delegates to torchao's
+# MXFP8TrainingOpConfig, recipe "mxfp8_rceil", through MXFP8Converter,
+# torchtitan/components/quantization/mx.py:25-128, and torchao is absent;
+# this restates torchao's published to_mx with the RCEIL scale derivation)
+# ---------------------------------------------------------------------------
+
+MX_BLOCK = 32  # elements per e8m0 scale
+MXFP8_PAD = 32  # token-group alignment (quantization/__init__.py:36-40)
+E8M0_BIAS = 127
+
+
+def quant_mxfp8(x: torch.Tensor, dim: int = -1):
+    """MX quantization along `dim` in blocks of 32 (RCEIL):
+    e = clamp(ceil(log2(amax / 448)), -127, 127) + 127 (255 where amax / 448
+    is NaN), q = e4m3fn(clamp(x * m, -448, 448)) with m = 2^(127 - e), or
+    m = 1 where e == 0. Returns (q float8_e4m3fn, e uint8 with `dim` / 32)."""
+    xf = x.float().movedim(dim, -1)
+    shp = xf.shape
+    if shp[-1] % MX_BLOCK:
+        raise ValueError(f"dimension {dim} ({shp[-1]}) is not a multiple of {MX_BLOCK}")
+    blocks = xf.reshape(*shp[:-1], shp[-1] // MX_BLOCK, MX_BLOCK)
+    amax = blocks.abs().amax(-1, keepdim=True)
+    descale = amax / FP8_MAX
+    e = torch.where(torch.isnan(descale), torch.full_like(descale, 255.0),
+                    torch.clamp(torch.ceil(torch.log2(descale)), -E8M0_BIAS, E8M0_BIAS) + E8M0_BIAS)
+    mult = torch.where(e == 0, torch.ones_like(e), torch.ldexp(torch.ones_like(e), (E8M0_BIAS - e)))
+    q = torch.clamp(blocks * mult, -FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q.reshape(shp).movedim(-1, dim), e.squeeze(-1).to(torch.uint8).movedim(-1, dim)
+
+
+def mx_dequant(q: torch.Tensor, e: torch.Tensor) -> torch.Tensor:
+    """fp64 values q * 2^(e - 127) of an MX tensor quantized along its last dim."""
+    f = torch.ldexp(torch.ones(e.shape, dtype=torch.float64), e.to(torch.float64) - E8M0_BIAS)
+    return q.double() * f.repeat_interleave(MX_BLOCK, dim=-1)
+
+
+def _mx_mm(qa, sa, qb, sb):
+    """MX grouped-GEMM block: dequant(qa) @ dequant(qb)^T accumulated in fp64,
+    returned as fp32 (both operands quantized along the contraction)."""
+    return (mx_dequant(qa, sa) @ mx_dequant(qb, sb).t()).float()
+
+
+def _pad_tokens(t: torch.Tensor, mult: int = MXFP8_PAD) -> torch.Tensor:
+    """Zero-pads the last dimension (a token group) to a multiple of `mult`."""
+    n = t.shape[-1]
+    pad = (n + mult - 1) // mult * mult - n
+    return torch.nn.functional.pad(t, (0, pad)) if pad else t
+
+
+def experts_mxfp8_forward(w1, w2, w3, x, counts):
+    """MXFP8 forward of _run_experts_grouped_mm (moe.py:53-70): x, h and every
+    weight quantized in 32-blocks along the contraction, fp32 accumulation,
+    g, u, h, y rounded to bf16 at the reference's points."""
+    qx, sx = quant_mxfp8(x)
+    qw1, sw1 = quant_mxfp8(w1)
+    qw3, sw3 = quant_mxfp8(w3)
+    qw2, sw2 = quant_mxfp8(w2)
+    gs, us, hs = [], [], []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        g = _mx_mm(qx[sl], sx[sl], qw1[e], sw1[e]).bfloat16()
+        u = _mx_mm(qx[sl], sx[sl], qw3[e], sw3[e]).bfloat16()
+        gs.append(g); us.append(u); hs.append(F.silu(g) * u)
+        start += c
+    g, u, h = torch.cat(gs), torch.cat(us), torch.cat(hs)
+    qh, sh = quant_mxfp8(h)
+    ys = []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        ys.append(_mx_mm(qh[sl], sh[sl], qw2[e], sw2[e]).bfloat16())
+        start += c
+    return torch.cat(ys), g, u, h
+
+
+def experts_mxfp8_backward(w1, w2, w3, x, counts, g, u, h, dy):
+    """MXFP8 backward matching experts_mxfp8_forward (each grouped GEMM's
+    backward as torchao's MX grouped-mm autograd function): dh = dy . w2 with
+    dy blocked along D and w2 blocked along D per (expert, h); SwiGLU backward
+    in bf16; dx = bf16(dg . w1) + bf16(du . w3) with dg, du and w1, w3 blocked
+    along H; dw = per-group products over the expert's tokens, both operands
+    blocked along the tokens of the group zero-padded to a multiple of 32."""
+    qdy, sdy = quant_mxfp8(dy)
+    dgs, dus = [], []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        qw2t, sw2t = quant_mxfp8(w2[e].t())  # [H, D]
+        dh = _mx_mm(qdy[sl], sdy[sl], qw2t, sw2t).bfloat16()
+        gg, uu = g[sl], u[sl]
+        dsl = dh * uu
+        du = dh * F.silu(gg)
+        dg = torch.ops.aten.silu_backward(dsl, gg)
+        dgs.append(dg); dus.append(du)
+        start += c
+    dg, du = torch.cat(dgs), torch.cat(dus)
+    qdg, sdg = quant_mxfp8(dg)
+    qdu, sdu = quant_mxfp8(du)
+    dxs, dw1s, dw2s, dw3s = [], [], [], []
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        sl = slice(start, start + c)
+        qw1t, sw1t = quant_mxfp8(w1[e].t())  # [D, H]
+        qw3t, sw3t = quant_mxfp8(w3[e].t())
+        dxs.append(_mx_mm(qdg[sl], sdg[sl], qw1t, sw1t).bfloat16() + _mx_mm(qdu[sl], sdu[sl], qw3t, sw3t).bfloat16())
+        if c == 0:
+            dw1s.append(torch.zeros_like(w1[e])); dw3s.append(torch.zeros_like(w3[e])); dw2s.append(torch.zeros_like(w2[e]))
+        else:
+            def qt(t):
+                return quant_mxfp8(_pad_tokens(t[sl].t()))
+            (qdgt, sdgt), (qdut, sdut), (qxt, sxt) = qt(dg), qt(du), qt(x)
+            (qdyt, sdyt), (qht, sht) = qt(dy), qt(h)
+            dw1s.append(_mx_mm(qdgt, sdgt, qxt, sxt).bfloat16())
+            dw3s.append(_mx_mm(qdut, sdut, qxt, sxt).bfloat16())
+            dw2s.append(_mx_mm(qdyt, sdyt, qht, sht).bfloat16())
+        start += c
+    return torch.cat(dxs), torch.stack(dw1s), torch.stack(dw2s), torch.stack(dw3s)

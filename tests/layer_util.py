@@ -29,6 +29,7 @@ class LayerShape:
     bias: float = 0.01
     zipf: float | None = None
     fp8: bool = False
+    mxfp8: bool = False
 
 
 def build_layer(sh: LayerShape, dev: torch.device, seed: int):
@@ -65,6 +66,10 @@ def build_layer(sh: LayerShape, dev: torch.device, seed: int):
         from torchtitan_amd.quantization import Float8GroupedMMConverter
 
         Float8GroupedMMConverter.Config(fqns=["experts"]).build().convert(moe)
+    if sh.mxfp8:
+        from torchtitan_amd.quantization import MXFP8Converter
+
+        MXFP8Converter.Config(fqns=["experts"]).build().convert(moe)
     x = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
     g = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
     return moe, x, g

@@ -10,11 +10,13 @@ run by torch on the same GPU (oracle.moe_forward_reference_ops):
          after the experts;
   kimi_fp8  the Kimi shape with 32768 tokens and fp8 e4m3 grouped GEMMs,
          against the same bf16 reference (the reference's own fp8 path is
-         torchao's and absent, so fp8 parity is unpinned).
+         torchao's and absent, so fp8 parity is unpinned);
+  kimi_mxfp8  the same with MXFP8 grouped GEMMs (block-32 e8m0 scales, RCEIL;
+         torchao's as well, unpinned).
 
 Routing (indices, counts, top scores) must be bit-exact; the output and all
 gradients within 1e-2 normwise relative error (max |ours - ref| / max |ref|),
-0.1 for the fp8 layer against the bf16 reference.
+0.1 for the fp8 and MXFP8 layers against the bf16 reference.
 """
 
 import pytest
@@ -33,9 +35,11 @@ SHAPES = {
                        groups=(8, 4), score_before=False, std=0.006),
     "kimi_fp8": LayerShape(bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
                            fp8=True),
+    "kimi_mxfp8": LayerShape(bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+                             mxfp8=True),
 }
 
-TOL = {"kimi_fp8": 0.1}
+TOL = {"kimi_fp8": 0.1, "kimi_mxfp8": 0.1}
 
 
 @pytest.mark.parametrize("name", list(SHAPES))

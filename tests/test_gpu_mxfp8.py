@@ -1,0 +1,257 @@
+"""MXFP8 grouped SwiGLU experts on the GPU.
+
+Parity is unpinned against the reference (its MXFP8 path is torchao's
+MXFP8TrainingOpConfig, absent here); the kernels are checked against the
+oracle's restatement of that recipe (quant_mxfp8, _mx_mm, experts_mxfp8_*),
+which tests/test_oracle.py pins on the CPU, and against the bf16 experts:
+  * quantizers: e4m3 bytes and e8m0 scales bit-exact vs the oracle, including
+    blocks of zeros, blocks too small for any scale (e == 0) and wide dynamic
+    ranges;
+  * each MXFP8 GEMM entry point, fed the oracle's own quantized operands:
+    normwise relative error <= 1e-2 (only the fp32 summation order differs);
+    scale blocks the kernels must not read are poisoned with NaN (0xff);
+  * the chained op (fwd + bwd): <= 5e-2 vs the emulation and <= 0.1 vs the
+    fp32 reference on the bf16 inputs.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe_ref as R
+from tests.conftest import banner
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 1e-2
+EMU_TOL = 5e-2
+BF16_TOL = 0.1
+NAN_E8M0 = 255
+
+
+def _rel(a, b):
+    a, b = a.detach().float().cpu(), b.detach().float().cpu()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def _u8(q):
+    return q.view(torch.uint8).contiguous()
+
+
+def _tokens_t(t, segs, rpad):
+    """Oracle token-transposed layout: q [C, rpad] with 32-aligned zero-padded
+    groups, scales [rpad / 32, C] k-block major (NaN where no group writes)."""
+    c = t.shape[1]
+    q = torch.zeros(c, rpad, dtype=torch.uint8)
+    sc = torch.full((rpad // 32, c), NAN_E8M0, dtype=torch.uint8)
+    per, pstart = [], 0
+    for s0, n in segs:
+        if n:
+            qq, ss = R.quant_mxfp8(R._pad_tokens(t[s0:s0 + n].t()))
+            n32 = qq.shape[1]
+            q[:, pstart:pstart + n32] = qq.view(torch.uint8)
+            sc[pstart // 32:pstart // 32 + n32 // 32] = ss.t()
+            per.append((qq, ss))
+        else:
+            per.append(None)
+        pstart += (n + 31) // 32 * 32
+    return q, sc, per
+
+
+def test_mxfp8_quantizers_bit_exact(dev):
+    banner("mxfp8 quantizers")
+    from torchtitan_amd import _lib, ops
+
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(300, 512, generator=g)
+         * torch.exp(torch.randn(300, 16, generator=g) * 4).repeat_interleave(32, 1)).bfloat16()
+    x[7] = 0                      # all-zero blocks: e = 0
+    x[9, 64:96] = 2.0 ** -121     # amax / 448 below 2^-127: e = 0, multiplier 1
+    x[11, 0:32] = 448.0           # exact power-of-two boundary
+    x[11, 32:64] = 450.0
+    q, s = ops._mx_quant_rows(x.to(dev), 512)
+    rq, rs = R.quant_mxfp8(x)
+    assert torch.equal(s.cpu(), rs), "e8m0 scales differ"
+    assert torch.equal(q.cpu(), rq.view(torch.uint8)), "MX bytes differ"
+    # columns, transposed and strided: w [E, A, B] -> rows (e, b) of A values
+    e, a, b = 3, 256, 128
+    w = (torch.randn(e, a, b, generator=g) * torch.exp(torch.randn(e, a, 1, generator=g) * 2)).bfloat16()
+    qt = torch.zeros(e, b, 2 * a, dtype=torch.uint8, device=dev)        # a row stride of 2a: the [E, D, 2H] layout
+    stt = torch.zeros(e, b, 2 * a // 32, dtype=torch.uint8, device=dev)
+    wd = w.to(dev)
+    _lib.call("moe_mxfp8_quant_cols_t", wd.data_ptr(), e, a, b, qt.data_ptr() + a, b * 2 * a, 2 * a,
+              stt.data_ptr() + a // 32, b * (2 * a // 32), 2 * a // 32, st)
+    qt, stt = qt.cpu(), stt.cpu()
+    for i in range(e):
+        rq, rs = R.quant_mxfp8(w[i].t())
+        assert torch.equal(qt[i, :, a:], rq.view(torch.uint8))
+        assert torch.equal(stt[i, :, a // 32:], rs)
+        assert torch.count_nonzero(qt[i, :, :a]) == 0 and torch.count_nonzero(stt[i, :, :a // 32]) == 0
+    # token groups, transposed and 32-padded, k-block-major scales
+    counts = torch.tensor([5, 0, 33, 32, 1, 64, 200], dtype=torch.int64)
+    r, c = int(counts.sum()), 128
+    xt = torch.randn(r, c, generator=g).bfloat16()
+    rpad = ops._mx_padded_rows(r, len(counts))
+    assert rpad % 32 == 0 and rpad >= r + 31 * len(counts)
+    q2, s2 = ops._mx_quant_tokens_t(xt.to(dev), counts.to(dev), len(counts), rpad)
+    q2, s2 = q2.cpu(), s2.cpu()
+    segs = [(int(counts[:i].sum()), int(n)) for i, n in enumerate(counts)]
+    rq2, rs2, _ = _tokens_t(xt, segs, rpad)
+    used = sum((n + 31) // 32 * 32 for _, n in segs)
+    assert torch.equal(q2[:, :used], rq2[:, :used])
+    assert torch.equal(s2[:used // 32], rs2[:used // 32])
+
+
+def test_mxfp8_gemm_entry_points_match_emulation(dev):
+    """Every MXFP8 GEMM kernel against R._mx_mm on identical quantized operands."""
+    banner("mxfp8 GEMM entry points")
+    from torchtitan_amd import _lib, ops
+
+    e, d, h, counts = 6, 256, 256, [40, 0, 130, 17, 64, 3]
+    gen = torch.Generator().manual_seed(2)
+    r = sum(counts)
+    cnt = torch.tensor(counts, dtype=torch.int64)
+
+    def rnd(*shape, scale=1.0):
+        # block-varying magnitudes so that neighbouring scales differ
+        t = torch.randn(*shape, generator=gen) * scale
+        return (t * torch.exp2(torch.randint(-3, 4, (*shape[:-1], shape[-1] // 32), generator=gen).float()
+                               ).repeat_interleave(32, -1)).bfloat16()
+    x = rnd(r, d)
+    w1, w3 = rnd(e, h, d, scale=0.05), rnd(e, h, d, scale=0.05)
+    w2 = rnd(e, d, h, scale=0.05)
+    dy = rnd(r, d)
+    gg, uu = rnd(r, h), rnd(r, h)
+    dgu = rnd(r, 2 * h)
+    hh = rnd(r, h)
+    st = torch.cuda.current_stream().cuda_stream
+    keep = []  # device copies must outlive the launches that read them
+
+    def P(t):
+        dt = t.to(dev).contiguous()
+        keep.append(dt)
+        return dt.data_ptr()
+    cd = cnt.to(dev)
+    segs = [(sum(counts[:i]), c) for i, c in enumerate(counts)]
+
+    def per_expert(fn):
+        return torch.cat([fn(i, slice(s0, s0 + c)) for i, (s0, c) in enumerate(segs)])
+
+    # gate_up
+    qx, sx = R.quant_mxfp8(x)
+    qw1, sw1 = R.quant_mxfp8(w1)
+    qw3, sw3 = R.quant_mxfp8(w3)
+    g_, u_, h_ = (torch.empty(r, h, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    _lib.call("moe_mxfp8_gemm_gate_up", P(_u8(qx)), P(sx), P(_u8(qw1)), P(sw1), P(_u8(qw3)), P(sw3), cd.data_ptr(),
+              r, e, d, h, g_.data_ptr(), u_.data_ptr(), h_.data_ptr(), st)
+    eg = per_expert(lambda i, sl: R._mx_mm(qx[sl], sx[sl], qw1[i], sw1[i]).bfloat16())
+    eu = per_expert(lambda i, sl: R._mx_mm(qx[sl], sx[sl], qw3[i], sw3[i]).bfloat16())
+    print(f"[case] gate_up g {_rel(g_, eg):.2e} u {_rel(u_, eu):.2e}", flush=True)
+    assert _rel(g_, eg) <= GEMM_TOL and _rel(u_, eu) <= GEMM_TOL
+    assert _rel(h_, F.silu(eg) * eu) <= GEMM_TOL
+    # down
+    qh, sh = R.quant_mxfp8(hh)
+    qw2, sw2 = R.quant_mxfp8(w2)
+    y_ = torch.empty(r, d, dtype=torch.bfloat16, device=dev)
+    _lib.call("moe_mxfp8_gemm_down", P(_u8(qh)), P(sh), P(_u8(qw2)), P(sw2), cd.data_ptr(), r, e, d, h,
+              y_.data_ptr(), st)
+    ey = per_expert(lambda i, sl: R._mx_mm(qh[sl], sh[sl], qw2[i], sw2[i]).bfloat16())
+    print(f"[case] down {_rel(y_, ey):.2e}", flush=True)
+    assert _rel(y_, ey) <= GEMM_TOL
+    # bwd dgu (dh checked through du = dh * bf16(silu(g)))
+    qdy, sdy = R.quant_mxfp8(dy)
+    qw2t, sw2t = zip(*(R.quant_mxfp8(w2[i].t()) for i in range(e)))
+    qw2t, sw2t = torch.stack(qw2t), torch.stack(sw2t)
+    dgu_ = torch.empty(r, 2 * h, dtype=torch.bfloat16, device=dev)
+    _lib.call("moe_mxfp8_gemm_bwd_dgu", P(_u8(qdy)), P(sdy), P(_u8(qw2t)), P(sw2t), P(gg), P(uu), cd.data_ptr(), r,
+              e, d, h, dgu_.data_ptr(), st)
+    dh = per_expert(lambda i, sl: R._mx_mm(qdy[sl], sdy[sl], qw2t[i], sw2t[i]).bfloat16())
+    assert _rel(dgu_[:, h:], dh * F.silu(gg)) <= GEMM_TOL
+    assert _rel(dgu_[:, :h], torch.ops.aten.silu_backward(dh * uu, gg)) <= GEMM_TOL
+    # bwd dx: [dg | du] blocked along 2H, w1^T and w3^T side by side
+    qdgu, sdgu = R.quant_mxfp8(dgu)
+    qw1t, sw1t = zip(*(R.quant_mxfp8(w1[i].t()) for i in range(e)))
+    qw3t, sw3t = zip(*(R.quant_mxfp8(w3[i].t()) for i in range(e)))
+    qw13t = torch.cat([torch.stack(qw1t).view(torch.uint8), torch.stack(qw3t).view(torch.uint8)], dim=2)
+    sw13t = torch.cat([torch.stack(sw1t), torch.stack(sw3t)], dim=2)
+    dx_ = torch.empty(r, d, dtype=torch.bfloat16, device=dev)
+    _lib.call("moe_mxfp8_gemm_bwd_dx", P(_u8(qdgu)), P(sdgu), P(qw13t), P(sw13t), cd.data_ptr(), r, e, d, h,
+              dx_.data_ptr(), st)
+    hb = h // 32
+    edx = per_expert(lambda i, sl: R._mx_mm(qdgu[sl, :h], sdgu[sl, :hb], qw1t[i], sw1t[i]).bfloat16()
+                     + R._mx_mm(qdgu[sl, h:], sdgu[sl, hb:], qw3t[i], sw3t[i]).bfloat16())
+    print(f"[case] dx {_rel(dx_, edx):.2e}", flush=True)
+    assert _rel(dx_, edx) <= GEMM_TOL
+    # bwd dw13 / dw2 from token-transposed, 32-padded operands
+    rpad = ops._mx_padded_rows(r, e)
+    qdgut, sdgut, ldgu = _tokens_t(dgu, segs, rpad)
+    qxt, sxt, lx = _tokens_t(x, segs, rpad)
+    dw1_, dw3_ = torch.empty_like(w1, device=dev), torch.empty_like(w3, device=dev)
+    _lib.call("moe_mxfp8_gemm_bwd_dw13", P(qdgut), P(sdgut), P(qxt), P(sxt), cd.data_ptr(), r, rpad, e, d, h,
+              dw1_.data_ptr(), dw3_.data_ptr(), st)
+    qdyt, sdyt, ldy = _tokens_t(dy, segs, rpad)
+    qht, sht, lh = _tokens_t(hh, segs, rpad)
+    dw2_ = torch.empty_like(w2, device=dev)
+    _lib.call("moe_mxfp8_gemm_bwd_dw2", P(qdyt), P(sdyt), P(qht), P(sht), cd.data_ptr(), r, rpad, e, d, h,
+              dw2_.data_ptr(), st)
+    for i, (s0, n) in enumerate(segs):
+        if n == 0:
+            for t in (dw1_, dw2_, dw3_):
+                assert torch.count_nonzero(t[i]) == 0
+            continue
+        (qa, sa), (qb, sb) = ldgu[i], lx[i]
+        edw = R._mx_mm(qa, sa, qb, sb).bfloat16()  # [2H, D]
+        errs = (_rel(dw1_[i], edw[:h]), _rel(dw3_[i], edw[h:]))
+        (qa, sa), (qb, sb) = ldy[i], lh[i]
+        errs += (_rel(dw2_[i], R._mx_mm(qa, sa, qb, sb).bfloat16()),)
+        print(f"[case] expert {i} ({n} tokens) dw1/dw3/dw2 " + " ".join(f"{v:.2e}" for v in errs), flush=True)
+        assert max(errs) <= GEMM_TOL, errs
+
+
+CASES = {
+    "ragged_e8": (8, 256, 512, [37, 0, 130, 16, 255, 1, 64, 100]),
+    "e16_d512_h256": (16, 512, 256, [96, 81, 0, 0, 200, 17, 33, 64, 128, 5, 70, 90, 300, 2, 0, 40]),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_mxfp8_grouped_swiglu_fwd_bwd(dev, name):
+    e, d, h, counts = CASES[name]
+    banner(f"mxfp8 grouped swiglu {name}")
+    from torchtitan_amd import ops
+
+    g = torch.Generator().manual_seed(1)
+    r = sum(counts)
+    x = torch.randn(r, d, generator=g).bfloat16()
+    w1 = (torch.randn(e, h, d, generator=g) * 0.05).bfloat16()
+    w2 = (torch.randn(e, d, h, generator=g) * 0.05).bfloat16()
+    w3 = (torch.randn(e, h, d, generator=g) * 0.05).bfloat16()
+    dy = torch.randn(r, d, generator=g).bfloat16()
+    cnt = torch.tensor(counts, dtype=torch.int64)
+    xs, a, b, c = (t.to(dev).requires_grad_(True) for t in (x, w1, w2, w3))
+    y, gg, uu, hh = ops.grouped_swiglu_mxfp8(xs, a, b, c, cnt.to(dev))
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    ey, eg, eu, eh = R.experts_mxfp8_forward(w1, w2, w3, x, cnt)
+    edx, edw1, edw2, edw3 = R.experts_mxfp8_backward(w1, w2, w3, x, cnt, eg, eu, eh, dy)
+    errs = {"y": _rel(y, ey), "g": _rel(gg, eg), "h": _rel(hh, eh), "dx": _rel(xs.grad, edx),
+            "dw1": _rel(a.grad, edw1), "dw2": _rel(b.grad, edw2), "dw3": _rel(c.grad, edw3)}
+    print(f"[case] {name} vs MXFP8 emulation: {errs}", flush=True)
+    assert all(v <= EMU_TOL for v in errs.values()), errs
+    for i, n in enumerate(counts):
+        if n == 0:
+            for t in (a.grad, b.grad, c.grad):
+                assert torch.count_nonzero(t[i]) == 0
+    xr, w1r, w2r, w3r = (t.float().requires_grad_(True) for t in (x, w1, w2, w3))
+    ys, start = [], 0
+    for i, n in enumerate(counts):
+        xe = xr[start:start + n]
+        ys.append((F.silu(xe @ w1r[i].t()) * (xe @ w3r[i].t())) @ w2r[i].t())
+        start += n
+    yr = torch.cat(ys)
+    yr.backward(dy.float())
+    loose = {"y": _rel(y, yr), "dx": _rel(xs.grad, xr.grad), "dw1": _rel(a.grad, w1r.grad),
+             "dw2": _rel(b.grad, w2r.grad), "dw3": _rel(c.grad, w3r.grad)}
+    print(f"[case] {name} vs fp32 reference: {loose}", flush=True)
+    assert all(v <= BF16_TOL for v in loose.values()), loose

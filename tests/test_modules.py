@@ -144,6 +144,22 @@ def test_float8_converter_selects_experts_by_fqn():
     assert Float8GroupedMMConverter.Config(fqns="experts").build().fqns == ["experts"]
 
 
+def test_mxfp8_converter_selects_experts_by_fqn():
+    from torchtitan_amd.quantization import MXFP8Converter, find_pad_multiple
+
+    model = torch.nn.ModuleDict({"a": _cfg(hs=0).build(), "b": _cfg(hs=0).build()})
+    conv_cfg = MXFP8Converter.Config(fqns="b.experts")
+    conv = conv_cfg.build()
+    assert conv.recipe_name == "mxfp8_rceil"
+    assert conv.convert(model) == ["b.experts"]
+    assert model["b"].experts.mxfp8 and not model["a"].experts.mxfp8
+    assert not model["b"].experts.float8
+    assert set(model["a"].state_dict()) == set(model["b"].state_dict())
+    assert find_pad_multiple([conv_cfg]) == 32
+    with pytest.raises(ValueError):
+        MXFP8Converter.Config(recipe_name="mxfp8_floor").build()
+
+
 def test_load_balancing_hook_registration_follows_reference_rules():
     """register_moe_load_balancing_hook registers only when the MoE layers have a
     coefficient (optimizer.py:352-362, 439-444); the walk goes layers -> block.moe."""

@@ -17,7 +17,12 @@ What fixes each function, independently of the formula being checked:
   * router gradients: float64 finite differences;
   * moe_forward: the reference op sequence (moe_forward_reference_ops) on the CPU;
   * expert_bias_update: closed forms on hand-worked loads (balanced, one hot
-    expert, ties with the mean, the recomputation halving).
+    expert, ties with the mean, the recomputation halving);
+  * quant_mxfp8 / _mx_mm: an independent bit-level derivation of the RCEIL
+    exponent (biased exponent of amax / 448, +1 for a non-zero mantissa),
+    hand-worked blocks, values on the e4m3 grid that must round-trip exactly,
+    power-of-two equivariance, the e4m3 rounding bound, and exact GEMMs of
+    grid values whose blocks carry different scales.
 The GPU-lowering rules the oracle states (top-k tie order, deterministic
 scatter-add order, index-backward rounding, short-row sum order) are pinned
 against torch on the device in tests/test_gpu_oracle_pins.py.
@@ -453,3 +458,139 @@ def test_permute_pad_layout_reduces_to_the_unpadded_permute(pad):
             assert np.all(grp[ntok[e]:] == n_in) and np.all(grp[:ntok[e]] != n_in)
         if pad == 1:
             assert np.array_equal(pidx, idx)
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 quantization (torchao's to_mx, RCEIL) and the MX GEMM emulation
+# ---------------------------------------------------------------------------
+
+
+def _rceil_bits(amax: float) -> int:
+    """RCEIL e8m0 exponent from the fp32 bits of amax / 448: the biased exponent,
+    plus one when the mantissa is non-zero; subnormals above 2^-127 give 1."""
+    d = np.float32(amax) / np.float32(448.0)
+    if np.isnan(d):
+        return 255
+    b = int(np.array([d], dtype=np.float32).view(np.uint32)[0])
+    if b >= 0x7F800000:
+        return 254
+    ex, man = b >> 23, b & 0x7FFFFF
+    if ex == 0:
+        return 1 if man > 0x400000 else 0
+    return min(ex + (man != 0), 254)
+
+
+def _e4m3_grid() -> torch.Tensor:
+    """Every finite non-negative float8_e4m3fn value (bytes 0x00..0x7e)."""
+    return torch.arange(0, 0x7F, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+
+
+def test_mx_exponent_matches_bit_derivation():
+    g = torch.Generator().manual_seed(0)
+    vals = [0.0, 448.0, 449.0, 450.0, 447.0, 1.0, 3.5, 224.0, 896.0]
+    vals += [448.0 * 2.0 ** k for k in range(-125, 120, 7)]
+    vals += (torch.randn(400, generator=g).abs() * torch.exp2(torch.randint(-120, 110, (400,), generator=g).float())
+             ).bfloat16().float().tolist()
+    vals += [2.0 ** -120, 2.0 ** -126 * 448.0 * 1.5, 2.0 ** -127 * 448.0]
+    x = torch.zeros(len(vals), 32)
+    x[:, 5] = torch.tensor(vals)
+    _, e = R.quant_mxfp8(x.bfloat16())
+    bf = x.bfloat16().float()[:, 5]
+    want = torch.tensor([_rceil_bits(v) for v in bf.tolist()], dtype=torch.uint8)
+    assert torch.equal(e.view(-1), want)
+
+
+def test_mx_hand_worked_blocks():
+    x = torch.zeros(4, 64)
+    x[0, 0], x[0, 1], x[0, 2] = 448.0, 1.0, -3.0   # amax 448: e = 127, values kept
+    x[1, 0], x[1, 1] = 450.0, 3.0                  # 450 / 448 > 1: e = 128, values halved
+    x[1, 40] = 0.5                                 # second block: 0.5 / 448 = 2^-9.8 -> ceil -9 -> e = 118
+    x[2, 33] = 2.0 ** -120                         # ceil(log2) < -127: e = 0 and multiplier 1 -> q = 0
+    q, e = R.quant_mxfp8(x.bfloat16())
+    qf = q.float()
+    assert e.tolist() == [[127, 0], [128, 118], [0, 0], [0, 0]]
+    assert qf[0, :3].tolist() == [448.0, 1.0, -3.0]
+    assert qf[1, :2].tolist() == [224.0, 1.5]      # 225 rounds to the e4m3 step 224
+    assert qf[1, 40].item() == 256.0               # 0.5 * 2^9
+    assert torch.count_nonzero(qf[2]) == 0 and torch.count_nonzero(qf[3]) == 0
+    nan = torch.zeros(1, 32)
+    nan[0, 3] = float("nan")
+    assert R.quant_mxfp8(nan.bfloat16())[1].item() == 255
+
+
+def test_mx_grid_round_trip_and_equivariance():
+    grid = _e4m3_grid()
+    g = torch.Generator().manual_seed(1)
+    blocks = grid[torch.randint(0, len(grid), (64, 32), generator=g)] * torch.where(
+        torch.rand(64, 32, generator=g) < 0.5, -1.0, 1.0)
+    blocks[:, 7] = 448.0  # amax 448: e = 127, grid values are exact
+    q, e = R.quant_mxfp8(blocks.bfloat16())
+    assert torch.equal(e, torch.full((64, 1), 127, dtype=torch.uint8))
+    assert torch.equal(q.float(), blocks)
+    for k in (-100, -7, 1, 60):
+        qk, ek = R.quant_mxfp8((blocks * 2.0 ** k).bfloat16())
+        assert torch.equal(qk.float(), blocks) and torch.equal(ek.long(), e.long() + k)
+
+
+def test_mx_rounding_bound_and_block_locality():
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(50, 256, generator=g) * torch.exp(torch.randn(50, 8, generator=g) * 4).repeat_interleave(32, 1)
+         ).bfloat16()
+    q, e = R.quant_mxfp8(x)
+    deq = R.mx_dequant(q, e)
+    xf = x.double()
+    step = torch.ldexp(torch.ones(e.shape, dtype=torch.float64), e.double() - 127 - 10).repeat_interleave(32, 1)
+    assert ((deq - xf).abs() <= torch.maximum(xf.abs() * 2.0 ** -4, step)).all()
+    # blocks along the other dimension: the transposed quantization
+    qt, et = R.quant_mxfp8(x.t().contiguous(), dim=0)
+    assert torch.equal(qt.float(), q.float().t()) and torch.equal(et, e.t())
+    # changing one element moves only its own block's scale
+    y = x.clone()
+    y[3, 70] = 1e4
+    _, e2 = R.quant_mxfp8(y)
+    diff = (e2 != e).nonzero().tolist()
+    assert diff == [[3, 2]]
+
+
+def test_mx_mm_exact_on_grid_values_with_block_scales():
+    grid = _e4m3_grid()
+    g = torch.Generator().manual_seed(3)
+    a = grid[torch.randint(0, len(grid), (5, 96), generator=g)]
+    b = grid[torch.randint(0, len(grid), (7, 96), generator=g)] * -1.0
+    a[:, 0::32] = 448.0
+    b[:, 0::32] = -448.0
+    ka = torch.tensor([-3.0, 0.0, 5.0]).repeat_interleave(32)  # different power-of-two per block
+    kb = torch.tensor([2.0, -6.0, 1.0]).repeat_interleave(32)
+    xa, xb = a * torch.exp2(ka), b * torch.exp2(kb)
+    qa, sa = R.quant_mxfp8(xa.bfloat16())
+    qb, sb = R.quant_mxfp8(xb.bfloat16())
+    assert sa[0].tolist() == [124, 127, 132] and sb[0].tolist() == [129, 121, 128]
+    assert torch.equal(R.mx_dequant(qa, sa), xa.double()) and torch.equal(R.mx_dequant(qb, sb), xb.double())
+    assert torch.equal(R._mx_mm(qa, sa, qb, sb), (xa.double() @ xb.double().t()).float())
+
+
+def test_mx_experts_close_to_bf16_reference():
+    g = torch.Generator().manual_seed(4)
+    e, d, h, counts = 3, 64, 96, [20, 0, 45]
+    r = sum(counts)
+    x = torch.randn(r, d, generator=g).bfloat16()
+    w1, w3 = ((torch.randn(e, h, d, generator=g) * 0.1).bfloat16() for _ in range(2))
+    w2 = (torch.randn(e, d, h, generator=g) * 0.1).bfloat16()
+    dy = torch.randn(r, d, generator=g).bfloat16()
+    cnt = torch.tensor(counts)
+    y, g_, u_, h_ = R.experts_mxfp8_forward(w1, w2, w3, x, cnt)
+    dx, dw1, dw2, dw3 = R.experts_mxfp8_backward(w1, w2, w3, x, cnt, g_, u_, h_, dy)
+    xr, w1r, w2r, w3r = (t.double().requires_grad_(True) for t in (x, w1, w2, w3))
+    ys, s0 = [], 0
+    for i, c in enumerate(counts):
+        xe = xr[s0:s0 + c]
+        ys.append((F.silu(xe @ w1r[i].t()) * (xe @ w3r[i].t())) @ w2r[i].t())
+        s0 += c
+    yr = torch.cat(ys)
+    yr.backward(dy.double())
+
+    def rel(a, b):
+        return ((a.double() - b).abs().max() / b.abs().max()).item()
+    errs = [rel(y, yr.detach()), rel(dx, xr.grad), rel(dw1, w1r.grad), rel(dw2, w2r.grad), rel(dw3, w3r.grad)]
+    assert max(errs) < 0.1, errs
+    assert torch.count_nonzero(dw1[1]) == 0 and torch.count_nonzero(dw2[1]) == 0

@@ -52,13 +52,24 @@ SIGNATURES: dict[str, list] = {
     "moe_fp8_gemm_bwd_dx": [P, P, P, P, P, I64, I32, I32, I32, P, P],
     "moe_fp8_gemm_bwd_dw13": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P, P],
     "moe_fp8_gemm_bwd_dw2": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P],
+    "moe_mxfp8_padded_rows": [I64, I32],
+    "moe_mxfp8_quant_rows": [P, I64, I32, P, P, P],
+    "moe_mxfp8_quant_cols_t": [P, I32, I32, I32, P, I64, I64, P, I64, I64, P],
+    "moe_mxfp8_quant_tokens_t": [P, P, I64, I32, I32, I64, P, P, P],
+    "moe_mxfp8_gemm_gate_up": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
+    "moe_mxfp8_gemm_down": [P, P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_mxfp8_gemm_bwd_dgu": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_mxfp8_gemm_bwd_dx": [P, P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_mxfp8_gemm_bwd_dw13": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P, P],
+    "moe_mxfp8_gemm_bwd_dw2": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P],
     "moe_expert_bias_update": [P, P, P, P, I32, I32, P],
     "moe_ep_permute_indices": [P, I32, I32, I64, P, P, P],
     "moe_ep_permute_pad_indices": [P, I32, I32, I32, I64, P, P, P, P],
     "moe_gather_rows": [P, I64, P, I64, I32, I32, P, P],
     "moe_scatter_rows": [P, P, I64, I32, I32, P, I64, P],
 }
-_RESTYPES = {"moe_reorder_workspace_bytes": ctypes.c_int64, "moe_fp8_padded_rows": ctypes.c_int64}
+_RESTYPES = {"moe_reorder_workspace_bytes": ctypes.c_int64, "moe_fp8_padded_rows": ctypes.c_int64,
+             "moe_mxfp8_padded_rows": ctypes.c_int64}
 
 _ERRORS = {
     -1: "invalid argument",

@@ -29,6 +29,22 @@
 // chunks (lane >> 4) and 4 + (lane >> 4) of its row (any k order is valid as
 // long as both operands share it). Rows past a segment and k past a padded
 // token group are copied from a zero row.
+//
+// MXFP8 (torchao's MXFP8TrainingOpConfig, recipe "mxfp8_rceil", converted by
+// torchtitan/components/quantization/mx.py:25-128; token groups padded to 32,
+// quantization/__init__.py:36-40) uses the same kernels with one e8m0 scale
+// per 32 consecutive k of every row:
+//  * scale exponent e = clamp(ceil(log2(amax / 448)), -127, 127) + 127 (NaN
+//    -> 255), elements q = e4m3fn(clamp(x * 2^(127 - e), +-448)), with x * 1
+//    when e == 0 (torchao's RCEIL derivation);
+//  * the MFMA applies the two scales itself: in the fragment layout above lane
+//    group g holds k [16 g, +16) and [64 + 16 g, +16) of its row, and the
+//    instruction's 32-k scale block b is k [32 b, 32 b + 32) with its scale
+//    taken from lane group b of that row, so lane (row, g) passes the scale
+//    of k-block 4 kt + g;
+//  * scales reach LDS by direct-to-LDS copies next to the data: rows x 4
+//    bytes (one dword = the 4 k-blocks of a 128-k stage) for row-grouped
+//    operands, k-block x 16 rows for token-transposed ones.
 #include "common.h"
 
 namespace moe {
@@ -67,6 +83,29 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 __device__ __forceinline__ float scale_of(float amax) { return fmaxf(amax, 1e-12f) / kFp8Max; }
+
+constexpr int kMxBlock = 32;  // MXFP8 scaling block (k elements per e8m0 scale)
+constexpr int kMxPad = 32;    // MXFP8 token-group alignment
+
+// e8m0 exponent of an MX block from its amax (RCEIL):
+// clamp(ceil(log2(amax / 448)), -127, 127) + 127, 255 for NaN.
+__device__ __forceinline__ uint32_t mx_exponent(float amax) {
+  const float d = amax / kFp8Max;
+  if (d != d) return 255u;
+  const uint32_t b = __float_as_uint(d);
+  if (b >= 0x7f800000u) return 254u;
+  const uint32_t ex = b >> 23, man = b & 0x7fffffu;
+  if (ex == 0) return man > 0x400000u ? 1u : 0u;  // subnormal: above 2^-127 rounds up to 2^-126
+  const uint32_t e = ex + (man != 0u);
+  return e > 254u ? 254u : e;
+}
+
+// the element multiplier 2^(127 - e) (1 when e == 0)
+__device__ __forceinline__ float mx_multiplier(uint32_t e) {
+  if (e == 0) return 1.0f;
+  if (e <= 253u) return __uint_as_float((254u - e) << 23);
+  return __uint_as_float(0x400000u >> (e - 254u));  // 2^-127, 2^-128 (subnormal)
+}
 
 // ---------------------------------------------------------------------------
 // quantizers
@@ -273,6 +312,152 @@ __global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __r
 }
 
 // ---------------------------------------------------------------------------
+// MXFP8 quantizers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint2 mx_quant8(uint4 v, float f) {
+  const uint32_t lo = e4m3(bf_lo(v.x) * f) | (e4m3(bf_hi(v.x) * f) << 8) | (e4m3(bf_lo(v.y) * f) << 16) |
+                      (e4m3(bf_hi(v.y) * f) << 24);
+  const uint32_t hi = e4m3(bf_lo(v.z) * f) | (e4m3(bf_hi(v.z) * f) << 8) | (e4m3(bf_lo(v.w) * f) << 16) |
+                      (e4m3(bf_hi(v.w) * f) << 24);
+  return make_uint2(lo, hi);
+}
+
+// x viewed as n_chunks 16-byte chunks of 8 bf16 (rows of K, K % 32 == 0): four
+// consecutive lanes hold one 32-element block, reduce its amax by shuffles
+// and write one e8m0 byte (block index = chunk / 4, i.e. scale [rows][K/32]).
+// Four chunks per thread are loaded before any is processed.
+__global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint4* __restrict__ x, int64_t n_chunks,
+                                                            uint2* __restrict__ q, uint8_t* __restrict__ scale) {
+  const int64_t S = (int64_t)gridDim.x * 256;
+  for (int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x; c0 - threadIdx.x < n_chunks; c0 += 4 * S) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = c0 + u * S;
+      v[u] = c < n_chunks ? x[c] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = c0 + u * S;
+      float a = amax8(v[u]);
+      a = fmaxf(a, __shfl_xor(a, 1));
+      a = fmaxf(a, __shfl_xor(a, 2));
+      const uint32_t e = mx_exponent(a);
+      if (c < n_chunks) {
+        q[c] = mx_quant8(v[u], mx_multiplier(e));
+        if ((c & 3) == 0) scale[c >> 2] = (uint8_t)e;
+      }
+    }
+  }
+}
+
+// MX counterpart of slab_transpose_quant: a [rows x 64] bf16 slab becomes 64
+// output rows of fp8 along the slab's rows, one e8m0 scale per 32 of them.
+// Scale of (slab column b, block k) at sc + b * sc_b + k * sc_k. Rows >=
+// n_rows up to n_out (a multiple of 32) are zero.
+__device__ __forceinline__ void mx_slab_transpose_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows,
+                                                        int n_out, uint8_t* __restrict__ out, int64_t ldo,
+                                                        uint8_t* __restrict__ sc, int64_t sc_b, int64_t sc_k,
+                                                        uint16_t (*s_tile)[kSlabRows + 2]) {
+  const int t = threadIdx.x;
+  for (int a0 = 0; a0 < n_out; a0 += kSlabRows) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = t + i * 256;
+      const int r = c >> 3, ch = c & 7;
+      v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = t + i * 256;
+      const int r = c >> 3, ch = c & 7;
+      const uint16_t* pv = (const uint16_t*)&v[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_tile[ch * 8 + j][r] = pv[j];
+    }
+    __syncthreads();
+    // thread -> (column b, one 32-row block)
+    const int b = t >> 2, rr = (t & 3) * kMxBlock;
+    if (a0 + rr < n_out) {
+      const uint32_t* row = (const uint32_t*)&s_tile[b][rr];  // 4-byte aligned: row stride 260 bytes, rr even
+      uint32_t w[16];
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        w[i] = row[i];
+        a = fmaxf(a, fmaxf(fabsf(bf_lo(w[i])), fabsf(bf_hi(w[i]))));
+      }
+      const uint32_t e = mx_exponent(a);
+      const float f = mx_multiplier(e);
+      uint32_t o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        o[i] = e4m3(bf_lo(w[2 * i]) * f) | (e4m3(bf_hi(w[2 * i]) * f) << 8) | (e4m3(bf_lo(w[2 * i + 1]) * f) << 16) |
+               (e4m3(bf_hi(w[2 * i + 1]) * f) << 24);
+      uint8_t* dst = out + (int64_t)b * ldo + a0 + rr;
+      *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
+      *(uint4*)(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+      sc[(int64_t)b * sc_b + (int64_t)((a0 + rr) / kMxBlock) * sc_k] = (uint8_t)e;
+    }
+    __syncthreads();
+  }
+}
+
+// x [E][A][B] -> q rows (e, b) of A values at q + e * q_estride + b * q_ld, and
+// their A/32 scales at s + e * s_estride + b * s_ld. Block per (e, 64 columns).
+__global__ __launch_bounds__(256) void mx_quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
+                                                              uint8_t* __restrict__ q, int64_t q_estride,
+                                                              int64_t q_ld, uint8_t* __restrict__ s,
+                                                              int64_t s_estride, int64_t s_ld) {
+  __shared__ uint16_t s_tile[64][kSlabRows + 2];
+  const int nb = B / 64;
+  const int64_t e = blockIdx.x / nb;
+  const int b0 = (blockIdx.x % nb) * 64;
+  mx_slab_transpose_quant(x + e * A * (int64_t)B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
+                          s + e * s_estride + b0 * s_ld, s_ld, 1, s_tile);
+}
+
+// x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
+// 32-aligned offset pstart_e, zero padded to ceil32(count_e)) and the scales
+// k-block major, s [Rpad / 32][C]. Block per (e, 64 columns); empty groups exit.
+__global__ __launch_bounds__(256) void mx_quant_tokens_t_kernel(const uint16_t* __restrict__ x,
+                                                                const int64_t* __restrict__ counts, int64_t R, int E,
+                                                                int C, int64_t Rpad, uint8_t* __restrict__ q,
+                                                                uint8_t* __restrict__ s) {
+  __shared__ uint16_t s_tile[64][kSlabRows + 2];
+  __shared__ int s_tmp[8];
+  __shared__ int s_seg[3];
+  const int nc = C / 64;
+  const int e = blockIdx.x / nc;
+  const int c0 = (blockIdx.x % nc) * 64;
+  {
+    int cnt[4], pc[4], st[4], pst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ee = threadIdx.x * 4 + i;
+      const int64_t c = ee < E ? counts[ee] : 0;
+      cnt[i] = c < 0 ? 0 : (int)(c > R ? R : c);
+      pc[i] = (cnt[i] + kMxPad - 1) / kMxPad * kMxPad;
+    }
+    block_exclusive_scan4(cnt, st, s_tmp);
+    block_exclusive_scan4(pc, pst, s_tmp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (threadIdx.x * 4 + i == e) { s_seg[0] = st[i]; s_seg[1] = pst[i]; s_seg[2] = cnt[i]; }
+    __syncthreads();
+  }
+  const int seg0 = s_seg[0], pstart = s_seg[1];
+  int n = s_seg[2];
+  if ((int64_t)seg0 + n > R) n = (int)(R - seg0 > 0 ? R - seg0 : 0);
+  const int n_out = (n + kMxPad - 1) / kMxPad * kMxPad;
+  if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
+  mx_slab_transpose_quant(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
+                          s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C, s_tile);
+}
+
+// ---------------------------------------------------------------------------
 // fp8 grouped GEMM
 // ---------------------------------------------------------------------------
 enum Mode : int { kGateUp = 0, kDown = 1, kDgu = 2, kDx = 3, kDw13 = 4, kDw2 = 5 };
@@ -292,6 +477,9 @@ struct Params {
   uint16_t* o0;  // outputs (mode dependent)
   uint16_t* o1;
   uint16_t* o2;
+  const uint8_t* ep;   // MXFP8: e8m0 scales of P, Q and the second Q operand
+  const uint8_t* eq;
+  const uint8_t* eq2;
 };
 
 #define LDSP __attribute__((address_space(3)))
@@ -306,17 +494,32 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* ptr) { return (uint3
 // 16-byte chunk c of row r; conflict-free for fragment reads of 16 rows.
 __device__ __forceinline__ int rm_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
+// One wave-wide 4-byte direct-to-LDS copy: lane i's dword lands at lds + 4 i.
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, off" :: "v"(g), "{m0}"(lds) : "memory");
+}
+
 __device__ const uint4 kZeroRow[64] = {};  // source of zero rows and k past a segment
+// e8m0 127 (= 1.0) scales for rows past a segment and k-blocks past a group
+__device__ const uint4 kUnitScales[1] = {{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu}};
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
-template <int MODE, int BM, int BN, int OCC>
+// MX: e8m0 block scales (p.ep / p.eq / p.eq2) applied by the MFMA instead of
+// the fp32 row scales of the epilogues; token groups aligned to 32.
+template <int MODE, int BM, int BN, int OCC, bool MX>
 __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
   constexpr bool kRowGrouped = MODE <= kDx;
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
   constexpr int CPW_P = BM / 8 / 4, CPW_Q = BN / 8 / 4;  // 1 KB copies (8 rows x 128 B) per wave and stage
+  constexpr int PAD = MX ? kMxPad : kPad;
+  static_assert(!MX || (BM == 128 && BN == 128), "the MX scale copies assume 128 x 128 tiles");
   __shared__ __attribute__((aligned(1024))) uint8_t sP[2][BM * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ[2][BN * 128];
+  // MX scales of a stage: row-grouped, P row m's 4 k-blocks at 4 m and Q row n's
+  // at 512 + 4 n; token-transposed, k-block j of P row m at 128 j + m, of Q
+  // row n at 512 + 128 j + n
+  __shared__ __attribute__((aligned(16))) uint8_t sS[2][MX ? 1024 : 16];
   __shared__ int s_seg[kMaxE + 1];
   __shared__ int s_pst[kMaxE + 1];
   __shared__ int s_tile[kMaxE + 1];
@@ -350,7 +553,7 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         const int64_t lo = pre[i] < p.R ? pre[i] : p.R;
         const int64_t hi = (int64_t)pre[i] + cnt[i] < p.R ? (int64_t)pre[i] + cnt[i] : p.R;
         cnt[i] = (int)(hi - lo);
-        pc[i] = (cnt[i] + kPad - 1) / kPad * kPad;
+        pc[i] = (cnt[i] + PAD - 1) / PAD * PAD;
       }
     }
 #pragma unroll
@@ -438,6 +641,44 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
       }
       srcQ[b] = rowp + chQ[b];
     }
+    // MX scale copy source of this lane (row-grouped: one dword copy per wave,
+    // waves 0-1 P rows, 2-3 Q rows; token-transposed: one 16-byte copy by wave 0,
+    // lanes 0-31 P, 32-63 Q, each 16 rows of k-block 4 kt + (lane & 31) / 8)
+    const uint8_t* srcS = nullptr;
+    bool okS = false;
+    int64_t kstrideS = 0;
+    if (MX) {
+      if (kRowGrouped) {
+        const int kb_row = Kfix / kMxBlock;  // scale bytes per row
+        if (wv < 2) {
+          const int r = row0 + wv * 64 + lane;
+          okS = r < seg1;
+          srcS = p.ep + (int64_t)r * kb_row;
+        } else {
+          const int n = (wv - 2) * 64 + lane;
+          okS = true;
+          int64_t qrow;
+          const uint8_t* base = p.eq;
+          if (MODE == kGateUp) {
+            const int blk = n >> 4;
+            qrow = e64 * H + nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
+            if (blk & 1) base = p.eq2;
+          } else if (MODE == kDown) {
+            qrow = e64 * D + nt * BN + n;
+          } else if (MODE == kDgu) {
+            qrow = e64 * H + nt * BN + n;
+          } else {
+            qrow = e64 * D + nt * BN + n;
+          }
+          srcS = base + qrow * kb_row;
+        }
+      } else {
+        const int sub = lane & 31;
+        const int64_t kb0 = pst0 / kMxBlock + (sub >> 3);
+        kstrideS = lane < 32 ? Mfix : Ntot;
+        srcS = (lane < 32 ? p.ep + kb0 * Mfix + mt * BM : p.eq + kb0 * Ntot + nt * BN) + (sub & 7) * 16;
+      }
+    }
     auto issue = [&](int kt) {
       const int s = kt & 1;
       const int k0 = kt * 128;
@@ -451,6 +692,14 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         const bool ok = k0 + chQ[b] < Klen;
         dma16(ok ? (const void*)(srcQ[b] + k0) : (const void*)kZeroRow, lds_addr(&sQ[s][(wv * CPW_Q + b) * 1024]));
       }
+      if (MX) {
+        if (kRowGrouped) {
+          dma4(okS ? (const void*)(srcS + kt * 4) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 256]));
+        } else if (wv == 0) {
+          const bool ok = (4 * kt + ((lane & 31) >> 3)) * kMxBlock < Klen;
+          dma16(ok ? (const void*)(srcS + 4 * kt * kstrideS) : (const void*)kUnitScales, lds_addr(&sS[s][0]));
+        }
+      }
     };
 
     f32x4_t acc[TM][TN];
@@ -461,6 +710,19 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
 
     const int ml = lane & 15, nql = (lane >> 4) * 4, g4 = lane >> 4;
     auto compute = [&](int s) {
+      int scp[TM], scq[TN];
+      if (MX) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int m = wm * WM + i * 16 + ml;
+          scp[i] = sS[s][kRowGrouped ? m * 4 + g4 : g4 * 128 + m];
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = wn * WN + j * 16 + ml;
+          scq[j] = sS[s][kRowGrouped ? 512 + n * 4 + g4 : 512 + g4 * 128 + n];
+        }
+      }
       v8i_t af[TM];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -477,7 +739,8 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         const v8i_t bq = v8i_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq, af[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq, af[i], acc[i][j], 0, 0, 0,
+                                                                       MX ? scq[j] : 127, 0, MX ? scp[i] : 127);
       }
     };
 
@@ -491,10 +754,15 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         for (int j = 0; j < TN; ++j) {
           if (r < seg1) {
             const int n = nt * BN + wn * WN + j * 16 + nql;
-            const float sp = p.sp[(int64_t)r * 2];
             float v[4];
+            if (MX) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * p.sq[e64 * 2 * D + n + q];
+              for (int q = 0; q < 4; ++q) v[q] = acc[i][j][q];
+            } else {
+              const float sp = p.sp[(int64_t)r * 2];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * p.sq[e64 * 2 * D + n + q];
+            }
             *(uint2*)(p.o0 + (int64_t)r * D + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
           }
           acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -520,15 +788,15 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
-          const float sx = p.sp[r];
+          const float sx = MX ? 1.f : p.sp[r];
 #pragma unroll
           for (int jj = 0; jj < TN / 2; ++jj) {
             const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nql;
             float gv[4], uv[4], hv[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              gv[q] = round_bf((acc[i][2 * jj][q] * sx) * p.sq[e64 * H + hc + q]);
-              uv[q] = round_bf((acc[i][2 * jj + 1][q] * sx) * p.sq2[e64 * H + hc + q]);
+              gv[q] = round_bf(MX ? acc[i][2 * jj][q] : (acc[i][2 * jj][q] * sx) * p.sq[e64 * H + hc + q]);
+              uv[q] = round_bf(MX ? acc[i][2 * jj + 1][q] : (acc[i][2 * jj + 1][q] * sx) * p.sq2[e64 * H + hc + q]);
               hv[q] = round_bf(silu_f(gv[q])) * uv[q];
             }
             const int64_t off = (int64_t)r * H + hc;
@@ -543,15 +811,20 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
-          const float sp = (MODE == kDx) ? p.sp[(int64_t)r * 2 + 1] : p.sp[r];
+          const float sp = MX ? 1.f : ((MODE == kDx) ? p.sp[(int64_t)r * 2 + 1] : p.sp[r]);
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int n = nt * BN + wn * WN + j * 16 + nql;
             uint16_t* dst = p.o0 + (int64_t)r * D + n;
-            const float* sq = (MODE == kDx) ? p.sq + e64 * 2 * D + D + n : p.sq + e64 * D + n;
             float v[4];
+            if (MX) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * sq[q];
+              for (int q = 0; q < 4; ++q) v[q] = acc[i][j][q];
+            } else {
+              const float* sq = (MODE == kDx) ? p.sq + e64 * 2 * D + D + n : p.sq + e64 * D + n;
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * sq[q];
+            }
             if (MODE == kDx) {
               const uint2 pw = *(const uint2*)dst;
               v[0] = bf_lo(pw.x) + round_bf(v[0]);
@@ -568,7 +841,7 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
-          const float sp = p.sp[r];
+          const float sp = MX ? 1.f : p.sp[r];
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int hh = nt * BN + wn * WN + j * 16 + nql;
@@ -580,7 +853,7 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
             float dg[4], du[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const float dh = round_bf((acc[i][j][q] * sp) * p.sq[e64 * H + hh + q]);
+              const float dh = round_bf(MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * H + hh + q]);
               const float sl = round_bf(silu_f(gv[q]));
               const float dsl = round_bf(dh * uv[q]);
               du[q] = dh * sl;
@@ -598,7 +871,7 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
       for (int i = 0; i < TM; ++i) {
         const int m = mt * BM + wm * WM + i * 16 + ml;
         // an expert without tokens gets zero gradients (its scales are never written)
-        const float sp = (nk > 0) ? p.sp[e64 * Mfix + m] : 0.f;
+        const float sp = (nk > 0) ? (MX ? 1.f : p.sp[e64 * Mfix + m]) : 0.f;
         uint16_t* rowp;
         if (MODE == kDw13)
           rowp = (m < H) ? p.o0 + (e64 * H + m) * (int64_t)D : p.o1 + (e64 * H + (m - H)) * (int64_t)D;
@@ -609,7 +882,8 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
           const int n = nt * BN + wn * WN + j * 16 + nql;
           float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = (nk > 0) ? (acc[i][j][q] * sp) * p.sq[e64 * Ntot + n + q] : 0.f;
+          for (int q = 0; q < 4; ++q)
+            v[q] = (nk > 0) ? (MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * Ntot + n + q]) : 0.f;
           *(uint2*)(rowp + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
         }
       }
@@ -631,7 +905,7 @@ static int cu_count() {
 
 constexpr int kBM = 128, kBN = 128, kOcc = 2;
 
-template <int MODE>
+template <int MODE, bool MX = false>
 static void launch(const Params& p, hipStream_t stream) {
   int64_t max_tiles;
   if (MODE == kGateUp) max_tiles = (p.R / kBM + p.E) * (2 * p.H / kBN);
@@ -643,7 +917,7 @@ static void launch(const Params& p, hipStream_t stream) {
   if (g > max_tiles) g = max_tiles;
   if (g >= 8) g -= g % 8;
   if (g < 1) g = 1;
-  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, kBM, kBN, kOcc>), dim3((int)g), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, kBM, kBN, kOcc, MX>), dim3((int)g), dim3(kThreads), 0, stream, p);
 }
 
 static int check_shape(int64_t R, int E, int D, int H) {
@@ -795,5 +1069,133 @@ MOE_API int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const u
   if (!dw2 || (n_rows > 0 && (!qdyt || !sdyt || !qht || !sht))) return kErrInvalidArgument;
   p.Rpad = padded_rows; p.qp = qdyt; p.sp = sdyt; p.qq = qht; p.sq = sht; p.o0 = dw2;
   launch<kDw2>(p, stream);
+  return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// MXFP8 entry points (e8m0 scales as uint8 bytes)
+// ---------------------------------------------------------------------------
+
+MOE_API int64_t moe_mxfp8_padded_rows(int64_t n_rows, int32_t n_experts) {
+  const int64_t n = n_rows + (int64_t)n_experts * (kMxPad - 1);
+  return (n + kMxPad - 1) / kMxPad * kMxPad;
+}
+
+MOE_API int moe_mxfp8_quant_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q, uint8_t* scale,
+                                 hipStream_t stream) {
+  if (rows < 0 || cols < kMxBlock || cols % kMxBlock) return kErrInvalidArgument;
+  if (rows == 0) return kOk;
+  if (!x || !q || !scale) return kErrInvalidArgument;
+  const int64_t chunks = rows * (cols / 8);
+  int64_t g = (chunks + 4 * 256 - 1) / (4 * 256);
+  if (g > 32768) g = 32768;
+  hipLaunchKernelGGL(mx_quant_rows_kernel, dim3((int)g), dim3(256), 0, stream, (const uint4*)x, chunks, (uint2*)q,
+                     scale);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
+                                   int64_t q_expert_stride, int64_t q_row_stride, uint8_t* scale,
+                                   int64_t scale_expert_stride, int64_t scale_row_stride, hipStream_t stream) {
+  if (n_experts < 1 || a < kMxBlock || a % kMxBlock || b < 64 || b % 64) return kErrInvalidArgument;
+  if (q_row_stride < a || q_row_stride % 16 || q_expert_stride < (int64_t)(b - 1) * q_row_stride + a)
+    return kErrInvalidArgument;
+  if (scale_row_stride < a / kMxBlock || scale_expert_stride < (int64_t)(b - 1) * scale_row_stride + a / kMxBlock)
+    return kErrInvalidArgument;
+  if (!x || !q || !scale) return kErrInvalidArgument;
+  hipLaunchKernelGGL(mx_quant_cols_t_kernel, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
+                     q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                     int32_t cols, int64_t padded_rows, uint8_t* q, uint8_t* scale,
+                                     hipStream_t stream) {
+  if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
+  if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
+  if (!x || !counts || !q || !scale) return kErrInvalidArgument;
+  hipLaunchKernelGGL(mx_quant_tokens_t_kernel, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts, n_rows,
+                     n_experts, cols, padded_rows, q, scale);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_gemm_gate_up(const uint8_t* qx, const uint8_t* sx, const uint8_t* qw1, const uint8_t* sw1,
+                                   const uint8_t* qw3, const uint8_t* sw3, const int64_t* counts, int64_t n_rows,
+                                   int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* g, uint16_t* u,
+                                   uint16_t* h, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qx || !sx || !qw1 || !sw1 || !qw3 || !sw3 || !g || !u || !h) return kErrInvalidArgument;
+  p.qp = qx; p.ep = sx; p.qq = qw1; p.eq = sw1; p.qq2 = qw3; p.eq2 = sw3; p.o0 = g; p.o1 = u; p.o2 = h;
+  launch<kGateUp, true>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_gemm_down(const uint8_t* qh, const uint8_t* sh, const uint8_t* qw2, const uint8_t* sw2,
+                                const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                int32_t hidden, uint16_t* y, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qh || !sh || !qw2 || !sw2 || !y) return kErrInvalidArgument;
+  p.qp = qh; p.ep = sh; p.qq = qw2; p.eq = sw2; p.o0 = y;
+  launch<kDown, true>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_gemm_bwd_dgu(const uint8_t* qdy, const uint8_t* sdy, const uint8_t* qw2t,
+                                   const uint8_t* sw2t, const uint16_t* g, const uint16_t* u, const int64_t* counts,
+                                   int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dgu,
+                                   hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qdy || !sdy || !qw2t || !sw2t || !g || !u || !dgu) return kErrInvalidArgument;
+  p.qp = qdy; p.ep = sdy; p.qq = qw2t; p.eq = sw2t; p.g = g; p.u = u; p.o0 = dgu;
+  launch<kDgu, true>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_gemm_bwd_dx(const uint8_t* qdgu, const uint8_t* sdgu, const uint8_t* qw13t,
+                                  const uint8_t* sw13t, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                  int32_t dim, int32_t hidden, uint16_t* dx, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!qdgu || !sdgu || !qw13t || !sw13t || !dx) return kErrInvalidArgument;
+  p.qp = qdgu; p.ep = sdgu; p.qq = qw13t; p.eq = sw13t; p.o0 = dx;
+  launch<kDx, true>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_gemm_bwd_dw13(const uint8_t* qdgut, const uint8_t* sdgut, const uint8_t* qxt,
+                                    const uint8_t* sxt, const int64_t* counts, int64_t n_rows, int64_t padded_rows,
+                                    int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dw1, uint16_t* dw3,
+                                    hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
+  if (!dw1 || !dw3 || (n_rows > 0 && (!qdgut || !sdgut || !qxt || !sxt))) return kErrInvalidArgument;
+  p.Rpad = padded_rows; p.qp = qdgut; p.ep = sdgut; p.qq = qxt; p.eq = sxt; p.o0 = dw1; p.o1 = dw3;
+  launch<kDw13, true>(p, stream);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_gemm_bwd_dw2(const uint8_t* qdyt, const uint8_t* sdyt, const uint8_t* qht, const uint8_t* sht,
+                                   const int64_t* counts, int64_t n_rows, int64_t padded_rows, int32_t n_experts,
+                                   int32_t dim, int32_t hidden, uint16_t* dw2, hipStream_t stream) {
+  Params p;
+  int st = fp8_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
+  if (!dw2 || (n_rows > 0 && (!qdyt || !sdyt || !qht || !sht))) return kErrInvalidArgument;
+  p.Rpad = padded_rows; p.qp = qdyt; p.ep = sdyt; p.qq = qht; p.eq = sht; p.o0 = dw2;
+  launch<kDw2, true>(p, stream);
   return launch_status();
 }

@@ -33,6 +33,7 @@ __all__ = [
     "_run_experts_for_loop",
     "_run_experts_grouped_mm",
     "_run_experts_grouped_mm_fp8",
+    "_run_experts_grouped_mm_mxfp8",
 ]
 
 
@@ -81,6 +82,20 @@ def _run_experts_grouped_mm_fp8(
     return y.type_as(x)
 
 
+def _run_experts_grouped_mm_mxfp8(
+    w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor, x: torch.Tensor,
+    num_tokens_per_expert: torch.Tensor,
+) -> torch.Tensor:
+    """The MXFP8 grouped GEMMs the reference gets from torchao's
+    MXFP8TrainingOpConfig, recipe "mxfp8_rceil" (torchtitan/components/quantization/mx.py:85-128):
+    e4m3 elements with one e8m0 scale per 32 along each contraction, fp32
+    accumulation, bf16 outputs."""
+    y, _, _, _ = ops.grouped_swiglu_mxfp8(
+        x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16(), num_tokens_per_expert
+    )
+    return y.type_as(x)
+
+
 class GroupedExperts(Module):
     @dataclass(kw_only=True, slots=True)
     class Config(Module.Config):
@@ -96,11 +111,14 @@ class GroupedExperts(Module):
         self.w2 = nn.Parameter(torch.empty(config.num_experts, config.dim, config.hidden_dim))
         self.w3 = nn.Parameter(torch.empty(config.num_experts, config.hidden_dim, config.dim))
         self.use_grouped_mm = config.use_grouped_mm
-        # set by quantization.Float8GroupedMMConverter.convert
+        # set by quantization.Float8GroupedMMConverter / MXFP8Converter .convert
         self.float8 = False
+        self.mxfp8 = False
 
     def forward(self, x: torch.Tensor, num_tokens_per_expert: torch.Tensor) -> torch.Tensor:
         w1, w2, w3 = _local(self.w1), _local(self.w2), _local(self.w3)
+        if self.mxfp8:
+            return _run_experts_grouped_mm_mxfp8(w1, w2, w3, x, num_tokens_per_expert)
         if self.float8:
             return _run_experts_grouped_mm_fp8(w1, w2, w3, x, num_tokens_per_expert)
         if self.use_grouped_mm:

@@ -567,6 +567,142 @@ grouped_swiglu_fp8.register_autograd(_gs8_bwd, setup_context=_gs_setup)
 
 
 # ---------------------------------------------------------------------------
+# MXFP8 grouped SwiGLU experts (e8m0 scales per 32 elements along the
+# contraction, RCEIL; fp32 accumulate)
+# ---------------------------------------------------------------------------
+MX_BLOCK = 32
+
+
+def _mx_quant_rows(x: Tensor, cols: int) -> tuple[Tensor, Tensor]:
+    """x viewed as [rows, cols] bf16 -> (q uint8 [rows, cols], e8m0 uint8 [rows, cols / 32])."""
+    rows = x.numel() // cols
+    q = torch.empty(rows, cols, dtype=FP8, device=x.device)
+    s = torch.empty(rows, cols // MX_BLOCK, dtype=torch.uint8, device=x.device)
+    call("moe_mxfp8_quant_rows", ptr(x), rows, cols, ptr(q), ptr(s), stream_of(x))
+    return q, s
+
+
+def _mx_padded_rows(r: int, e: int) -> int:
+    return int(lib().moe_mxfp8_padded_rows(r, e))
+
+
+def _mx_quant_tokens_t(x: Tensor, counts: Tensor, e: int, rpad: int) -> tuple[Tensor, Tensor]:
+    """x [R, C] bf16 in expert token groups -> (q [C, rpad], e8m0 [rpad / 32, C])."""
+    r, c = x.shape
+    q = torch.empty(c, rpad, dtype=FP8, device=x.device)
+    s = torch.empty(rpad // MX_BLOCK, c, dtype=torch.uint8, device=x.device)
+    call("moe_mxfp8_quant_tokens_t", ptr(x), ptr(counts), r, e, c, rpad, ptr(q), ptr(s), stream_of(x))
+    return q, s
+
+
+def _check_bf16(op: str, **tensors: Tensor) -> None:
+    for name, t in tensors.items():
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{op} expects bfloat16 {name}, got {t.dtype}")
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_mxfp8", mutates_args=())
+def grouped_swiglu_mxfp8(
+    x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """MXFP8 grouped SwiGLU: x, h and the weights quantized in 32-element
+    blocks along each GEMM's contraction; bf16 outputs (y, g, u, h)."""
+    require_gpu(x, w1, w2, w3, num_tokens_per_expert)
+    _check_bf16("grouped_swiglu_mxfp8", x=x, w1=w1, w2=w2, w3=w3)
+    x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    s = stream_of(x)
+    qx, sx = _mx_quant_rows(x, d)
+    qw1, sw1 = _mx_quant_rows(w1, d)
+    qw3, sw3 = _mx_quant_rows(w3, d)
+    qw2, sw2 = _mx_quant_rows(w2, h_dim)
+    g = x.new_empty(r, h_dim)
+    u = x.new_empty(r, h_dim)
+    h = x.new_empty(r, h_dim)
+    y = x.new_empty(r, d)
+    call("moe_mxfp8_gemm_gate_up", ptr(qx), ptr(sx), ptr(qw1), ptr(sw1), ptr(qw3), ptr(sw3), ptr(counts), r, e, d,
+         h_dim, ptr(g), ptr(u), ptr(h), s)
+    qh, sh = _mx_quant_rows(h, h_dim)
+    call("moe_mxfp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
+    return y, g, u, h
+
+
+@grouped_swiglu_mxfp8.register_fake
+def _(x, w1, w2, w3, num_tokens_per_expert):
+    r, d = x.shape
+    h_dim = w1.shape[1]
+    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_mxfp8_backward", mutates_args=())
+def grouped_swiglu_mxfp8_backward(
+    dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
+    g: Tensor, u: Tensor, h: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
+    dy = dy.to(torch.bfloat16).contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    dev = x.device
+    s = stream_of(x)
+    # dh = dy . w2 (contraction over D): dy and w2 per (e, h) column, both blocked along D
+    qdy, sdy = _mx_quant_rows(dy, d)
+    qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
+    sw2t = torch.empty(e, h_dim, d // MX_BLOCK, dtype=torch.uint8, device=dev)
+    call("moe_mxfp8_quant_cols_t", ptr(w2), e, d, h_dim, ptr(qw2t), h_dim * d, d, ptr(sw2t),
+         h_dim * (d // MX_BLOCK), d // MX_BLOCK, s)
+    dgu = x.new_empty(r, 2 * h_dim)
+    call("moe_mxfp8_gemm_bwd_dgu", ptr(qdy), ptr(sdy), ptr(qw2t), ptr(sw2t), ptr(g), ptr(u), ptr(counts), r, e, d,
+         h_dim, ptr(dgu), s)
+    # dx = dg . w1 + du . w3 (contraction over H, blocks never straddle the halves):
+    # w1 and w3 per (e, d) column, written side by side as [E, D, 2H]
+    qdgu, sdgu = _mx_quant_rows(dgu, 2 * h_dim)
+    qw13t = torch.empty(e, d, 2 * h_dim, dtype=FP8, device=dev)
+    nb = 2 * h_dim // MX_BLOCK
+    sw13t = torch.empty(e, d, nb, dtype=torch.uint8, device=dev)
+    call("moe_mxfp8_quant_cols_t", ptr(w1), e, h_dim, d, ptr(qw13t), d * 2 * h_dim, 2 * h_dim, ptr(sw13t),
+         d * nb, nb, s)
+    call("moe_mxfp8_quant_cols_t", ptr(w3), e, h_dim, d, qw13t.data_ptr() + h_dim, d * 2 * h_dim, 2 * h_dim,
+         sw13t.data_ptr() + h_dim // MX_BLOCK, d * nb, nb, s)
+    dx = x.new_empty(r, d)
+    call("moe_mxfp8_gemm_bwd_dx", ptr(qdgu), ptr(sdgu), ptr(qw13t), ptr(sw13t), ptr(counts), r, e, d, h_dim,
+         ptr(dx), s)
+    # weight gradients: contraction over each expert's tokens (groups padded to 32)
+    rpad = _mx_padded_rows(r, e)
+    qdgut, sdgut = _mx_quant_tokens_t(dgu, counts, e, rpad)
+    qxt, sxt = _mx_quant_tokens_t(x, counts, e, rpad)
+    dw1 = torch.empty_like(w1)
+    dw3 = torch.empty_like(w3)
+    call("moe_mxfp8_gemm_bwd_dw13", ptr(qdgut), ptr(sdgut), ptr(qxt), ptr(sxt), ptr(counts), r, rpad, e, d, h_dim,
+         ptr(dw1), ptr(dw3), s)
+    qdyt, sdyt = _mx_quant_tokens_t(dy, counts, e, rpad)
+    qht, sht = _mx_quant_tokens_t(h, counts, e, rpad)
+    dw2 = torch.empty_like(w2)
+    call("moe_mxfp8_gemm_bwd_dw2", ptr(qdyt), ptr(sdyt), ptr(qht), ptr(sht), ptr(counts), r, rpad, e, d, h_dim,
+         ptr(dw2), s)
+    return dx, dw1, dw2, dw3
+
+
+@grouped_swiglu_mxfp8_backward.register_fake
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h):
+    return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
+
+
+def _gsmx_bwd(ctx, dy, _dg, _du, _dh):
+    x, w1, w2, w3, counts, g, u, h = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None, None
+    dx, dw1, dw2, dw3 = grouped_swiglu_mxfp8_backward(dy, x, w1, w2, w3, counts, g, u, h)
+    return dx, dw1, dw2, dw3, None
+
+
+grouped_swiglu_mxfp8.register_autograd(_gsmx_bwd, setup_context=_gs_setup)
+
+
+# ---------------------------------------------------------------------------
 # row gather / scatter by an index (expert-parallel permute and unpermute)
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("moe_mi355x::gather_rows", mutates_args=())
