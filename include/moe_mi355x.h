@@ -128,7 +128,7 @@ int moe_combine_bwd(const void* grad_out, const void* routed_output, const int32
  * g = x.w1^T, u = x.w3^T, h = silu(g)*u, y = h.w2^T, all bf16 with fp32
  * accumulation. counts [E] int64 (num_tokens_per_expert); x [R,D];
  * w1,w3 [E,H,D]; w2 [E,D,H]. Outputs g,u,h [R,H] (g,u,h saved for
- * backward) and y [R,D]. D % 256 == 0, H % 256 == 0, E <= 1024. */
+ * backward) and y [R,D]. D % 64 == 0, H % 64 == 0, E <= 1024. */
 int moe_grouped_swiglu_fwd(const uint16_t* x, const uint16_t* w1, const uint16_t* w2,
                            const uint16_t* w3, const int64_t* counts, int64_t n_rows,
                            int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* g,
@@ -177,6 +177,50 @@ int moe_grouped_gemm_bwd_dw13(const uint16_t* dgu, const uint16_t* x, const int6
 int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, const int64_t* counts,
                              int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
                              uint16_t* dw2, moe_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * gpt-oss experts (torchtitan/models/gpt_oss/moe.py:43-52, 92-122, the
+ * grouped-mm path): mlp1_weight [E, 2H, D] bf16 with the glu row 2j and the
+ * linear row 2j + 1, mlp1_bias [E, 2H], mlp2_weight [E, D, H], mlp2_bias
+ * [E, D] (biases bf16). Forward, every op rounded to bf16:
+ *   h1 = bf16(x . mlp1^T) + mlp1_bias;  g = h1[:, 0::2], u = h1[:, 1::2]
+ *   h  = (clamp(g, max=L) * sigmoid(1.702 clamp(g, max=L))) * (clamp(u, -L, L) + 1)
+ *   y  = bf16(h . mlp2^T) + mlp2_bias
+ * with L = swiglu_limit rounded to bf16. D % 64 == 0, H % 64 == 0.
+ * ------------------------------------------------------------------------- */
+
+/* g, u, h [R, H] (g, u = the biased pre-clamp halves, saved for backward). */
+int moe_grouped_gemm_oss_gate_up(const uint16_t* x, const uint16_t* mlp1_weight, const uint16_t* mlp1_bias,
+                                 const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                 int32_t hidden, float swiglu_limit, uint16_t* g, uint16_t* u, uint16_t* h,
+                                 moe_stream_t stream);
+/* y [R, D] = bf16(h . mlp2^T) + mlp2_bias. */
+int moe_grouped_gemm_oss_down(const uint16_t* h, const uint16_t* mlp2_weight, const uint16_t* mlp2_bias,
+                              const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                              int32_t hidden, uint16_t* y, moe_stream_t stream);
+/* dh = bf16(dy . mlp2), then the autograd of the clamped SwiGLU (each bf16 op's
+ * gradient rounded to bf16, clamp gradients zero outside the limits):
+ * dgu [R, 2H] = [dg | du] (the gradients of the glu and linear halves of h1). */
+int moe_grouped_gemm_oss_bwd_dgu(const uint16_t* dy, const uint16_t* mlp2_weight, const uint16_t* g,
+                                 const uint16_t* u, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                 int32_t dim, int32_t hidden, float swiglu_limit, uint16_t* dgu,
+                                 moe_stream_t stream);
+/* dx [R, D] = dh1 . mlp1 (one fp32 accumulation over 2H, rounded once). */
+int moe_grouped_gemm_oss_bwd_dx(const uint16_t* dgu, const uint16_t* mlp1_weight, const int64_t* counts,
+                                int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden, uint16_t* dx,
+                                moe_stream_t stream);
+/* dmlp1_weight [E, 2H, D] = dh1_e^T . x_e, glu / linear rows interleaved (zeros
+ * for empty experts). dmlp2_weight is moe_grouped_gemm_bwd_dw2 (same layout as w2). */
+int moe_grouped_gemm_oss_bwd_dw1(const uint16_t* dgu, const uint16_t* x, const int64_t* counts,
+                                 int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                                 uint16_t* dmlp1_weight, moe_stream_t stream);
+/* Bias gradients (the backward of bias.repeat_interleave(counts)): per expert e
+ * and column c < cols, out[e*ld_out + c*col_stride] = sum over the expert's rows
+ * r of src[r*ld_src + c], fp32 in a fixed order. src bf16, cols % 64 == 0,
+ * ld_src % 8 == 0. */
+int moe_grouped_col_sum(const uint16_t* src, int64_t ld_src, const int64_t* counts, int64_t n_rows,
+                        int32_t n_experts, int32_t cols, float* out, int64_t ld_out, int32_t col_stride,
+                        moe_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * fp8 e4m3 (OCP e4m3fn) grouped SwiGLU experts. The reference's fp8 path is

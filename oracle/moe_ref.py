@@ -9,6 +9,7 @@ It restates the reference's algorithm (QIU023/torchtitan):
   torchtitan/ops/scatter_add.py:10-48          (deterministic scatter_add + backward)
   torchtitan/models/common/feed_forward.py:34-54
   torchtitan/distributed/expert_parallel.py:26-67 (_generate_permute_indices)
+  torchtitan/models/gpt_oss/moe.py:43-122      (gpt-oss experts)
 with the GPU lowering of the ops the reference calls made explicit, because on
 the GPU those are what define the reference's results:
   * torch.topk(sorted=False): radix order, lowest index first among ties, output
@@ -323,6 +324,55 @@ def experts_for_loop(w1, w2, w3, x, counts):
         xe = x[start : start + c]
         h = F.silu(xe @ w1[e].t()) * (xe @ w3[e].t())
         outs.append(h @ w2[e].t())
+        start += c
+    return torch.cat(outs, 0)
+
+
+# ---------------------------------------------------------------------------
+# gpt-oss experts (torchtitan/models/gpt_oss/moe.py:43-122)
+# ---------------------------------------------------------------------------
+
+OSS_ALPHA = 1.702
+
+
+def oss_swiglu(h1: torch.Tensor, limit: float, alpha: float = OSS_ALPHA) -> torch.Tensor:
+    """swiglu (gpt_oss/moe.py:43-52) on an interleaved [.., 2H] tensor: glu =
+    even columns clamped above at limit, linear = odd columns clamped to
+    [-limit, limit]; glu * sigmoid(alpha glu) * (linear + 1), in h1's dtype."""
+    x_glu, x_linear = h1[..., ::2], h1[..., 1::2]
+    x_glu = x_glu.clamp(min=None, max=limit)
+    x_linear = x_linear.clamp(min=-limit, max=limit)
+    out_glu = x_glu * torch.sigmoid(alpha * x_glu)
+    return out_glu * (x_linear + 1)
+
+
+def oss_experts_grouped_mm(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, limit, x, counts):
+    """The grouped-mm path (gpt_oss/moe.py:92-122) with the reference's torch
+    calls: torch._grouped_mm over int32 offsets, biases broadcast per row with
+    repeat_interleave (plus the zero row for rows past the groups) and added in
+    bf16, then the clamped SwiGLU and the second grouped GEMM."""
+    offsets = torch.cumsum(counts, dim=0, dtype=torch.int32)
+    tail = (x.shape[0] - offsets[-1]).unsqueeze(0).to(counts.dtype)
+    counts_long = torch.cat([counts, tail]).long()
+    h = torch._grouped_mm(x.bfloat16(), mlp1_weight.transpose(-2, -1).bfloat16(), offs=offsets)
+    b1 = torch.cat([mlp1_bias, mlp1_bias.new_zeros(1, mlp1_bias.shape[-1])])
+    b1 = b1.repeat_interleave(counts_long, dim=0, output_size=x.shape[0])
+    h = h + b1.to(h.dtype)
+    h = oss_swiglu(h, limit)
+    h = torch._grouped_mm(h, mlp2_weight.transpose(-2, -1).bfloat16(), offs=offsets)
+    b2 = torch.cat([mlp2_bias, mlp2_bias.new_zeros(1, mlp2_bias.shape[-1])])
+    b2 = b2.repeat_interleave(counts_long, dim=0, output_size=x.shape[0])
+    return h + b2.to(h.dtype)
+
+
+def oss_experts_for_loop(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, limit, x, counts):
+    """The for-loop path (gpt_oss/moe.py:55-89): matmuls in x's dtype."""
+    outs, start = [], 0
+    for e, c in enumerate(counts.tolist()):
+        xe = x[start:start + c]
+        h = xe @ mlp1_weight[e].transpose(-2, -1) + mlp1_bias[e]
+        h = oss_swiglu(h, limit)
+        outs.append(h @ mlp2_weight[e].transpose(-2, -1) + mlp2_bias[e])
         start += c
     return torch.cat(outs, 0)
 

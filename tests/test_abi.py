@@ -72,9 +72,14 @@ def test_host_side_validation_returns_status_codes(lib):
     # rows: dims that are not whole 16-byte chunks
     assert lib.moe_permute(null, null, null, 4, 12, 2, 0, null, null) == -1
     assert lib.moe_combine(null, null, null, null, 4, 6, 2, 1, null, null) == -1
-    # grouped GEMM shape rules: dims below one 256 tile are invalid, ragged dims unsupported
-    assert lib.moe_grouped_gemm_gate_up(null, null, null, null, 8, 4, 128, 256, null, null, null, null) == -1
-    assert lib.moe_grouped_gemm_gate_up(null, null, null, null, 8, 4, 768 + 64, 256, null, null, null, null) == -2
+    # grouped GEMM shape rules: dims below 64 are invalid, dims not a multiple of 64 unsupported
+    assert lib.moe_grouped_gemm_gate_up(null, null, null, null, 8, 4, 32, 256, null, null, null, null) == -1
+    assert lib.moe_grouped_gemm_gate_up(null, null, null, null, 8, 4, 768 + 32, 256, null, null, null, null) == -2
+    assert lib.moe_grouped_gemm_oss_gate_up(null, null, null, null, 8, 4, 2880, 2880 + 16, 7.0, null, null, null,
+                                            null) == -2
+    # the fp8 / MXFP8 kernels keep D, H multiples of 256
+    assert lib.moe_fp8_gemm_down(null, null, null, null, null, 8, 4, 768 + 64, 256, null, null) == -2
+    assert lib.moe_mxfp8_gemm_down(null, null, null, null, null, 8, 4, 768 + 64, 256, null, null) == -2
     assert lib.moe_grouped_gemm_bwd_dw2(null, null, null, 8, 0, 256, 256, null, null) == -1
 
 

@@ -192,6 +192,9 @@ GEMM_CASES = {
     "uniform_e8": (8, 256, 512, [130, 128, 127, 1, 255, 256, 257, 100]),
     "empty_and_skewed": (8, 512, 256, [0, 700, 0, 3, 0, 0, 129, 0]),
     "single_expert": (1, 256, 256, [333]),
+    # D, H multiples of 64 but not of the tile widths: partial last n- and m-tiles
+    "tails_d320_h192": (6, 320, 192, [100, 0, 257, 31, 64, 200]),
+    "tails_d2880_h2880": (3, 2880, 2880, [300, 0, 77]),
 }
 
 

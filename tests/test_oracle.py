@@ -594,3 +594,57 @@ def test_mx_experts_close_to_bf16_reference():
     errs = [rel(y, yr.detach()), rel(dx, xr.grad), rel(dw1, w1r.grad), rel(dw2, w2r.grad), rel(dw3, w3r.grad)]
     assert max(errs) < 0.1, errs
     assert torch.count_nonzero(dw1[1]) == 0 and torch.count_nonzero(dw2[1]) == 0
+
+
+# ---------------------------------------------------------------------------
+# gpt-oss experts (gpt_oss/moe.py:43-122)
+# ---------------------------------------------------------------------------
+
+
+def test_oss_swiglu_hand_worked_values():
+    import math
+
+    L, a = 7.0, 1.702
+    h1 = torch.tensor([[10.0, -9.0, -3.0, 0.5, 2.0, 8.0, 7.0, -7.0]], dtype=torch.float64)
+    out = R.oss_swiglu(h1, L)[0].tolist()
+
+    def sig(z):
+        return 1.0 / (1.0 + math.exp(-z))
+    want = [7.0 * sig(a * 7.0) * (-7.0 + 1.0),   # glu clamped to 7, linear clamped to -7
+            -3.0 * sig(-3.0 * a) * 1.5,          # no clamp; the glu is not clamped from below
+            2.0 * sig(2.0 * a) * (7.0 + 1.0),    # linear clamped to +7
+            7.0 * sig(7.0 * a) * (-7.0 + 1.0)]   # exactly at the limits
+    assert out == pytest.approx(want, rel=1e-12)
+
+
+def test_oss_swiglu_gradient_masks_and_finite_differences():
+    L = 7.0
+    h1 = torch.tensor([[10.0, -9.0, -3.0, 0.5, 6.5, 7.5, -2.0, -6.0]], dtype=torch.float64, requires_grad=True)
+    R.oss_swiglu(h1, L).sum().backward()
+    gr = h1.grad[0]
+    assert gr[0] == 0 and gr[1] == 0 and gr[5] == 0      # clamped inputs get no gradient
+    assert gr[2] != 0 and gr[3] != 0 and gr[4] != 0 and gr[6] != 0 and gr[7] != 0
+    eps = 1e-6
+    for i in (2, 3, 4, 6, 7):
+        hp, hm = h1.detach().clone(), h1.detach().clone()
+        hp[0, i] += eps
+        hm[0, i] -= eps
+        fd = (R.oss_swiglu(hp, L).sum() - R.oss_swiglu(hm, L).sum()) / (2 * eps)
+        assert gr[i].item() == pytest.approx(fd.item(), rel=1e-6)
+
+
+def test_oss_grouped_mm_matches_for_loop_and_float64():
+    g = torch.Generator().manual_seed(5)
+    e, d, h = 4, 64, 48
+    cnt = torch.tensor([9, 0, 17, 4])
+    r = int(cnt.sum())
+    x = torch.randn(r, d, generator=g).bfloat16()
+    w1 = (torch.randn(e, 2 * h, d, generator=g) * 0.3).bfloat16()
+    b1 = torch.randn(e, 2 * h, generator=g).bfloat16()
+    w2 = (torch.randn(e, d, h, generator=g) * 0.3).bfloat16()
+    b2 = torch.randn(e, d, generator=g).bfloat16()
+    grouped = R.oss_experts_grouped_mm(w1, b1, w2, b2, 7.0, x, cnt)
+    loop = R.oss_experts_for_loop(w1, b1, w2, b2, 7.0, x, cnt)
+    assert torch.equal(grouped, loop)
+    f64 = R.oss_experts_for_loop(w1.double(), b1.double(), w2.double(), b2.double(), 7.0, x.double(), cnt)
+    assert ((grouped.double() - f64).abs().max() / f64.abs().max()).item() < 2e-2

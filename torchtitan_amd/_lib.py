@@ -52,6 +52,12 @@ SIGNATURES: dict[str, list] = {
     "moe_fp8_gemm_bwd_dx": [P, P, P, P, P, I64, I32, I32, I32, P, P],
     "moe_fp8_gemm_bwd_dw13": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P, P],
     "moe_fp8_gemm_bwd_dw2": [P, P, P, P, P, I64, I64, I32, I32, I32, P, P],
+    "moe_grouped_gemm_oss_gate_up": [P, P, P, P, I64, I32, I32, I32, F32, P, P, P, P],
+    "moe_grouped_gemm_oss_down": [P, P, P, P, I64, I32, I32, I32, P, P],
+    "moe_grouped_gemm_oss_bwd_dgu": [P, P, P, P, P, I64, I32, I32, I32, F32, P, P],
+    "moe_grouped_gemm_oss_bwd_dx": [P, P, P, I64, I32, I32, I32, P, P],
+    "moe_grouped_gemm_oss_bwd_dw1": [P, P, P, I64, I32, I32, I32, P, P],
+    "moe_grouped_col_sum": [P, I64, P, I64, I32, I32, P, I64, I32, P],
     "moe_mxfp8_padded_rows": [I64, I32],
     "moe_mxfp8_quant_rows": [P, I64, I32, P, P, P],
     "moe_mxfp8_quant_cols_t": [P, I32, I32, I32, P, I64, I64, P, I64, I64, P],

@@ -33,6 +33,12 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-file additions. The grouped GEMM epilogues (fully unrolled over the
+# accumulator tile) exceed clang's default size limit for #pragma unroll in the
+# gpt-oss backward variant; a partially unrolled epilogue indexes the
+# accumulators dynamically and moves them to scratch memory.
+EXTRA_FLAGS = {"grouped_gemm.hip": ["-mllvm", "-pragma-unroll-threshold=1000000"]}
+
 
 def _hipcc() -> str:
     for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -43,7 +49,7 @@ def _hipcc() -> str:
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

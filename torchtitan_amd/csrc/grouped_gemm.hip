@@ -49,6 +49,7 @@
 //    rounded to bf16 once, at the points the reference's bf16 autograd rounds;
 //    the outputs are bit-identical to torch._grouped_mm and its autograd on
 //    this GPU.
+#include <cstring>
 #include <type_traits>
 
 #include "common.h"
@@ -91,10 +92,33 @@ struct GemmParams {
   uint16_t* out_dw1;
   uint16_t* out_dw2;
   uint16_t* out_dw3;
+  // w1 / w3 (and dw1 / dw3) row j of expert e at base + e * w13_estride + j * w13_rstride:
+  // (H D, D) for separate [E, H, D] tensors; (2 H D, 2 D) with w3 = w1 + D for the
+  // interleaved gate/linear rows of gpt-oss's mlp1_weight [E, 2H, D]
+  int64_t w13_estride, w13_rstride;
+  // gpt-oss expert epilogue (torchtitan/models/gpt_oss/moe.py:43-52, 92-122)
+  const uint16_t* b1;  // mlp1_bias [E, 2H] bf16 (glu 2j, linear 2j + 1)
+  const uint16_t* b2;  // mlp2_bias [E, D] bf16
+  float limit;         // swiglu_limit as bf16
+  float alpha;         // 1.702
 };
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Expert epilogue variants: the SwiGLU of moe.py:53-70 and gpt-oss's biased,
+// clamped SwiGLU with interleaved mlp1 rows (gpt_oss/moe.py:43-52, 92-122).
+enum ExpertAct : int { kSwiGLU = 0, kOssGLU = 1 };
+
+// gpt-oss activation on bf16 values g (glu), u (linear), every op rounded to
+// bf16 as the reference's bf16 tensor ops: clamp(g, max=L), clamp(u, -L, L),
+// g * sigmoid(alpha g), times (u + 1). Returns the last product unrounded.
+__device__ __forceinline__ float oss_glu(float g, float u, float L, float alpha) {
+  const float xg = g > L ? L : g;                      // NaN passes, as torch.clamp
+  const float xl = u < -L ? -L : (u > L ? L : u);
+  const float s = round_bf(sigmoid_f(round_bf(xg * alpha)));
+  return round_bf(xg * s) * round_bf(xl + 1.0f);
+}
 template <int MODE>
 struct ModeTraits {
   static constexpr bool kRowGrouped = MODE <= kBwdDx;   // m = token rows of one expert
@@ -104,10 +128,11 @@ struct ModeTraits {
 
 // Interleave of the gate_up output columns: 16-column blocks alternate
 // between g (w1) and u (w3), so a lane's SwiGLU operands sit in one wave.
+__device__ __forceinline__ int gate_up_col(int nt, int n, int BN) {
+  return nt * (BN / 2) + ((n >> 4) >> 1) * 16 + (n & 15);
+}
 __device__ __forceinline__ const uint16_t* gate_up_row(const GemmParams& p, int64_t e, int nt, int n, int BN) {
-  const int blk = n >> 4;
-  const int hc = nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
-  return ((blk & 1) ? p.w3 : p.w1) + (e * p.H + hc) * (int64_t)p.D;
+  return (((n >> 4) & 1) ? p.w3 : p.w1) + e * p.w13_estride + (int64_t)gate_up_col(nt, n, BN) * p.w13_rstride;
 }
 
 #define LDSP __attribute__((address_space(3)))
@@ -151,7 +176,9 @@ __device__ __forceinline__ bf16x8_t frag_km(const uint16_t* tile, int row0, int 
 
 __device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a segment
 
-template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC>
+// TAIL: the n extent (and, for dW, the m extent) is not a multiple of the tile;
+// compiled only for such shapes so that whole-tile shapes keep the tighter code.
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT, bool TAIL>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p) {
   using T = ModeTraits<MODE>;
   constexpr int WGN = NW / WGM;
@@ -178,8 +205,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
   if (MODE == kBwdDx) { Ntot = D; Kfix = 2 * H; }
   if (MODE == kBwdDw13) { Ntot = D; Mfix = 2 * H; }
   if (MODE == kBwdDw2) { Ntot = H; Mfix = D; }
-  const int NT = Ntot / BN;
-  const int MT = T::kRowGrouped ? 0 : Mfix / BM;
+  // D and H are multiples of 64: the last n-tile (and, for dW, m-tile) may be
+  // partial; its copies past the edge read the zero row and its stores are skipped
+  const int NT = (Ntot + BN - 1) / BN;
+  const int MT = T::kRowGrouped ? 0 : (Mfix + BM - 1) / BM;
 
   {
     int cnt[4], tl[4], seg[4], tst[4];
@@ -252,6 +281,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     const uint16_t* srcQ[CPW_Q];
     const uint16_t* srcQ3[CPW_Q];  // dx: the w3 half of the k range
     int klP[CPW_P], klQ[CPW_Q];    // k-major copies: the k-row this lane fills (P rows: the token row)
+    bool inP[CPW_P], inQ[CPW_Q];   // the copied m / n lies inside the matrix
     int64_t stepP = BK, stepQ = BK;  // element advance per k-step
     if constexpr (!T::kPT) {
       const uint16_t* pb;
@@ -265,6 +295,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const int r = row0 + (wv * CPW_P + b) * 16 + dr;
         srcP[b] = pb + (int64_t)r * ldp + dc * 8;
         klP[b] = r;  // rows past the segment copy the zero row
+        inP[b] = true;
       }
     } else {
       const uint16_t* pb = (MODE == kBwdDw13) ? p.dgu : p.dy;
@@ -277,12 +308,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const int c = (slot % CHP) ^ kswz(kl);
         srcP[b] = pb + (int64_t)(seg0 + kl) * ldp + mt * BM + c * 8;
         klP[b] = kl;
+        inP[b] = mt * BM + c * 8 < Mfix;
       }
     }
     if constexpr (!T::kQT) {
 #pragma unroll
       for (int b = 0; b < CPW_Q; ++b) {
         const int n = (wv * CPW_Q + b) * 16 + dr;
+        inQ[b] = (MODE == kFwdGateUp) ? gate_up_col(nt, n, BN) < H : nt * BN + n < D;
         const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, nt, n, BN)
                                                      : p.w2 + (e64 * D + nt * BN + n) * (int64_t)H;
         srcQ[b] = rowp + dc * 8;
@@ -292,7 +325,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       const uint16_t* qb;
       int ldq;
       if (MODE == kBwdDgu) { qb = p.w2 + e64 * D * (int64_t)H; ldq = H; }        // rows k of w2[e] (D x H)
-      else if (MODE == kBwdDx) { qb = p.w1 + e64 * H * (int64_t)D; ldq = D; }    // rows k of w1[e], then w3[e]
+      else if (MODE == kBwdDx) { qb = p.w1 + e64 * p.w13_estride; ldq = (int)p.w13_rstride; }  // rows k of w1[e], then w3[e]
       else if (MODE == kBwdDw13) { qb = p.x + (int64_t)seg0 * D; ldq = D; }
       else { qb = p.h + (int64_t)seg0 * H; ldq = H; }
       stepQ = (int64_t)BK * ldq;
@@ -303,8 +336,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const int c = (slot % CHQ) ^ kswz(kl);
         const int64_t off = (int64_t)kl * ldq + nt * BN + c * 8;
         srcQ[b] = qb + off;
-        if (MODE == kBwdDx) srcQ3[b] = p.w3 + e64 * H * (int64_t)D + off;
+        if (MODE == kBwdDx) srcQ3[b] = p.w3 + e64 * p.w13_estride + off;
         klQ[b] = kl;
+        inQ[b] = nt * BN + c * 8 < Ntot;
       }
     }
 
@@ -315,7 +349,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       for (int b = 0; b < CPW_P; ++b) {
         const uint16_t* src = srcP[b] + kt * stepP;
         if constexpr (T::kPT) {
-          if (seg0 + k0 + klP[b] >= seg1) src = (const uint16_t*)kZeroRow;
+          if (seg0 + k0 + klP[b] >= seg1 || (TAIL && !inP[b])) src = (const uint16_t*)kZeroRow;
         } else {
           if (klP[b] >= seg1) src = (const uint16_t*)kZeroRow;
         }
@@ -325,11 +359,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       for (int b = 0; b < CPW_Q; ++b) {
         const uint16_t* src = srcQ[b] + kt * stepQ;
         if constexpr (MODE == kBwdDx) {
-          if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * D;
+          if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * p.w13_rstride;
         }
         if constexpr (MODE >= kBwdDw13) {
           if (seg0 + k0 + klQ[b] >= seg1) src = (const uint16_t*)kZeroRow;
         }
+        if (TAIL && !inQ[b]) src = (const uint16_t*)kZeroRow;
         dma16(src, lds_addr(&sQ[s][(wv * CPW_Q + b) * 512]));
       }
     };
@@ -348,8 +383,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const int r = row0 + wm * WM + i * 16 + ml;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if (r < seg1) {
-            const int n = nt * BN + wn * WN + j * 16 + nq;
+          const int n = nt * BN + wn * WN + j * 16 + nq;
+          if (r < seg1 && (!TAIL || n < D)) {
             *(uint2*)(p.out_dx + (int64_t)r * D + n) =
                 make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3]));
           }
@@ -392,7 +427,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         if (NS == 3 && kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(CPW) : "memory");
         else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (kt + NS - 1 < nk) issue(kt + NS - 1);
-        if (MODE == kBwdDx && kt == kt_half) park_dx_half();
+        if (MODE == kBwdDx && ACT == kSwiGLU && kt == kt_half) park_dx_half();
         if (decltype(full)::value || tmv > 0) compute(kt % NS);
       }
     };
@@ -408,12 +443,25 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
           for (int jj = 0; jj < TN / 2; ++jj) {
             const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nq;
+            if (TAIL && hc >= H) continue;
             float gv[4], uv[4], hv[4];
+            if constexpr (ACT == kOssGLU) {
+              // h1 = bf16(x . mlp1^T) + bias (bf16 add), then the clamped SwiGLU
+              const uint4 bw = *(const uint4*)(p.b1 + e64 * 2 * H + 2 * hc);  // (glu, linear) x 4 columns
+              const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              gv[q] = round_bf(acc[i][2 * jj][q]);
-              uv[q] = round_bf(acc[i][2 * jj + 1][q]);
-              hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+              for (int q = 0; q < 4; ++q) {
+                gv[q] = round_bf(round_bf(acc[i][2 * jj][q]) + bf_lo(bb[q]));
+                uv[q] = round_bf(round_bf(acc[i][2 * jj + 1][q]) + bf_hi(bb[q]));
+                hv[q] = oss_glu(gv[q], uv[q], p.limit, p.alpha);
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                gv[q] = round_bf(acc[i][2 * jj][q]);
+                uv[q] = round_bf(acc[i][2 * jj + 1][q]);
+                hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+              }
             }
             const int64_t off = (int64_t)r * H + hc;
             *(uint2*)(p.out_g + off) = make_uint2(pack_bf2(gv[0], gv[1]), pack_bf2(gv[2], gv[3]));
@@ -431,9 +479,17 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int n = nt * BN + wn * WN + j * 16 + nq;
+            if (TAIL && n >= D) continue;
             uint16_t* dst = outp + (int64_t)r * D + n;
             float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            if (MODE == kBwdDx) {
+            if (MODE == kFwdDown && ACT == kOssGLU) {  // bf16(h . mlp2^T) + mlp2_bias (bf16 add)
+              const uint2 bw = *(const uint2*)(p.b2 + e64 * D + n);
+              v[0] = round_bf(v[0]) + bf_lo(bw.x);
+              v[1] = round_bf(v[1]) + bf_hi(bw.x);
+              v[2] = round_bf(v[2]) + bf_lo(bw.y);
+              v[3] = round_bf(v[3]) + bf_hi(bw.y);
+            }
+            if (MODE == kBwdDx && ACT == kSwiGLU) {
               const uint2 pw = *(const uint2*)dst;
               v[0] = bf_lo(pw.x) + round_bf(v[0]);
               v[1] = bf_hi(pw.x) + round_bf(v[1]);
@@ -452,20 +508,41 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
             const int hh = nt * BN + wn * WN + j * 16 + nq;
+            if (TAIL && hh >= H) continue;
             const int64_t off = (int64_t)r * H + hh;
             const uint2 gw = *(const uint2*)(p.g + off);
             const uint2 uw = *(const uint2*)(p.u + off);
             const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
             const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
             float dg[4], du[4];
+            if constexpr (ACT == kOssGLU) {
+              // autograd of oss_glu, each bf16 op's gradient rounded to bf16
+              const float L = p.limit, al = p.alpha;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float dh = round_bf(acc[i][j][q]);
-              const float sl = round_bf(silu_f(gv[q]));
-              const float dsl = round_bf(dh * uv[q]);
-              du[q] = dh * sl;
-              const float sg = 1.0f / (1.0f + expf(-gv[q]));
-              dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
+              for (int q = 0; q < 4; ++q) {
+                const float dh = round_bf(acc[i][j][q]);
+                const float xg = gv[q] > L ? L : gv[q];
+                const float xl = uv[q] < -L ? -L : (uv[q] > L ? L : uv[q]);
+                const float s = round_bf(sigmoid_f(round_bf(xg * al)));
+                const float og = round_bf(xg * s);
+                const float da = round_bf(dh * round_bf(xl + 1.0f));  // d(glu output)
+                const float dl = round_bf(dh * og);                    // d(linear + 1)
+                const float ds = round_bf(da * xg);                    // d(sigmoid output)
+                const float dz = round_bf((ds * (1.0f - s)) * s);      // sigmoid_backward
+                const float dxg = round_bf(da * s) + round_bf(dz * al);
+                dg[q] = gv[q] <= L ? dxg : 0.f;                        // clamp(max=L) backward
+                du[q] = (uv[q] >= -L && uv[q] <= L) ? dl : 0.f;        // clamp(-L, L) backward
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const float dh = round_bf(acc[i][j][q]);
+                const float sl = round_bf(silu_f(gv[q]));
+                const float dsl = round_bf(dh * uv[q]);
+                du[q] = dh * sl;
+                const float sg = 1.0f / (1.0f + expf(-gv[q]));
+                dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
+              }
             }
             const int64_t o2 = (int64_t)r * (2 * H) + hh;
             *(uint2*)(p.out_dgu + o2) = make_uint2(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]));
@@ -477,14 +554,17 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int m = mt * BM + wm * WM + i * 16 + ml;
+        if (TAIL && m >= Mfix) continue;
         uint16_t* rowp;
         if (MODE == kBwdDw13)
-          rowp = (m < H) ? p.out_dw1 + (e64 * H + m) * (int64_t)D : p.out_dw3 + (e64 * H + (m - H)) * (int64_t)D;
+          rowp = (m < H) ? p.out_dw1 + e64 * p.w13_estride + m * p.w13_rstride
+                         : p.out_dw3 + e64 * p.w13_estride + (m - H) * p.w13_rstride;
         else
           rowp = p.out_dw2 + (e64 * D + m) * (int64_t)H;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int n = nt * BN + wn * WN + j * 16 + nq;
+          if (TAIL && n >= Ntot) continue;
           *(uint2*)(rowp + n) =
               make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3]));
         }
@@ -518,17 +598,27 @@ static int persistent_grid(int64_t max_tiles, int per_cu) {
 
 // One launch of grouped_gemm_kernel with NW waves in WGM x (NW / WGM), wave
 // tiles (16 TM) x (16 TN), NS LDS stages and OCC workgroups per CU.
-template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC>
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT>
 static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
   constexpr int BM = WGM * TM * 16, BN = (NW / WGM) * TN * 16;
+  auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
   int64_t max_tiles;
-  if (MODE == kFwdGateUp) max_tiles = (R / BM + p.E) * (2 * p.H / BN);
-  else if (MODE == kFwdDown || MODE == kBwdDx) max_tiles = (R / BM + p.E) * (p.D / BN);
-  else if (MODE == kBwdDgu) max_tiles = (R / BM + p.E) * (p.H / BN);
-  else if (MODE == kBwdDw13) max_tiles = (int64_t)p.E * (2 * p.H / BM) * (p.D / BN);
-  else max_tiles = (int64_t)p.E * (p.D / BM) * (p.H / BN);
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC>), dim3(persistent_grid(max_tiles, OCC)),
-                     dim3(NW * 64), 0, stream, p);
+  if (MODE == kFwdGateUp) max_tiles = (R / BM + p.E) * cdiv(2 * p.H, BN);
+  else if (MODE == kFwdDown || MODE == kBwdDx) max_tiles = (R / BM + p.E) * cdiv(p.D, BN);
+  else if (MODE == kBwdDgu) max_tiles = (R / BM + p.E) * cdiv(p.H, BN);
+  else if (MODE == kBwdDw13) max_tiles = (int64_t)p.E * cdiv(2 * p.H, BM) * cdiv(p.D, BN);
+  else max_tiles = (int64_t)p.E * cdiv(p.D, BM) * cdiv(p.H, BN);
+  bool tail;
+  if (MODE == kFwdGateUp) tail = (2 * p.H) % BN != 0;
+  else if (MODE == kFwdDown || MODE == kBwdDx) tail = p.D % BN != 0;
+  else if (MODE == kBwdDgu) tail = p.H % BN != 0;
+  else if (MODE == kBwdDw13) tail = (2 * p.H) % BM != 0 || p.D % BN != 0;
+  else tail = p.D % BM != 0 || p.H % BN != 0;
+  const dim3 grid(persistent_grid(max_tiles, OCC)), block(NW * 64);
+  if (tail)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC, ACT, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC, ACT, false>), grid, block, 0, stream, p);
 }
 
 // Tile per mode (measured at the Kimi and DSv3 shapes). The forward modes run
@@ -536,28 +626,28 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 // one eight-wave workgroup per CU with three LDS stages and wider tiles, which
 // halves the copy traffic per flop of the dW operands: 128 x 512 (dgu, and dx
 // when D is a multiple of 512), 128 x 384 (dx, D a multiple of 384), 256 x 256
-// (dW). D and H are multiples of 256 (check_gemm_shape). The tail skip is
+// (dW). D and H are multiples of 64 (check_gemm_shape). The tail skip is
 // compiled into the row-grouped modes except dx, whose second copy of the K
 // loop costs more registers than the skip saves.
-template <int MODE>
+template <int MODE, int ACT = kSwiGLU>
 static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
   if constexpr (MODE == kFwdGateUp || MODE == kFwdDown) {
-    launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2>(p, R, stream);
+    launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2, ACT>(p, R, stream);
   } else if constexpr (MODE == kBwdDgu) {
-    if (p.H % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, true, 1>(p, R, stream);
-    else launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2>(p, R, stream);
+    if (p.H % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, true, 1, ACT>(p, R, stream);
+    else launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2, ACT>(p, R, stream);
   } else if constexpr (MODE == kBwdDx) {
-    if (p.D % 384 == 0) launch_cfg<MODE, 8, 2, 4, 6, 3, false, 1>(p, R, stream);
-    else if (p.D % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, false, 1>(p, R, stream);
-    else launch_cfg<MODE, 4, 2, 4, 8, 2, false, 2>(p, R, stream);
+    if (p.D % 384 == 0) launch_cfg<MODE, 8, 2, 4, 6, 3, false, 1, ACT>(p, R, stream);
+    else if (p.D % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, false, 1, ACT>(p, R, stream);
+    else launch_cfg<MODE, 4, 2, 4, 8, 2, false, 2, ACT>(p, R, stream);
   } else {
-    launch_cfg<MODE, 8, 4, 4, 8, 3, false, 1>(p, R, stream);
+    launch_cfg<MODE, 8, 4, 4, 8, 3, false, 1, kSwiGLU>(p, R, stream);
   }
 }
 
 static int check_gemm_shape(int64_t R, int32_t E, int32_t D, int32_t H) {
-  if (R < 0 || E < 1 || E > kGemmMaxE || D < 256 || H < 256) return kErrInvalidArgument;
-  if (D % 256 || H % 256) return kErrUnsupportedShape;
+  if (R < 0 || E < 1 || E > kGemmMaxE || D < 64 || H < 64) return kErrInvalidArgument;
+  if (D % 64 || H % 64) return kErrUnsupportedShape;
   if (R >= (int64_t)INT32_MAX / 2) return kErrUnsupportedShape;
   return kOk;
 }
@@ -573,6 +663,8 @@ static int gemm_params(GemmParams& p, const int64_t* counts, int64_t n_rows, int
   if (!counts) return kErrInvalidArgument;
   p = GemmParams{};
   p.counts = counts; p.R = n_rows; p.E = n_experts; p.D = dim; p.H = hidden;
+  p.w13_estride = (int64_t)hidden * dim;
+  p.w13_rstride = dim;
   return kOk;
 }
 
@@ -677,4 +769,103 @@ MOE_API int moe_grouped_swiglu_bwd(const uint16_t* dy, const uint16_t* x, const 
   st = moe_grouped_gemm_bwd_dw13(dgu_workspace, x, counts, n_rows, n_experts, dim, hidden, dw1, dw3, stream);
   if (st) return st;
   return moe_grouped_gemm_bwd_dw2(dy, h, counts, n_rows, n_experts, dim, hidden, dw2, stream);
+}
+
+// ---------------------------------------------------------------------------
+// gpt-oss experts (torchtitan/models/gpt_oss/moe.py:92-122): mlp1_weight
+// [E, 2H, D] with glu row 2j and linear row 2j + 1, mlp1_bias [E, 2H],
+// mlp2_weight [E, D, H], mlp2_bias [E, D]; swiglu with alpha 1.702 and a
+// clamp limit. The same kernels with interleaved w1 / w3 row strides and the
+// biased, clamped epilogues; the saved g / u are the biased pre-clamp halves.
+// ---------------------------------------------------------------------------
+
+static constexpr float kOssAlpha = 1.702f;
+
+static int oss_params(GemmParams& p, const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                      int32_t hidden, const uint16_t* mlp1) {
+  const int st = gemm_params(p, counts, n_rows, n_experts, dim, hidden);
+  if (st) return st;
+  p.w1 = mlp1;
+  p.w3 = mlp1 ? mlp1 + dim : nullptr;
+  p.w13_estride = 2 * (int64_t)hidden * dim;
+  p.w13_rstride = 2 * (int64_t)dim;
+  p.alpha = kOssAlpha;
+  return kOk;
+}
+
+static float bf16_round_host(float v) {
+  uint32_t u;
+  std::memcpy(&u, &v, 4);
+  if ((u & 0x7f800000u) != 0x7f800000u) u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+MOE_API int moe_grouped_gemm_oss_gate_up(const uint16_t* x, const uint16_t* mlp1_weight, const uint16_t* mlp1_bias,
+                                         const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                         int32_t hidden, float swiglu_limit, uint16_t* g, uint16_t* u, uint16_t* h,
+                                         hipStream_t stream) {
+  GemmParams p;
+  int st = oss_params(p, counts, n_rows, n_experts, dim, hidden, mlp1_weight);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!x || !mlp1_weight || !mlp1_bias || !g || !u || !h) return kErrInvalidArgument;
+  p.x = x; p.b1 = mlp1_bias; p.limit = bf16_round_host(swiglu_limit);
+  p.out_g = g; p.out_u = u; p.out_h = h;
+  launch_mode<kFwdGateUp, kOssGLU>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_oss_down(const uint16_t* h, const uint16_t* mlp2_weight, const uint16_t* mlp2_bias,
+                                      const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                      int32_t hidden, uint16_t* y, hipStream_t stream) {
+  GemmParams p;
+  int st = oss_params(p, counts, n_rows, n_experts, dim, hidden, nullptr);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!h || !mlp2_weight || !mlp2_bias || !y) return kErrInvalidArgument;
+  p.h = h; p.w2 = mlp2_weight; p.b2 = mlp2_bias; p.out_y = y;
+  launch_mode<kFwdDown, kOssGLU>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_oss_bwd_dgu(const uint16_t* dy, const uint16_t* mlp2_weight, const uint16_t* g,
+                                         const uint16_t* u, const int64_t* counts, int64_t n_rows,
+                                         int32_t n_experts, int32_t dim, int32_t hidden, float swiglu_limit,
+                                         uint16_t* dgu, hipStream_t stream) {
+  GemmParams p;
+  int st = oss_params(p, counts, n_rows, n_experts, dim, hidden, nullptr);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!dy || !mlp2_weight || !g || !u || !dgu) return kErrInvalidArgument;
+  p.dy = dy; p.w2 = mlp2_weight; p.g = g; p.u = u; p.out_dgu = dgu; p.limit = bf16_round_host(swiglu_limit);
+  launch_mode<kBwdDgu, kOssGLU>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_oss_bwd_dx(const uint16_t* dgu, const uint16_t* mlp1_weight, const int64_t* counts,
+                                        int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                                        uint16_t* dx, hipStream_t stream) {
+  GemmParams p;
+  int st = oss_params(p, counts, n_rows, n_experts, dim, hidden, mlp1_weight);
+  if (st) return st;
+  if (n_rows == 0) return kOk;
+  if (!dgu || !mlp1_weight || !dx) return kErrInvalidArgument;
+  p.dgu = dgu; p.out_dx = dx;
+  launch_mode<kBwdDx, kOssGLU>(p, n_rows, stream);
+  return launch_status();
+}
+
+MOE_API int moe_grouped_gemm_oss_bwd_dw1(const uint16_t* dgu, const uint16_t* x, const int64_t* counts,
+                                         int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
+                                         uint16_t* dmlp1_weight, hipStream_t stream) {
+  GemmParams p;
+  int st = oss_params(p, counts, n_rows, n_experts, dim, hidden, nullptr);
+  if (st) return st;
+  if (!dmlp1_weight || (n_rows > 0 && (!dgu || !x))) return kErrInvalidArgument;
+  p.dgu = dgu; p.x = x; p.out_dw1 = dmlp1_weight; p.out_dw3 = dmlp1_weight + dim;
+  launch_mode<kBwdDw13>(p, n_rows, stream);
+  return launch_status();
 }

@@ -438,6 +438,103 @@ combine.register_autograd(_combine_bwd, setup_context=_combine_setup)
 
 
 # ---------------------------------------------------------------------------
+# gpt-oss experts: biased, clamped SwiGLU with interleaved mlp1 rows
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_oss", mutates_args=())
+def grouped_swiglu_oss(
+    x: Tensor, mlp1_weight: Tensor, mlp1_bias: Tensor, mlp2_weight: Tensor, mlp2_bias: Tensor,
+    num_tokens_per_expert: Tensor, swiglu_limit: float,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """gpt-oss grouped experts (gpt_oss/moe.py:92-122) in bf16: returns y [R, D]
+    and the saved g, u (biased pre-clamp halves of h1) and h [R, H]."""
+    require_gpu(x, mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, num_tokens_per_expert)
+    x, w1, w2 = (t.contiguous() for t in (x, mlp1_weight, mlp2_weight))
+    for t, name in ((x, "x"), (w1, "mlp1_weight"), (w2, "mlp2_weight")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"grouped_swiglu_oss expects bfloat16 {name}, got {t.dtype}")
+    b1 = mlp1_bias.to(torch.bfloat16).contiguous()
+    b2 = mlp2_bias.to(torch.bfloat16).contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h2, _ = w1.shape
+    h_dim = h2 // 2
+    s = stream_of(x)
+    g = x.new_empty(r, h_dim)
+    u = x.new_empty(r, h_dim)
+    h = x.new_empty(r, h_dim)
+    y = x.new_empty(r, d)
+    call("moe_grouped_gemm_oss_gate_up", ptr(x), ptr(w1), ptr(b1), ptr(counts), r, e, d, h_dim, float(swiglu_limit),
+         ptr(g), ptr(u), ptr(h), s)
+    call("moe_grouped_gemm_oss_down", ptr(h), ptr(w2), ptr(b2), ptr(counts), r, e, d, h_dim, ptr(y), s)
+    return y, g, u, h
+
+
+@grouped_swiglu_oss.register_fake
+def _(x, mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, num_tokens_per_expert, swiglu_limit):
+    r, d = x.shape
+    h_dim = mlp1_weight.shape[1] // 2
+    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_oss_backward", mutates_args=())
+def grouped_swiglu_oss_backward(
+    dy: Tensor, x: Tensor, mlp1_weight: Tensor, mlp1_bias: Tensor, mlp2_weight: Tensor, mlp2_bias: Tensor,
+    num_tokens_per_expert: Tensor, g: Tensor, u: Tensor, h: Tensor, swiglu_limit: float,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients (dx, dmlp1_weight, dmlp1_bias, dmlp2_weight, dmlp2_bias); the
+    bias gradients are fp32 per-expert sums in a fixed order, cast to the bias dtype."""
+    require_gpu(dy, x, mlp1_weight, mlp2_weight, num_tokens_per_expert, g, u, h)
+    dy = dy.to(torch.bfloat16).contiguous()
+    x, w1, w2 = (t.contiguous() for t in (x, mlp1_weight, mlp2_weight))
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h2, _ = w1.shape
+    h_dim = h2 // 2
+    s = stream_of(x)
+    dgu = x.new_empty(r, 2 * h_dim)
+    call("moe_grouped_gemm_oss_bwd_dgu", ptr(dy), ptr(w2), ptr(g), ptr(u), ptr(counts), r, e, d, h_dim,
+         float(swiglu_limit), ptr(dgu), s)
+    dx = x.new_empty(r, d)
+    call("moe_grouped_gemm_oss_bwd_dx", ptr(dgu), ptr(w1), ptr(counts), r, e, d, h_dim, ptr(dx), s)
+    dw1 = torch.empty_like(w1)
+    call("moe_grouped_gemm_oss_bwd_dw1", ptr(dgu), ptr(x), ptr(counts), r, e, d, h_dim, ptr(dw1), s)
+    dw2 = torch.empty_like(w2)
+    call("moe_grouped_gemm_bwd_dw2", ptr(dy), ptr(h), ptr(counts), r, e, d, h_dim, ptr(dw2), s)
+    db1 = torch.empty(e, 2 * h_dim, dtype=torch.float32, device=x.device)
+    call("moe_grouped_col_sum", ptr(dgu), 2 * h_dim, ptr(counts), r, e, h_dim, ptr(db1), 2 * h_dim, 2, s)
+    call("moe_grouped_col_sum", dgu.data_ptr() + 2 * h_dim, 2 * h_dim, ptr(counts), r, e, h_dim,
+         db1.data_ptr() + 4, 2 * h_dim, 2, s)
+    db2 = torch.empty(e, d, dtype=torch.float32, device=x.device)
+    call("moe_grouped_col_sum", ptr(dy), d, ptr(counts), r, e, d, ptr(db2), d, 1, s)
+    return dx, dw1, db1.to(mlp1_bias.dtype), dw2, db2.to(mlp2_bias.dtype)
+
+
+@grouped_swiglu_oss_backward.register_fake
+def _(dy, x, mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, num_tokens_per_expert, g, u, h, swiglu_limit):
+    return (x.new_empty(x.shape), torch.empty_like(mlp1_weight), torch.empty_like(mlp1_bias),
+            torch.empty_like(mlp2_weight), torch.empty_like(mlp2_bias))
+
+
+def _oss_setup(ctx, inputs, output):
+    x, w1, b1, w2, b2, counts, limit = inputs
+    _, g, u, h = output
+    ctx.save_for_backward(x, w1, b1, w2, b2, counts, g, u, h)
+    ctx.swiglu_limit = limit
+    ctx.set_materialize_grads(False)
+
+
+def _oss_bwd(ctx, dy, _dg, _du, _dh):
+    x, w1, b1, w2, b2, counts, g, u, h = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None, None, None, None
+    dx, dw1, db1, dw2, db2 = grouped_swiglu_oss_backward(dy, x, w1, b1, w2, b2, counts, g, u, h, ctx.swiglu_limit)
+    return dx, dw1, db1, dw2, db2, None, None
+
+
+grouped_swiglu_oss.register_autograd(_oss_bwd, setup_context=_oss_setup)
+
+
+# ---------------------------------------------------------------------------
 # fp8 e4m3 grouped SwiGLU experts (dynamic rowwise scaling, fp32 accumulate)
 # ---------------------------------------------------------------------------
 FP8 = torch.uint8  # fp8 e4m3fn bytes as produced by the quantizers
