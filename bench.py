@@ -69,10 +69,16 @@ WORKLOADS = {
         score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
         score_before=True, std=0.02, bias=0.01, zipf=None, mxfp8=True,
     ),
+    "gptoss_20b": dict(
+        desc="gpt-oss-20b-shape MoE layer (biased clamped-SwiGLU experts, biased softmax gate)",
+        bs=4, slen=4096, dim=2880, experts=32, top_k=4, hidden=2880, shared_hidden=0,
+        score_func="softmax", route_norm=True, route_scale=1.0, groups=None, limited=None,
+        score_before=False, std=0.02, bias=0.01, zipf=None, gptoss=True,
+    ),
 }
 
-GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm", "mxfp8_gemm")
-                     for m in ("gate_up", "down", "bwd_dgu", "bwd_dx", "bwd_dw13", "bwd_dw2"))
+GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm", "mxfp8_gemm", "grouped_gemm_oss")
+                     for m in ("gate_up", "down", "bwd_dgu", "bwd_dx", "bwd_dw13", "bwd_dw1", "bwd_dw2"))
 
 
 def kernel_work(name: str, w: dict) -> tuple[str, float]:
@@ -83,8 +89,8 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
     d, e, k, h = w["dim"], w["experts"], w["top_k"], w["hidden"]
     r = n * k
     b = 2  # bf16 rows
-    flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw2": 2}
-    for kind in ("moe_grouped_gemm_", "moe_fp8_gemm_", "moe_mxfp8_gemm_"):
+    flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw1": 4, "bwd_dw2": 2}
+    for kind in ("moe_grouped_gemm_oss_", "moe_grouped_gemm_", "moe_fp8_gemm_", "moe_mxfp8_gemm_"):
         if name.startswith(kind) and name[len(kind):] in flops:
             return "mfma", float(flops[name[len(kind):]] * r * d * h)
     nbytes = {
@@ -110,13 +116,16 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
 
 def make_layer(w: dict, device: torch.device, seed: int):
     from torchtitan_amd import FeedForward, GroupedExperts, Linear, MoE, TokenChoiceTopKRouter
+    from torchtitan_amd.gpt_oss import GptOssMoE
 
     d, e, h, hs = w["dim"], w["experts"], w["hidden"], w["shared_hidden"]
-    cfg = MoE.Config(
+    cls = GptOssMoE if w.get("gptoss") else MoE
+    cfg = cls.Config(
         num_experts=e,
         experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e),
         router=TokenChoiceTopKRouter.Config(
-            num_experts=e, gate=Linear.Config(in_features=d, out_features=e), top_k=w["top_k"],
+            num_experts=e, gate=Linear.Config(in_features=d, out_features=e, bias=bool(w.get("gptoss"))),
+            top_k=w["top_k"],
             score_func=w["score_func"], route_norm=w["route_norm"], route_scale=w["route_scale"],
             num_expert_groups=w["groups"], num_limited_groups=w["limited"],
         ),
@@ -166,21 +175,24 @@ def cpu_baseline(moe, w: dict, x: torch.Tensor, g: torch.Tensor, n_tokens: int) 
         threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
     torch.set_num_threads(threads)
     sd = {k: v.detach().cpu() for k, v in moe.state_dict().items()}
-    params = {
-        "gate": sd["router.gate.weight"], "w1": sd["experts.w1"], "w2": sd["experts.w2"],
-        "w3": sd["experts.w3"], "expert_bias": sd["expert_bias"],
-    }
+    params = {"gate": sd["router.gate.weight"], "expert_bias": sd["expert_bias"]}
+    if w.get("gptoss"):
+        params["gate_bias"] = sd["router.gate.bias"]
+        params.update({k: sd[f"experts.{k}"] for k in ("mlp1_weight", "mlp1_bias", "mlp2_weight", "mlp2_bias")})
+    else:
+        params.update(w1=sd["experts.w1"], w2=sd["experts.w2"], w3=sd["experts.w3"])
     if w["shared_hidden"]:
         params.update(sw1=sd["shared_experts.w1.weight"], sw2=sd["shared_experts.w2.weight"],
                       sw3=sd["shared_experts.w3.weight"])
-    for k in ("gate", "w1", "w2", "w3", "sw1", "sw2", "sw3"):
-        if k in params:
-            params[k].requires_grad_(True)
+    for k, p in params.items():
+        if k != "expert_bias":
+            p.requires_grad_(True)
     rc = R.RouterCfg(num_experts=w["experts"], top_k=w["top_k"], score_func=w["score_func"],
                      num_expert_groups=w["groups"], num_limited_groups=w["limited"],
                      route_norm=w["route_norm"], route_scale=w["route_scale"])
     cfg = R.MoECfg(router=rc, dim=w["dim"], hidden_dim=w["hidden"], score_before_experts=w["score_before"],
-                   use_grouped_mm=True, has_shared=bool(w["shared_hidden"]))
+                   use_grouped_mm=True, has_shared=bool(w["shared_hidden"]),
+                   expert_kind="gptoss" if w.get("gptoss") else "swiglu")
     xs = x.reshape(-1, w["dim"])[:n_tokens].detach().cpu().reshape(1, n_tokens, w["dim"])
     gs = g.reshape(-1, w["dim"])[:n_tokens].detach().cpu().reshape(1, n_tokens, w["dim"])
     times = []

@@ -346,11 +346,13 @@ def oss_swiglu(h1: torch.Tensor, limit: float, alpha: float = OSS_ALPHA) -> torc
     return out_glu * (x_linear + 1)
 
 
-def oss_experts_grouped_mm(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, limit, x, counts):
+def oss_experts_grouped_mm(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, limit, x, counts, aux=None):
     """The grouped-mm path (gpt_oss/moe.py:92-122) with the reference's torch
     calls: torch._grouped_mm over int32 offsets, biases broadcast per row with
     repeat_interleave (plus the zero row for rows past the groups) and added in
-    bf16, then the clamped SwiGLU and the second grouped GEMM."""
+    bf16, then the clamped SwiGLU and the second grouped GEMM. With `aux`, the
+    biased h1 and the output keep their gradients (aux["h1"], aux["y"]): the
+    rows whose per-expert sums are the bias gradients."""
     offsets = torch.cumsum(counts, dim=0, dtype=torch.int32)
     tail = (x.shape[0] - offsets[-1]).unsqueeze(0).to(counts.dtype)
     counts_long = torch.cat([counts, tail]).long()
@@ -358,11 +360,18 @@ def oss_experts_grouped_mm(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, limit
     b1 = torch.cat([mlp1_bias, mlp1_bias.new_zeros(1, mlp1_bias.shape[-1])])
     b1 = b1.repeat_interleave(counts_long, dim=0, output_size=x.shape[0])
     h = h + b1.to(h.dtype)
+    if aux is not None and h.requires_grad:
+        h.retain_grad()
+        aux["h1"] = h
     h = oss_swiglu(h, limit)
     h = torch._grouped_mm(h, mlp2_weight.transpose(-2, -1).bfloat16(), offs=offsets)
     b2 = torch.cat([mlp2_bias, mlp2_bias.new_zeros(1, mlp2_bias.shape[-1])])
     b2 = b2.repeat_interleave(counts_long, dim=0, output_size=x.shape[0])
-    return h + b2.to(h.dtype)
+    y = h + b2.to(h.dtype)
+    if aux is not None and y.requires_grad:
+        y.retain_grad()
+        aux["y"] = y
+    return y
 
 
 def oss_experts_for_loop(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, limit, x, counts):
@@ -394,6 +403,8 @@ class MoECfg:
     score_before_experts: bool = True
     use_grouped_mm: bool = True
     has_shared: bool = False
+    expert_kind: str = "swiglu"  # or "gptoss" (gpt_oss/moe.py GptOssGroupedExperts)
+    swiglu_limit: float = 7.0
 
 
 def moe_forward(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None,
@@ -496,7 +507,7 @@ def _deterministic_scatter_add(out: torch.Tensor, index: torch.Tensor, src: torc
         torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
 
 
-def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg) -> torch.Tensor:
+def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None) -> torch.Tensor:
     """MoE.forward (moe.py:380-477) with the router (moe.py:211-274), the
     reorderer (moe.py:291-332), _run_experts_grouped_mm (moe.py:53-70) and the
     shared FeedForward (feed_forward.py:53-54) written as the same torch calls
@@ -517,7 +528,7 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg) -> tor
     with warnings.catch_warnings():
         warnings.simplefilter("ignore")
         with torch.autocast(device_type=x.device.type, dtype=torch.float32):
-            logits = F.linear(x2, gate_w)
+            logits = F.linear(x2, gate_w, params.get("gate_bias"))
     top_scores, idx, _counts, _scores = router_forward_torch(logits, params.get("expert_bias"), rc)
     flat = idx.view(-1)
     counts = _histc_counts(flat, rc.num_experts)
@@ -527,14 +538,21 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg) -> tor
     routed_input = x2[token_idx]
     if cfg.score_before_experts:
         routed_input = (routed_input.to(torch.float32) * scores_sorted.reshape(-1, 1)).to(x2.dtype)
-    w1, w2, w3 = params["w1"], params["w2"], params["w3"]
-    if cfg.use_grouped_mm:
+    if cfg.expert_kind == "gptoss":
+        run = oss_experts_grouped_mm if cfg.use_grouped_mm else oss_experts_for_loop
+        kw = {"aux": aux} if cfg.use_grouped_mm else {}
+        routed_output = run(params["mlp1_weight"], params["mlp1_bias"], params["mlp2_weight"], params["mlp2_bias"],
+                            cfg.swiglu_limit, routed_input, counts, **kw)
+        if aux is not None:
+            aux["counts"] = counts
+    elif cfg.use_grouped_mm:
+        w1, w2, w3 = params["w1"], params["w2"], params["w3"]
         offsets = torch.cumsum(counts, dim=0, dtype=torch.int32)
         h = F.silu(torch._grouped_mm(routed_input.bfloat16(), w1.bfloat16().transpose(-2, -1), offs=offsets))
         h = h * torch._grouped_mm(routed_input.bfloat16(), w3.bfloat16().transpose(-2, -1), offs=offsets)
         routed_output = torch._grouped_mm(h, w2.bfloat16().transpose(-2, -1), offs=offsets).type_as(routed_input)
     else:
-        routed_output = experts_for_loop(w1, w2, w3, routed_input, counts)
+        routed_output = experts_for_loop(params["w1"], params["w2"], params["w3"], routed_input, counts)
     if cfg.has_shared:
         out = feed_forward(x2, params["sw1"], params["sw2"], params["sw3"])
     else:

@@ -30,17 +30,25 @@ class LayerShape:
     zipf: float | None = None
     fp8: bool = False
     mxfp8: bool = False
+    gptoss: bool = False  # gpt-oss experts (GptOssMoE) and a gate with bias
+    swiglu_limit: float = 7.0
 
 
 def build_layer(sh: LayerShape, dev: torch.device, seed: int):
     from torchtitan_amd import FeedForward, GroupedExperts, Linear, MoE, TokenChoiceTopKRouter
 
     d, e, h, hs = sh.dim, sh.experts, sh.hidden, sh.shared_hidden
-    cfg = MoE.Config(
+    moe_cls = MoE
+    extra = {}
+    if sh.gptoss:
+        from torchtitan_amd.gpt_oss import GptOssMoE
+
+        moe_cls, extra = GptOssMoE, {"swiglu_limit": sh.swiglu_limit}
+    cfg = moe_cls.Config(
         num_experts=e,
         experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e),
         router=TokenChoiceTopKRouter.Config(
-            num_experts=e, gate=Linear.Config(in_features=d, out_features=e), top_k=sh.top_k,
+            num_experts=e, gate=Linear.Config(in_features=d, out_features=e, bias=sh.gptoss), top_k=sh.top_k,
             score_func=sh.score_func, route_norm=sh.route_norm, route_scale=sh.route_scale,
             num_expert_groups=sh.groups[0] if sh.groups else None,
             num_limited_groups=sh.groups[1] if sh.groups else None),
@@ -48,6 +56,7 @@ def build_layer(sh: LayerShape, dev: torch.device, seed: int):
         shared_experts=FeedForward.Config(
             w1=Linear.Config(in_features=d, out_features=hs), w2=Linear.Config(in_features=hs, out_features=d),
             w3=Linear.Config(in_features=d, out_features=hs)) if hs else None,
+        **extra,
     )
     with torch.device("meta"):
         moe = cfg.build()
@@ -89,8 +98,12 @@ def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape
     out.backward(g)
 
     sd = moe.state_dict()
-    names = {"gate": "router.gate.weight", "w1": "experts.w1", "w2": "experts.w2", "w3": "experts.w3",
-             "expert_bias": "expert_bias"}
+    if sh.gptoss:
+        names = {"gate": "router.gate.weight", "gate_bias": "router.gate.bias", "expert_bias": "expert_bias",
+                 **{k: f"experts.{k}" for k in ("mlp1_weight", "mlp1_bias", "mlp2_weight", "mlp2_bias")}}
+    else:
+        names = {"gate": "router.gate.weight", "w1": "experts.w1", "w2": "experts.w2", "w3": "experts.w3",
+                 "expert_bias": "expert_bias"}
     if sh.shared_hidden:
         names.update(sw1="shared_experts.w1.weight", sw2="shared_experts.w2.weight",
                      sw3="shared_experts.w3.weight")
@@ -100,25 +113,49 @@ def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape
                      num_expert_groups=sh.groups[0] if sh.groups else None,
                      num_limited_groups=sh.groups[1] if sh.groups else None)
     mc = R.MoECfg(router=rc, dim=d, hidden_dim=sh.hidden, score_before_experts=sh.score_before,
-                  use_grouped_mm=True, has_shared=bool(sh.shared_hidden))
+                  use_grouped_mm=True, has_shared=bool(sh.shared_hidden),
+                  expert_kind="gptoss" if sh.gptoss else "swiglu", swiglu_limit=sh.swiglu_limit)
     xb = x.clone().requires_grad_(True)
-    ref = R.moe_forward_reference_ops(params, xb, mc)
+    aux = {}
+    ref = R.moe_forward_reference_ops(params, xb, mc, aux=aux)
     ref.backward(g)
 
     x2 = x.view(-1, d)
     with torch.no_grad():
         top, idx, counts = moe.router(x2, moe.expert_bias)
         with torch.autocast(device_type="cuda", dtype=torch.float32):
-            logits = torch.nn.functional.linear(x2, params["gate"].detach())
+            gb = params.get("gate_bias")
+            logits = torch.nn.functional.linear(x2, params["gate"].detach(), None if gb is None else gb.detach())
         t_top, t_idx, t_counts, _ = R.router_forward_torch(logits, params["expert_bias"], rc)
     assert torch.equal(idx, t_idx), "selected experts differ from the reference op sequence"
     assert torch.equal(counts, t_counts), "tokens per expert differ"
     assert torch.equal(top, t_top), "top scores differ"
     pairs = {"out": (out, ref), "grad_x": (xa.grad, xb.grad),
-             "grad_gate": (moe.router.gate.weight.grad, params["gate"].grad),
-             "grad_w1": (moe.experts.w1.grad, params["w1"].grad),
-             "grad_w2": (moe.experts.w2.grad, params["w2"].grad),
-             "grad_w3": (moe.experts.w3.grad, params["w3"].grad)}
+             "grad_gate": (moe.router.gate.weight.grad, params["gate"].grad)}
+    res_extra = {}
+    if sh.gptoss:
+        pairs["grad_gate_bias"] = (moe.router.gate.bias.grad, params["gate_bias"].grad)
+        for k in ("mlp1_weight", "mlp2_weight"):
+            pairs[f"grad_{k}"] = (getattr(moe.experts, k).grad, params[k].grad)
+        # bias gradients: the reference sums each expert's rows with bf16 atomics
+        # (index_add through repeat_interleave); ours sums in fp32. Both are compared
+        # with the exact (fp64) per-expert sums of the reference's own row gradients.
+        bounds = torch.cumsum(aux["counts"], 0).tolist()
+        def seg_sums(rows):
+            rows, out, s0 = rows.double(), [], 0
+            for s1 in bounds:
+                out.append(rows[s0:s1].sum(0))
+                s0 = s1
+            return torch.stack(out)
+        exact1, exact2 = seg_sums(aux["h1"].grad), seg_sums(aux["y"].grad)
+        pairs["grad_mlp1_bias"] = (moe.experts.mlp1_bias.grad, exact1)
+        pairs["grad_mlp2_bias"] = (moe.experts.mlp2_bias.grad, exact2)
+        res_extra["_ref_bias_grad_err"] = (rel_err(params["mlp1_bias"].grad, exact1),
+                                           rel_err(params["mlp2_bias"].grad, exact2))
+    else:
+        for k in ("w1", "w2", "w3"):
+            pairs[f"grad_{k}"] = (getattr(moe.experts, k).grad, params[k].grad)
     res = {k: (rel_err(a, b), bool(torch.equal(a, b))) for k, (a, b) in pairs.items()}
     res["_counts"] = counts.cpu()
+    res.update(res_extra)
     return res

@@ -12,11 +12,17 @@ run by torch on the same GPU (oracle.moe_forward_reference_ops):
          against the same bf16 reference (the reference's own fp8 path is
          torchao's and absent, so fp8 parity is unpinned);
   kimi_mxfp8  the same with MXFP8 grouped GEMMs (block-32 e8m0 scales, RCEIL;
-         torchao's as well, unpinned).
+         torchao's as well, unpinned);
+  gptoss_20b  gpt-oss-20b MoE layer: 8192 tokens, dim 2880, 32 experts top-4
+         softmax with a biased gate, hidden 2880, biased clamped-SwiGLU experts
+         (GptOssMoE), scores applied after the experts.
 
 Routing (indices, counts, top scores) must be bit-exact; the output and all
 gradients within 1e-2 normwise relative error (max |ours - ref| / max |ref|),
-0.1 for the fp8 and MXFP8 layers against the bf16 reference.
+0.1 for the fp8 and MXFP8 layers against the bf16 reference. The gpt-oss bias
+gradients are compared with the exact (fp64) per-expert sums of the reference's
+own row gradients: the reference accumulates them into bf16 parameters with
+bf16 atomics (index_add behind repeat_interleave), which this layer does in fp32.
 """
 
 import pytest
@@ -37,6 +43,8 @@ SHAPES = {
                            fp8=True),
     "kimi_mxfp8": LayerShape(bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
                              mxfp8=True),
+    "gptoss_20b": LayerShape(bs=1, slen=8192, dim=2880, experts=32, top_k=4, hidden=2880, shared_hidden=0,
+                             score_func="softmax", route_scale=1.0, score_before=False, gptoss=True),
 }
 
 TOL = {"kimi_fp8": 0.1, "kimi_mxfp8": 0.1}
@@ -49,6 +57,10 @@ def test_layer_at_benchmark_shape(dev, name):
     moe, x, g = build_layer(sh, dev, seed=7)
     res = compare_with_reference(moe, x, g, sh)
     counts = res.pop("_counts")
+    ref_bias = res.pop("_ref_bias_grad_err", None)
+    if ref_bias is not None:
+        print(f"[case] {name}: the reference's own bf16 bias gradients vs the exact sums: "
+              f"mlp1_bias {ref_bias[0]:.2e}, mlp2_bias {ref_bias[1]:.2e}", flush=True)
     print(f"[case] {name}: max load {int(counts.max())}, mean {counts.float().mean().item():.0f}, "
           f"empty experts {int((counts == 0).sum())}", flush=True)
     print(f"[case] {name}: " + ", ".join(f"{k} {v[0]:.2e}{' (bit-identical)' if v[1] else ''}"
