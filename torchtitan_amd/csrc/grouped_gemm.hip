@@ -253,36 +253,48 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
   const int dr = lane >> 2;
   const int dc = (lane & 3) ^ ((dr >> 1) & 3);
 
-  for (int t = lb; t < total_tiles; t += G) {
+  // ---- tiles ----
+  struct TileRef { int e, seg0, seg1, mt, nt, nk; };
+  auto decode = [&](int t) {
+    TileRef r;
     int lo = 0, hi = E - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_tile[mid] <= t) lo = mid; else hi = mid - 1;
     }
-    const int e = lo;
-    const int64_t e64 = e;
-    const int local = t - s_tile[e];
-    const int seg0 = s_seg[e], seg1 = s_seg[e + 1];
-    int mt, nt;
+    r.e = lo;
+    const int local = t - s_tile[lo];
+    r.seg0 = s_seg[lo];
+    r.seg1 = s_seg[lo + 1];
     if (T::kRowGrouped) {
-      const int mtiles = (seg1 - seg0 + BM - 1) / BM;
-      nt = local / mtiles;
-      mt = local - nt * mtiles;
+      const int mtiles = (r.seg1 - r.seg0 + BM - 1) / BM;
+      r.nt = local / mtiles;
+      r.mt = local - r.nt * mtiles;
     } else {
-      nt = local / MT;
-      mt = local - nt * MT;
+      r.nt = local / MT;
+      r.mt = local - r.nt * MT;
     }
-    const int Ktot = T::kRowGrouped ? Kfix : (seg1 - seg0);
-    const int nk = (Ktot + BK - 1) / BK;
-    const int row0 = seg0 + mt * BM;
+    const int Ktot = T::kRowGrouped ? Kfix : (r.seg1 - r.seg0);
+    r.nk = (Ktot + BK - 1) / BK;
+    return r;
+  };
 
-    // ---- per-lane copy sources (copy c of this wave covers LDS bytes [1 KB (wv CPW_X + c), +1 KB)) ----
-    const uint16_t* srcP[CPW_P];
-    const uint16_t* srcQ[CPW_Q];
-    const uint16_t* srcQ3[CPW_Q];  // dx: the w3 half of the k range
-    int klP[CPW_P], klQ[CPW_Q];    // k-major copies: the k-row this lane fills (P rows: the token row)
-    bool inP[CPW_P], inQ[CPW_Q];   // the copied m / n lies inside the matrix
-    int64_t stepP = BK, stepQ = BK;  // element advance per k-step
+  // ---- per-lane copy sources of the tile being copied (copy c of this wave covers
+  // LDS bytes [1 KB (wv CPW_X + c), +1 KB)) ----
+  const uint16_t* srcP[CPW_P];
+  const uint16_t* srcQ[CPW_Q];
+  const uint16_t* srcQ3[CPW_Q];  // dx: the w3 half of the k range
+  int klP[CPW_P], klQ[CPW_Q];    // k-major copies: the k-row this lane fills (P rows: the token row)
+  bool inP[CPW_P], inQ[CPW_Q];   // the copied m / n lies inside the matrix
+  int64_t stepP = BK, stepQ = BK;  // element advance per k-step
+  if constexpr (T::kPT) stepP = (int64_t)BK * ((MODE == kBwdDw13) ? 2 * H : D);
+  if constexpr (MODE == kBwdDgu) stepQ = (int64_t)BK * H;
+  if constexpr (MODE == kBwdDx) stepQ = (int64_t)BK * p.w13_rstride;
+  if constexpr (MODE == kBwdDw13) stepQ = (int64_t)BK * D;
+  if constexpr (MODE == kBwdDw2) stepQ = (int64_t)BK * H;
+  auto setup = [&](const TileRef& r) {
+    const int64_t e64 = r.e;
+    const int row0 = r.seg0 + r.mt * BM;
     if constexpr (!T::kPT) {
       const uint16_t* pb;
       int ldp;
@@ -292,82 +304,115 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       else { pb = p.dgu; ldp = 2 * H; }
 #pragma unroll
       for (int b = 0; b < CPW_P; ++b) {
-        const int r = row0 + (wv * CPW_P + b) * 16 + dr;
-        srcP[b] = pb + (int64_t)r * ldp + dc * 8;
-        klP[b] = r;  // rows past the segment copy the zero row
+        const int rr = row0 + (wv * CPW_P + b) * 16 + dr;
+        srcP[b] = pb + (int64_t)rr * ldp + dc * 8;
+        klP[b] = rr;  // rows past the segment copy the zero row
         inP[b] = true;
       }
     } else {
       const uint16_t* pb = (MODE == kBwdDw13) ? p.dgu : p.dy;
       const int ldp = (MODE == kBwdDw13) ? 2 * H : D;
-      stepP = (int64_t)BK * ldp;
 #pragma unroll
       for (int b = 0; b < CPW_P; ++b) {
         const int slot = (wv * CPW_P + b) * 64 + lane;
         const int kl = slot / CHP;
         const int c = (slot % CHP) ^ kswz(kl);
-        srcP[b] = pb + (int64_t)(seg0 + kl) * ldp + mt * BM + c * 8;
+        srcP[b] = pb + (int64_t)(r.seg0 + kl) * ldp + r.mt * BM + c * 8;
         klP[b] = kl;
-        inP[b] = mt * BM + c * 8 < Mfix;
+        inP[b] = r.mt * BM + c * 8 < Mfix;
       }
     }
     if constexpr (!T::kQT) {
 #pragma unroll
       for (int b = 0; b < CPW_Q; ++b) {
         const int n = (wv * CPW_Q + b) * 16 + dr;
-        inQ[b] = (MODE == kFwdGateUp) ? gate_up_col(nt, n, BN) < H : nt * BN + n < D;
-        const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, nt, n, BN)
-                                                     : p.w2 + (e64 * D + nt * BN + n) * (int64_t)H;
+        inQ[b] = (MODE == kFwdGateUp) ? gate_up_col(r.nt, n, BN) < H : r.nt * BN + n < D;
+        const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, r.nt, n, BN)
+                                                     : p.w2 + (e64 * D + r.nt * BN + n) * (int64_t)H;
         srcQ[b] = rowp + dc * 8;
         klQ[b] = 0;
       }
     } else {
       const uint16_t* qb;
-      int ldq;
+      int64_t ldq;
       if (MODE == kBwdDgu) { qb = p.w2 + e64 * D * (int64_t)H; ldq = H; }        // rows k of w2[e] (D x H)
-      else if (MODE == kBwdDx) { qb = p.w1 + e64 * p.w13_estride; ldq = (int)p.w13_rstride; }  // rows k of w1[e], then w3[e]
-      else if (MODE == kBwdDw13) { qb = p.x + (int64_t)seg0 * D; ldq = D; }
-      else { qb = p.h + (int64_t)seg0 * H; ldq = H; }
-      stepQ = (int64_t)BK * ldq;
+      else if (MODE == kBwdDx) { qb = p.w1 + e64 * p.w13_estride; ldq = p.w13_rstride; }  // rows k of w1[e], then w3[e]
+      else if (MODE == kBwdDw13) { qb = p.x + (int64_t)r.seg0 * D; ldq = D; }
+      else { qb = p.h + (int64_t)r.seg0 * H; ldq = H; }
 #pragma unroll
       for (int b = 0; b < CPW_Q; ++b) {
         const int slot = (wv * CPW_Q + b) * 64 + lane;
         const int kl = slot / CHQ;
         const int c = (slot % CHQ) ^ kswz(kl);
-        const int64_t off = (int64_t)kl * ldq + nt * BN + c * 8;
+        const int64_t off = (int64_t)kl * ldq + r.nt * BN + c * 8;
         srcQ[b] = qb + off;
         if (MODE == kBwdDx) srcQ3[b] = p.w3 + e64 * p.w13_estride + off;
         klQ[b] = kl;
-        inQ[b] = nt * BN + c * 8 < Ntot;
+        inQ[b] = r.nt * BN + c * 8 < Ntot;
       }
     }
+  };
 
-    auto issue = [&](int kt) {
-      const int s = kt % NS;
-      const int k0 = kt * BK;
+  // stage kt of tile r into LDS buffer s
+  auto issue = [&](const TileRef& r, int kt, int s) {
+    const int k0 = kt * BK;
 #pragma unroll
-      for (int b = 0; b < CPW_P; ++b) {
-        const uint16_t* src = srcP[b] + kt * stepP;
-        if constexpr (T::kPT) {
-          if (seg0 + k0 + klP[b] >= seg1 || (TAIL && !inP[b])) src = (const uint16_t*)kZeroRow;
-        } else {
-          if (klP[b] >= seg1) src = (const uint16_t*)kZeroRow;
-        }
-        dma16(src, lds_addr(&sP[s][(wv * CPW_P + b) * 512]));
+    for (int b = 0; b < CPW_P; ++b) {
+      const uint16_t* src = srcP[b] + kt * stepP;
+      if constexpr (T::kPT) {
+        if (r.seg0 + k0 + klP[b] >= r.seg1 || (TAIL && !inP[b])) src = (const uint16_t*)kZeroRow;
+      } else {
+        if (klP[b] >= r.seg1) src = (const uint16_t*)kZeroRow;
       }
+      dma16(src, lds_addr(&sP[s][(wv * CPW_P + b) * 512]));
+    }
 #pragma unroll
-      for (int b = 0; b < CPW_Q; ++b) {
-        const uint16_t* src = srcQ[b] + kt * stepQ;
-        if constexpr (MODE == kBwdDx) {
-          if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * p.w13_rstride;
-        }
-        if constexpr (MODE >= kBwdDw13) {
-          if (seg0 + k0 + klQ[b] >= seg1) src = (const uint16_t*)kZeroRow;
-        }
-        if (TAIL && !inQ[b]) src = (const uint16_t*)kZeroRow;
-        dma16(src, lds_addr(&sQ[s][(wv * CPW_Q + b) * 512]));
+    for (int b = 0; b < CPW_Q; ++b) {
+      const uint16_t* src = srcQ[b] + kt * stepQ;
+      if constexpr (MODE == kBwdDx) {
+        if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * p.w13_rstride;
       }
-    };
+      if constexpr (MODE >= kBwdDw13) {
+        if (r.seg0 + k0 + klQ[b] >= r.seg1) src = (const uint16_t*)kZeroRow;
+      }
+      if (TAIL && !inQ[b]) src = (const uint16_t*)kZeroRow;
+      dma16(src, lds_addr(&sQ[s][(wv * CPW_Q + b) * 512]));
+    }
+  };
+
+  // One stream of copy stages across this workgroup's tiles: the copy cursor
+  // (tile ct_i, step ik) runs NS - 1 stages ahead of the MFMAs, through tile
+  // boundaries, so the next tile's first stages are in flight while this tile's
+  // epilogue runs. Stage g uses LDS buffer g % NS. Tiles without k-steps (dW of
+  // an expert without tokens) have no stages.
+  int ct_i = lb, ik = 0, gi = 0, gc = 0;
+  TileRef ir{};
+  auto seek = [&](int t0) {
+    for (ct_i = t0; ct_i < total_tiles; ct_i += G) {
+      ir = decode(ct_i);
+      if (ir.nk > 0) {
+        setup(ir);
+        break;
+      }
+    }
+    ik = 0;
+  };
+  auto issue_next = [&]() {
+    issue(ir, ik, gi % NS);
+    ++gi;
+    if (++ik == ir.nk) seek(ct_i + G);
+  };
+  seek(lb);
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (ct_i < total_tiles) issue_next();
+
+  for (int t = lb; t < total_tiles; t += G) {
+    const TileRef cr = decode(t);
+    const int e = cr.e;
+    const int64_t e64 = e;
+    const int seg1 = cr.seg1, mt = cr.mt, nt = cr.nt, nk = cr.nk;
+    const int row0 = cr.seg0 + mt * BM;
 
     f32x4_t acc[TM][TN];
 #pragma unroll
@@ -416,19 +461,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
           }
         }
       };
-      // the previous tile's LDS reads are done in every wave
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#pragma unroll
-      for (int i = 0; i < NS - 1; ++i)
-        if (i < nk) issue(i);
       for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed in every wave once at most the later stages' copies are
-        // outstanding; the barrier also retires every wave's reads of the buffer refilled next
-        if (NS == 3 && kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(CPW) : "memory");
+        // stage gc has landed in every wave once at most the one stage issued after it
+        // is outstanding (stores of the previous epilogue only add to the count); the
+        // barrier also retires every wave's reads of the buffer refilled next
+        if (NS == 3 && gi - gc >= 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(CPW) : "memory");
         else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (kt + NS - 1 < nk) issue(kt + NS - 1);
+        if (ct_i < total_tiles) issue_next();
         if (MODE == kBwdDx && ACT == kSwiGLU && kt == kt_half) park_dx_half();
-        if (decltype(full)::value || tmv > 0) compute(kt % NS);
+        if (decltype(full)::value || tmv > 0) compute(gc % NS);
+        ++gc;
       }
     };
     if (!SKIP || tmv == TM) run(std::true_type{});
