@@ -323,6 +323,20 @@ int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n
                              int32_t cols, int64_t padded_rows, uint8_t* q, uint8_t* scale,
                              moe_stream_t stream);
 
+/* Both MX layouts from one read of x [E, a, b] (weights): q_rows [E, a, b] with
+ * scale_rows [E, a, b/32] (as moe_mxfp8_quant_rows on [E*a, b]) and the
+ * transposed layout of moe_mxfp8_quant_cols_t (same strides). */
+int moe_mxfp8_quant_dual_cols(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q_rows,
+                              uint8_t* scale_rows, uint8_t* q, int64_t q_expert_stride, int64_t q_row_stride,
+                              uint8_t* scale, int64_t scale_expert_stride, int64_t scale_row_stride,
+                              moe_stream_t stream);
+/* Both MX layouts from one read of x [n_rows, cols] in token groups: q_rows
+ * [n_rows, cols] with scale_rows [n_rows, cols/32] for the rows of the groups,
+ * and the token-transposed layout of moe_mxfp8_quant_tokens_t. */
+int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                int32_t cols, int64_t padded_rows, uint8_t* q_rows, uint8_t* scale_rows,
+                                uint8_t* q, uint8_t* scale, moe_stream_t stream);
+
 /* MXFP8 g, u, h as moe_fp8_gemm_gate_up; sx [R, D/32], sw1 and sw3 [E, H, D/32]. */
 int moe_mxfp8_gemm_gate_up(const uint8_t* qx, const uint8_t* sx, const uint8_t* qw1, const uint8_t* sw1,
                            const uint8_t* qw3, const uint8_t* sw3, const int64_t* counts, int64_t n_rows,

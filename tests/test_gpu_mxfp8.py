@@ -101,6 +101,27 @@ def test_mxfp8_quantizers_bit_exact(dev):
     used = sum((n + 31) // 32 * 32 for _, n in segs)
     assert torch.equal(q2[:, :used], rq2[:, :used])
     assert torch.equal(s2[:used // 32], rs2[:used // 32])
+    # dual: one read, both layouts
+    qr, sr, qt, st_ = ops._mx_dual_tokens(xt.to(dev), counts.to(dev), len(counts), rpad)
+    rqr, rsr = R.quant_mxfp8(xt)
+    assert torch.equal(qr.cpu(), rqr.view(torch.uint8)) and torch.equal(sr.cpu(), rsr)
+    assert torch.equal(qt.cpu()[:, :used], rq2[:, :used]) and torch.equal(st_.cpu()[:used // 32], rs2[:used // 32])
+    w1 = (torch.randn(e, 2 * a, b, generator=g) * torch.exp(torch.randn(e, 2 * a, 1, generator=g))).bfloat16()
+    w3 = torch.randn(e, 2 * a, b, generator=g).bfloat16()
+    w2 = torch.randn(e, b, 2 * a, generator=g).bfloat16()
+    outs = ops._mx_weights(w1.to(dev), w2.to(dev), w3.to(dev), True)
+    qw1, sw1, qw3, sw3, qw2, sw2, qw2t, sw2t, qw13t, sw13t = (t.cpu() for t in outs)
+    hh_ = 2 * a
+    for w, q_, s_ in ((w1, qw1, sw1), (w3, qw3, sw3), (w2, qw2, sw2)):
+        rq, rs = R.quant_mxfp8(w.reshape(-1, w.shape[-1]))
+        assert torch.equal(q_, rq.view(torch.uint8)) and torch.equal(s_, rs)
+    for i in range(e):
+        rq, rs = R.quant_mxfp8(w2[i].t())
+        assert torch.equal(qw2t[i], rq.view(torch.uint8)) and torch.equal(sw2t[i], rs)
+        for half, w in ((0, w1), (1, w3)):
+            rq, rs = R.quant_mxfp8(w[i].t())
+            assert torch.equal(qw13t[i][:, half * hh_:(half + 1) * hh_], rq.view(torch.uint8))
+            assert torch.equal(sw13t[i][:, half * hh_ // 32:(half + 1) * hh_ // 32], rs)
 
 
 def test_mxfp8_gemm_entry_points_match_emulation(dev):
@@ -215,10 +236,13 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("for_backward", [True, False])
 @pytest.mark.parametrize("name", list(CASES))
-def test_mxfp8_grouped_swiglu_fwd_bwd(dev, name):
+def test_mxfp8_grouped_swiglu_fwd_bwd(dev, name, for_backward):
+    """for_backward=True: the forward's dual quantizers keep the transposed
+    layouts for the backward; False: the backward quantizes them itself."""
     e, d, h, counts = CASES[name]
-    banner(f"mxfp8 grouped swiglu {name}")
+    banner(f"mxfp8 grouped swiglu {name} for_backward={for_backward}")
     from torchtitan_amd import ops
 
     g = torch.Generator().manual_seed(1)
@@ -230,7 +254,7 @@ def test_mxfp8_grouped_swiglu_fwd_bwd(dev, name):
     dy = torch.randn(r, d, generator=g).bfloat16()
     cnt = torch.tensor(counts, dtype=torch.int64)
     xs, a, b, c = (t.to(dev).requires_grad_(True) for t in (x, w1, w2, w3))
-    y, gg, uu, hh = ops.grouped_swiglu_mxfp8(xs, a, b, c, cnt.to(dev))
+    y, gg, uu, hh, *_ = ops.grouped_swiglu_mxfp8(xs, a, b, c, cnt.to(dev), for_backward)
     y.backward(dy.to(dev))
     torch.cuda.synchronize()
     ey, eg, eu, eh = R.experts_mxfp8_forward(w1, w2, w3, x, cnt)

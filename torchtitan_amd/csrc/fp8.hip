@@ -124,6 +124,14 @@ __device__ __forceinline__ uint2 quant8(uint4 v, float s) {
   return make_uint2(lo, hi);
 }
 
+__device__ __forceinline__ uint2 mx_quant8(uint4 v, float f) {
+  const uint32_t lo = e4m3(bf_lo(v.x) * f) | (e4m3(bf_hi(v.x) * f) << 8) | (e4m3(bf_lo(v.y) * f) << 16) |
+                      (e4m3(bf_hi(v.y) * f) << 24);
+  const uint32_t hi = e4m3(bf_lo(v.z) * f) | (e4m3(bf_hi(v.z) * f) << 8) | (e4m3(bf_lo(v.w) * f) << 16) |
+                      (e4m3(bf_hi(v.w) * f) << 24);
+  return make_uint2(lo, hi);
+}
+
 // One wave per row of x [rows, K] (K % 8 == 0). With CPL > 0 the row (up to
 // 64 * CPL 16-byte chunks) stays in registers between the amax and the
 // quantize step, so it is read once; CPL == 0 reads it twice.
@@ -194,51 +202,93 @@ __device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int
   __syncthreads();
 }
 
-constexpr int kSlabRows = 128;  // rows transposed per pass
+constexpr int kTRows = 128;  // slab rows transposed per pass
 
-// Transposes a [rows x 64] bf16 slab (128 rows per pass, four loads in flight
-// per thread) into 64 output rows of fp8 (one per slab column), quantized with
-// that column's scale. out row b starts at out + b * ldo; rows >= n_rows up to
-// n_out (a multiple of 16) are zero.
-__device__ __forceinline__ void slab_transpose_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows,
-                                                     int n_out, uint8_t* __restrict__ out, int64_t ldo,
-                                                     const float* s_scale, uint16_t (*s_tile)[kSlabRows + 2]) {
+// Quantizes a [n_rows x 64] bf16 slab (row stride ld) transposed: output row b
+// (slab column b) holds n_out values at out + b * ldo, rows >= n_rows zero
+// (n_out a multiple of 16, and of 32 for MX).
+//  * fp8 (MX false): column b scaled by s_col[b];
+//  * MX: one e8m0 scale per (column b, 32-row block k) at sc + b * sc_b + k * sc_k;
+//  * ROWS (MX): the same read also quantizes the slab along its columns (the
+//    row-wise MX layout, blocks of 32 columns): row r's 64 values go to
+//    qr + r * ldr and its two block scales to sr + r * ldsr.
+// A pass moves 128 rows (four 16-byte loads per thread) through s_tile
+// (128 row-major rows of 128 bytes, written with 16-byte stores); thread
+// (c, j) then reads column c of rows [32 j, 32 j + 32) as 2-byte reads (a wave
+// reads one row at a time: conflict-free). The next pass's loads are issued as
+// soon as the tile is in LDS.
+template <bool MX, bool ROWS>
+__device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows, int n_out,
+                                             uint8_t* __restrict__ out, int64_t ldo, uint8_t* __restrict__ sc,
+                                             int64_t sc_b, int64_t sc_k, const float* s_col, uint32_t* s_tile,
+                                             uint8_t* __restrict__ qr = nullptr, int64_t ldr = 0,
+                                             uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0) {
   const int t = threadIdx.x;
-  for (int a0 = 0; a0 < n_out; a0 += kSlabRows) {
-    uint4 v[4];
+  const int col = t & 63, j = t >> 6;
+  uint4 v[4];
+  auto load = [&](int a0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * 256;
       const int r = c >> 3, ch = c & 7;
       v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
     }
+  };
+  if (n_out > 0) load(0);
+  for (int a0 = 0; a0 < n_out; a0 += kTRows) {
+    if constexpr (ROWS) {
+      // lanes t, t ^ 1, t ^ 2, t ^ 3 hold the four 8-column chunks of one 32-column block
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = t + i * 256;
+        const int r = c >> 3, ch = c & 7;
+        float a = amax8(v[i]);
+        a = fmaxf(a, __shfl_xor(a, 1));
+        a = fmaxf(a, __shfl_xor(a, 2));
+        const uint32_t e = mx_exponent(a);
+        if (a0 + r < n_rows) {
+          *(uint2*)(qr + (int64_t)(a0 + r) * ldr + ch * 8) = mx_quant8(v[i], mx_multiplier(e));
+          if ((ch & 3) == 0) sr[(int64_t)(a0 + r) * ldsr + (ch >> 2)] = (uint8_t)e;
+        }
+      }
+    }
+    __syncthreads();  // every thread's reads of the previous pass are done
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * 256;
-      const int r = c >> 3, ch = c & 7;
-      const uint16_t* pv = (const uint16_t*)&v[i];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_tile[ch * 8 + j][r] = pv[j];
+      *(uint4*)(s_tile + (c >> 3) * 32 + (c & 7) * 4) = v[i];
     }
     __syncthreads();
-    // write: thread -> (column b, 32 rows as two 16-byte stores)
-    const int b = t >> 2, seg = (t & 3) * 32;
-    const float s = s_scale[b];
+    if (a0 + kTRows < n_out) load(a0 + kTRows);
+    const int rb = a0 + j * 32;
+    if (rb < n_out) {
+      const uint16_t* xs = (const uint16_t*)s_tile + j * 32 * 64 + col;  // row k of the block at xs[64 k]
+      float f;
+      uint32_t e = 0;
+      if constexpr (MX) {
+        float am = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int rr = seg + 16 * h;
-      if (a0 + rr < n_out) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          w[j] = 0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) w[j] |= e4m3(bf2f(s_tile[b][rr + 4 * j + i]) / s) << (8 * i);
-        }
-        *(uint4*)(out + (int64_t)b * ldo + a0 + rr) = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int k = 0; k < 32; ++k) am = fmaxf(am, fabsf(bf2f(xs[64 * k])));
+        e = mx_exponent(am);
+        f = mx_multiplier(e);
+      } else {
+        f = s_col[col];
       }
+      uint32_t o[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        o[q] = 0;
+#pragma unroll
+        for (int bq = 0; bq < 4; ++bq) {
+          const float xv = bf2f(xs[64 * (4 * q + bq)]);
+          o[q] |= (MX ? e4m3(xv * f) : e4m3(xv / f)) << (8 * bq);
+        }
+      }
+      uint8_t* d = out + (int64_t)col * ldo + rb;
+      *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
+      if (rb + 32 <= n_out) *(uint4*)(d + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+      if constexpr (MX) sc[(int64_t)col * sc_b + (int64_t)(rb / kMxBlock) * sc_k] = (uint8_t)e;
     }
-    __syncthreads();
   }
 }
 
@@ -249,7 +299,7 @@ __global__ __launch_bounds__(256) void quant_cols_t_kernel(const uint16_t* __res
                                                            float* __restrict__ scale, int64_t s_estride) {
   __shared__ float s_red[64 * 33];
   __shared__ float s_amax[64];
-  __shared__ uint16_t s_tile[64][kSlabRows + 2];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
   const int nb = B / 64;
   const int64_t e = blockIdx.x / nb;
   const int b0 = (blockIdx.x % nb) * 64;
@@ -261,7 +311,7 @@ __global__ __launch_bounds__(256) void quant_cols_t_kernel(const uint16_t* __res
     scale[e * s_estride + b0 + threadIdx.x] = s;
   }
   __syncthreads();
-  slab_transpose_quant(base, B, A, A, q + e * q_estride + b0 * q_ld, q_ld, s_amax, s_tile);
+  slab_t_quant<false, false>(base, B, A, A, q + e * q_estride + b0 * q_ld, q_ld, nullptr, 0, 0, s_amax, s_tile);
 }
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
@@ -272,7 +322,7 @@ __global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __r
                                                              uint8_t* __restrict__ q, float* __restrict__ scale) {
   __shared__ float s_red[64 * 33];
   __shared__ float s_amax[64];
-  __shared__ uint16_t s_tile[64][kSlabRows + 2];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
   __shared__ int s_tmp[8];
   __shared__ int s_seg[2];
   const int nc = C / 64;
@@ -308,20 +358,14 @@ __global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __r
     scale[(int64_t)e * C + c0 + threadIdx.x] = s;
   }
   __syncthreads();
-  slab_transpose_quant(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, s_amax, s_tile);
+  slab_t_quant<false, false>(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, nullptr, 0, 0, s_amax,
+                             s_tile);
 }
 
 // ---------------------------------------------------------------------------
 // MXFP8 quantizers
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ uint2 mx_quant8(uint4 v, float f) {
-  const uint32_t lo = e4m3(bf_lo(v.x) * f) | (e4m3(bf_hi(v.x) * f) << 8) | (e4m3(bf_lo(v.y) * f) << 16) |
-                      (e4m3(bf_hi(v.y) * f) << 24);
-  const uint32_t hi = e4m3(bf_lo(v.z) * f) | (e4m3(bf_hi(v.z) * f) << 8) | (e4m3(bf_lo(v.w) * f) << 16) |
-                      (e4m3(bf_hi(v.w) * f) << 24);
-  return make_uint2(lo, hi);
-}
 
 // x viewed as n_chunks 16-byte chunks of 8 bf16 (rows of K, K % 32 == 0): four
 // consecutive lanes hold one 32-element block, reduce its amax by shuffles
@@ -352,81 +396,49 @@ __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint4* __restr
   }
 }
 
-// MX counterpart of slab_transpose_quant: a [rows x 64] bf16 slab becomes 64
-// output rows of fp8 along the slab's rows, one e8m0 scale per 32 of them.
-// Scale of (slab column b, block k) at sc + b * sc_b + k * sc_k. Rows >=
-// n_rows up to n_out (a multiple of 32) are zero.
-__device__ __forceinline__ void mx_slab_transpose_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows,
-                                                        int n_out, uint8_t* __restrict__ out, int64_t ldo,
-                                                        uint8_t* __restrict__ sc, int64_t sc_b, int64_t sc_k,
-                                                        uint16_t (*s_tile)[kSlabRows + 2]) {
-  const int t = threadIdx.x;
-  for (int a0 = 0; a0 < n_out; a0 += kSlabRows) {
-    uint4 v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = t + i * 256;
-      const int r = c >> 3, ch = c & 7;
-      v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = t + i * 256;
-      const int r = c >> 3, ch = c & 7;
-      const uint16_t* pv = (const uint16_t*)&v[i];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_tile[ch * 8 + j][r] = pv[j];
-    }
-    __syncthreads();
-    // thread -> (column b, one 32-row block)
-    const int b = t >> 2, rr = (t & 3) * kMxBlock;
-    if (a0 + rr < n_out) {
-      const uint32_t* row = (const uint32_t*)&s_tile[b][rr];  // 4-byte aligned: row stride 260 bytes, rr even
-      uint32_t w[16];
-      float a = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        w[i] = row[i];
-        a = fmaxf(a, fmaxf(fabsf(bf_lo(w[i])), fabsf(bf_hi(w[i]))));
-      }
-      const uint32_t e = mx_exponent(a);
-      const float f = mx_multiplier(e);
-      uint32_t o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        o[i] = e4m3(bf_lo(w[2 * i]) * f) | (e4m3(bf_hi(w[2 * i]) * f) << 8) | (e4m3(bf_lo(w[2 * i + 1]) * f) << 16) |
-               (e4m3(bf_hi(w[2 * i + 1]) * f) << 24);
-      uint8_t* dst = out + (int64_t)b * ldo + a0 + rr;
-      *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
-      *(uint4*)(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
-      sc[(int64_t)b * sc_b + (int64_t)((a0 + rr) / kMxBlock) * sc_k] = (uint8_t)e;
-    }
-    __syncthreads();
-  }
-}
-
 // x [E][A][B] -> q rows (e, b) of A values at q + e * q_estride + b * q_ld, and
 // their A/32 scales at s + e * s_estride + b * s_ld. Block per (e, 64 columns).
 __global__ __launch_bounds__(256) void mx_quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
                                                               uint8_t* __restrict__ q, int64_t q_estride,
                                                               int64_t q_ld, uint8_t* __restrict__ s,
                                                               int64_t s_estride, int64_t s_ld) {
-  __shared__ uint16_t s_tile[64][kSlabRows + 2];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
   const int nb = B / 64;
   const int64_t e = blockIdx.x / nb;
   const int b0 = (blockIdx.x % nb) * 64;
-  mx_slab_transpose_quant(x + e * A * (int64_t)B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
-                          s + e * s_estride + b0 * s_ld, s_ld, 1, s_tile);
+  slab_t_quant<true, false>(x + e * A * (int64_t)B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
+                            s + e * s_estride + b0 * s_ld, s_ld, 1, nullptr, s_tile);
+}
+
+// Both MX layouts of x [E][A][B] from one read: the row-wise one (q_r [E][A][B],
+// s_r [E][A][B / 32], as mx_quant_rows on [E A, B]) and the transposed one of
+// mx_quant_cols_t. Block per (e, 64 columns).
+__global__ __launch_bounds__(256) void mx_dual_cols_kernel(const uint16_t* __restrict__ x, int A, int B,
+                                                           uint8_t* __restrict__ q, int64_t q_estride, int64_t q_ld,
+                                                           uint8_t* __restrict__ s, int64_t s_estride, int64_t s_ld,
+                                                           uint8_t* __restrict__ qr, uint8_t* __restrict__ sr) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
+  const int nb = B / 64;
+  const int64_t e = blockIdx.x / nb;
+  const int b0 = (blockIdx.x % nb) * 64;
+  const int64_t row0 = e * A;  // first row of expert e in the [E A, B] view
+  slab_t_quant<true, true>(x + row0 * B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
+                           s + e * s_estride + b0 * s_ld, s_ld, 1, nullptr, s_tile, qr + row0 * B + b0, B,
+                           sr + row0 * (B / kMxBlock) + b0 / kMxBlock, B / kMxBlock);
 }
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
 // 32-aligned offset pstart_e, zero padded to ceil32(count_e)) and the scales
 // k-block major, s [Rpad / 32][C]. Block per (e, 64 columns); empty groups exit.
+// With ROWS, the same read also writes the row-wise layout of the group's rows
+// (qr [R][C], sr [R][C / 32]).
+template <bool ROWS>
 __global__ __launch_bounds__(256) void mx_quant_tokens_t_kernel(const uint16_t* __restrict__ x,
                                                                 const int64_t* __restrict__ counts, int64_t R, int E,
                                                                 int C, int64_t Rpad, uint8_t* __restrict__ q,
-                                                                uint8_t* __restrict__ s) {
-  __shared__ uint16_t s_tile[64][kSlabRows + 2];
+                                                                uint8_t* __restrict__ s, uint8_t* __restrict__ qr,
+                                                                uint8_t* __restrict__ sr) {
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
   __shared__ int s_tmp[8];
   __shared__ int s_seg[3];
   const int nc = C / 64;
@@ -453,8 +465,10 @@ __global__ __launch_bounds__(256) void mx_quant_tokens_t_kernel(const uint16_t* 
   if ((int64_t)seg0 + n > R) n = (int)(R - seg0 > 0 ? R - seg0 : 0);
   const int n_out = (n + kMxPad - 1) / kMxPad * kMxPad;
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
-  mx_slab_transpose_quant(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
-                          s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C, s_tile);
+  slab_t_quant<true, ROWS>(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
+                           s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C, nullptr, s_tile,
+                                ROWS ? qr + (int64_t)seg0 * C + c0 : nullptr, C,
+                                ROWS ? sr + (int64_t)seg0 * (C / kMxBlock) + c0 / kMxBlock : nullptr, C / kMxBlock);
 }
 
 // ---------------------------------------------------------------------------
@@ -1114,8 +1128,34 @@ MOE_API int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, i
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
   if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
   if (!x || !counts || !q || !scale) return kErrInvalidArgument;
-  hipLaunchKernelGGL(mx_quant_tokens_t_kernel, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts, n_rows,
-                     n_experts, cols, padded_rows, q, scale);
+  hipLaunchKernelGGL(mx_quant_tokens_t_kernel<false>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
+                     n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_quant_dual_cols(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q_rows,
+                                      uint8_t* scale_rows, uint8_t* q, int64_t q_expert_stride, int64_t q_row_stride,
+                                      uint8_t* scale, int64_t scale_expert_stride, int64_t scale_row_stride,
+                                      hipStream_t stream) {
+  if (n_experts < 1 || a < kMxBlock || a % kMxBlock || b < 64 || b % 64) return kErrInvalidArgument;
+  if (q_row_stride < a || q_row_stride % 16 || q_expert_stride < (int64_t)(b - 1) * q_row_stride + a)
+    return kErrInvalidArgument;
+  if (scale_row_stride < a / kMxBlock || scale_expert_stride < (int64_t)(b - 1) * scale_row_stride + a / kMxBlock)
+    return kErrInvalidArgument;
+  if (!x || !q || !scale || !q_rows || !scale_rows) return kErrInvalidArgument;
+  hipLaunchKernelGGL(mx_dual_cols_kernel, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
+                     q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride, q_rows, scale_rows);
+  return launch_status();
+}
+
+MOE_API int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                        int32_t cols, int64_t padded_rows, uint8_t* q_rows, uint8_t* scale_rows,
+                                        uint8_t* q, uint8_t* scale, hipStream_t stream) {
+  if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
+  if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
+  if (!x || !counts || !q || !scale || !q_rows || !scale_rows) return kErrInvalidArgument;
+  hipLaunchKernelGGL(mx_quant_tokens_t_kernel<true>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
+                     n_rows, n_experts, cols, padded_rows, q, scale, q_rows, scale_rows);
   return launch_status();
 }
 

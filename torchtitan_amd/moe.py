@@ -90,8 +90,9 @@ def _run_experts_grouped_mm_mxfp8(
     MXFP8TrainingOpConfig, recipe "mxfp8_rceil" (torchtitan/components/quantization/mx.py:85-128):
     e4m3 elements with one e8m0 scale per 32 along each contraction, fp32
     accumulation, bf16 outputs."""
-    y, _, _, _ = ops.grouped_swiglu_mxfp8(
-        x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16(), num_tokens_per_expert
+    for_backward = torch.is_grad_enabled() and any(t.requires_grad for t in (w1, w2, w3, x))
+    y, *_ = ops.grouped_swiglu_mxfp8(
+        x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16(), num_tokens_per_expert, for_backward
     )
     return y.type_as(x)
 

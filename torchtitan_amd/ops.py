@@ -698,12 +698,59 @@ def _check_bf16(op: str, **tensors: Tensor) -> None:
             raise TypeError(f"{op} expects bfloat16 {name}, got {t.dtype}")
 
 
+def _mx_dual_tokens(x: Tensor, counts: Tensor, e: int, rpad: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """One read of x [R, C] (token groups) -> the row-wise MX layout (q [R, C],
+    e8m0 [R, C / 32]) and the token-transposed one (q [C, rpad], e8m0 [rpad / 32, C])."""
+    r, c = x.shape
+    qr = torch.empty(r, c, dtype=FP8, device=x.device)
+    sr = torch.empty(r, c // MX_BLOCK, dtype=torch.uint8, device=x.device)
+    qt = torch.empty(c, rpad, dtype=FP8, device=x.device)
+    st = torch.empty(rpad // MX_BLOCK, c, dtype=torch.uint8, device=x.device)
+    call("moe_mxfp8_quant_dual_tokens", ptr(x), ptr(counts), r, e, c, rpad, ptr(qr), ptr(sr), ptr(qt), ptr(st),
+         stream_of(x))
+    return qr, sr, qt, st
+
+
+def _mx_weights(w1: Tensor, w2: Tensor, w3: Tensor, transposed: bool) -> tuple[Tensor, ...]:
+    """Row-wise MX layouts of w1, w3 (blocks along D) and w2 (along H); with
+    `transposed`, the same reads also write the backward's layouts: w2^T
+    [E, H, D] (blocks along D) and [w1^T | w3^T] [E, D, 2H] (blocks along H)."""
+    e, h_dim, d = w1.shape
+    dev = w1.device
+    s = stream_of(w1)
+    if not transposed:
+        qw1, sw1 = _mx_quant_rows(w1, d)
+        qw3, sw3 = _mx_quant_rows(w3, d)
+        qw2, sw2 = _mx_quant_rows(w2, h_dim)
+        return qw1, sw1, qw3, sw3, qw2, sw2
+    qw1 = torch.empty(e * h_dim, d, dtype=FP8, device=dev)
+    sw1 = torch.empty(e * h_dim, d // MX_BLOCK, dtype=torch.uint8, device=dev)
+    qw3, sw3 = torch.empty_like(qw1), torch.empty_like(sw1)
+    qw2 = torch.empty(e * d, h_dim, dtype=FP8, device=dev)
+    sw2 = torch.empty(e * d, h_dim // MX_BLOCK, dtype=torch.uint8, device=dev)
+    qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
+    sw2t = torch.empty(e, h_dim, d // MX_BLOCK, dtype=torch.uint8, device=dev)
+    nb = 2 * h_dim // MX_BLOCK
+    qw13t = torch.empty(e, d, 2 * h_dim, dtype=FP8, device=dev)
+    sw13t = torch.empty(e, d, nb, dtype=torch.uint8, device=dev)
+    call("moe_mxfp8_quant_dual_cols", ptr(w2), e, d, h_dim, ptr(qw2), ptr(sw2), ptr(qw2t), h_dim * d, d, ptr(sw2t),
+         h_dim * (d // MX_BLOCK), d // MX_BLOCK, s)
+    call("moe_mxfp8_quant_dual_cols", ptr(w1), e, h_dim, d, ptr(qw1), ptr(sw1), ptr(qw13t), d * 2 * h_dim, 2 * h_dim,
+         ptr(sw13t), d * nb, nb, s)
+    call("moe_mxfp8_quant_dual_cols", ptr(w3), e, h_dim, d, ptr(qw3), ptr(sw3), qw13t.data_ptr() + h_dim,
+         d * 2 * h_dim, 2 * h_dim, sw13t.data_ptr() + h_dim // MX_BLOCK, d * nb, nb, s)
+    return qw1, sw1, qw3, sw3, qw2, sw2, qw2t, sw2t, qw13t, sw13t
+
+
 @torch.library.custom_op("moe_mi355x::grouped_swiglu_mxfp8", mutates_args=())
 def grouped_swiglu_mxfp8(
-    x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
-) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor, for_backward: bool = False
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """MXFP8 grouped SwiGLU: x, h and the weights quantized in 32-element
-    blocks along each GEMM's contraction; bf16 outputs (y, g, u, h)."""
+    blocks along each GEMM's contraction; bf16 outputs (y, g, u, h). With
+    `for_backward`, the same quantizer reads also produce the layouts the
+    backward contracts over (x^T, h^T per token group; w1^T, w3^T, w2^T),
+    returned after (y, g, u, h); otherwise those are empty."""
     require_gpu(x, w1, w2, w3, num_tokens_per_expert)
     _check_bf16("grouped_swiglu_mxfp8", x=x, w1=w1, w2=w2, w3=w3)
     x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
@@ -711,72 +758,78 @@ def grouped_swiglu_mxfp8(
     r, d = x.shape
     e, h_dim, _ = w1.shape
     s = stream_of(x)
-    qx, sx = _mx_quant_rows(x, d)
-    qw1, sw1 = _mx_quant_rows(w1, d)
-    qw3, sw3 = _mx_quant_rows(w3, d)
-    qw2, sw2 = _mx_quant_rows(w2, h_dim)
+    def empty():  # distinct placeholders: custom-op outputs may not alias each other
+        return x.new_empty(0, dtype=torch.uint8)
+    if for_backward:
+        rpad = _mx_padded_rows(r, e)
+        qx, sx, qxt, sxt = _mx_dual_tokens(x, counts, e, rpad)
+        qw1, sw1, qw3, sw3, qw2, sw2, qw2t, sw2t, qw13t, sw13t = _mx_weights(w1, w2, w3, True)
+    else:
+        qx, sx = _mx_quant_rows(x, d)
+        qw1, sw1, qw3, sw3, qw2, sw2 = _mx_weights(w1, w2, w3, False)
+        qxt, sxt, qw2t, sw2t, qw13t, sw13t = (empty() for _ in range(6))
     g = x.new_empty(r, h_dim)
     u = x.new_empty(r, h_dim)
     h = x.new_empty(r, h_dim)
     y = x.new_empty(r, d)
     call("moe_mxfp8_gemm_gate_up", ptr(qx), ptr(sx), ptr(qw1), ptr(sw1), ptr(qw3), ptr(sw3), ptr(counts), r, e, d,
          h_dim, ptr(g), ptr(u), ptr(h), s)
-    qh, sh = _mx_quant_rows(h, h_dim)
+    if for_backward:
+        qh, sh, qht, sht = _mx_dual_tokens(h, counts, e, rpad)
+    else:
+        qh, sh = _mx_quant_rows(h, h_dim)
+        qht, sht = empty(), empty()
     call("moe_mxfp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
-    return y, g, u, h
+    return y, g, u, h, qxt, sxt, qht, sht, qw2t, sw2t, qw13t, sw13t
 
 
 @grouped_swiglu_mxfp8.register_fake
-def _(x, w1, w2, w3, num_tokens_per_expert):
+def _(x, w1, w2, w3, num_tokens_per_expert, for_backward=False):
     r, d = x.shape
-    h_dim = w1.shape[1]
-    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+    e, h_dim, _ = w1.shape
+    bf = (x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim))
+    u8 = lambda *shape: x.new_empty(*shape, dtype=torch.uint8)  # noqa: E731
+    if not for_backward:
+        return (*bf, *(u8(0) for _ in range(8)))
+    rpad = (r + e * 31 + 31) // 32 * 32
+    return (*bf, u8(d, rpad), u8(rpad // 32, d), u8(h_dim, rpad), u8(rpad // 32, h_dim),
+            u8(e, h_dim, d), u8(e, h_dim, d // 32), u8(e, d, 2 * h_dim), u8(e, d, 2 * h_dim // 32))
 
 
 @torch.library.custom_op("moe_mi355x::grouped_swiglu_mxfp8_backward", mutates_args=())
 def grouped_swiglu_mxfp8_backward(
     dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
-    g: Tensor, u: Tensor, h: Tensor,
+    g: Tensor, u: Tensor, h: Tensor, qxt: Tensor, sxt: Tensor, qht: Tensor, sht: Tensor,
+    qw2t: Tensor, sw2t: Tensor, qw13t: Tensor, sw13t: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients from the forward's transposed quantizations; dy and dgu are
+    quantized once each, in both layouts."""
     require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
     dy = dy.to(torch.bfloat16).contiguous()
     counts = num_tokens_per_expert.to(torch.int64).contiguous()
     r, d = x.shape
     e, h_dim, _ = w1.shape
-    dev = x.device
     s = stream_of(x)
-    # dh = dy . w2 (contraction over D): dy and w2 per (e, h) column, both blocked along D
-    qdy, sdy = _mx_quant_rows(dy, d)
-    qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
-    sw2t = torch.empty(e, h_dim, d // MX_BLOCK, dtype=torch.uint8, device=dev)
-    call("moe_mxfp8_quant_cols_t", ptr(w2), e, d, h_dim, ptr(qw2t), h_dim * d, d, ptr(sw2t),
-         h_dim * (d // MX_BLOCK), d // MX_BLOCK, s)
+    rpad = _mx_padded_rows(r, e)
+    if qxt.numel() == 0:  # the forward ran without for_backward
+        qxt, sxt = _mx_quant_tokens_t(x.contiguous(), counts, e, rpad)
+        qht, sht = _mx_quant_tokens_t(h, counts, e, rpad)
+        *_, qw2t, sw2t, qw13t, sw13t = _mx_weights(w1.contiguous(), w2.contiguous(), w3.contiguous(), True)
+    # dh = dy . w2 (contraction over D)
+    qdy, sdy, qdyt, sdyt = _mx_dual_tokens(dy, counts, e, rpad)
     dgu = x.new_empty(r, 2 * h_dim)
     call("moe_mxfp8_gemm_bwd_dgu", ptr(qdy), ptr(sdy), ptr(qw2t), ptr(sw2t), ptr(g), ptr(u), ptr(counts), r, e, d,
          h_dim, ptr(dgu), s)
-    # dx = dg . w1 + du . w3 (contraction over H, blocks never straddle the halves):
-    # w1 and w3 per (e, d) column, written side by side as [E, D, 2H]
-    qdgu, sdgu = _mx_quant_rows(dgu, 2 * h_dim)
-    qw13t = torch.empty(e, d, 2 * h_dim, dtype=FP8, device=dev)
-    nb = 2 * h_dim // MX_BLOCK
-    sw13t = torch.empty(e, d, nb, dtype=torch.uint8, device=dev)
-    call("moe_mxfp8_quant_cols_t", ptr(w1), e, h_dim, d, ptr(qw13t), d * 2 * h_dim, 2 * h_dim, ptr(sw13t),
-         d * nb, nb, s)
-    call("moe_mxfp8_quant_cols_t", ptr(w3), e, h_dim, d, qw13t.data_ptr() + h_dim, d * 2 * h_dim, 2 * h_dim,
-         sw13t.data_ptr() + h_dim // MX_BLOCK, d * nb, nb, s)
+    # dx = dg . w1 + du . w3 (contraction over H; blocks never straddle the halves)
+    qdgu, sdgu, qdgut, sdgut = _mx_dual_tokens(dgu, counts, e, rpad)
     dx = x.new_empty(r, d)
     call("moe_mxfp8_gemm_bwd_dx", ptr(qdgu), ptr(sdgu), ptr(qw13t), ptr(sw13t), ptr(counts), r, e, d, h_dim,
          ptr(dx), s)
     # weight gradients: contraction over each expert's tokens (groups padded to 32)
-    rpad = _mx_padded_rows(r, e)
-    qdgut, sdgut = _mx_quant_tokens_t(dgu, counts, e, rpad)
-    qxt, sxt = _mx_quant_tokens_t(x, counts, e, rpad)
     dw1 = torch.empty_like(w1)
     dw3 = torch.empty_like(w3)
     call("moe_mxfp8_gemm_bwd_dw13", ptr(qdgut), ptr(sdgut), ptr(qxt), ptr(sxt), ptr(counts), r, rpad, e, d, h_dim,
          ptr(dw1), ptr(dw3), s)
-    qdyt, sdyt = _mx_quant_tokens_t(dy, counts, e, rpad)
-    qht, sht = _mx_quant_tokens_t(h, counts, e, rpad)
     dw2 = torch.empty_like(w2)
     call("moe_mxfp8_gemm_bwd_dw2", ptr(qdyt), ptr(sdyt), ptr(qht), ptr(sht), ptr(counts), r, rpad, e, d, h_dim,
          ptr(dw2), s)
@@ -784,19 +837,27 @@ def grouped_swiglu_mxfp8_backward(
 
 
 @grouped_swiglu_mxfp8_backward.register_fake
-def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h):
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h, *quantized):
     return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
 
 
-def _gsmx_bwd(ctx, dy, _dg, _du, _dh):
-    x, w1, w2, w3, counts, g, u, h = ctx.saved_tensors
+def _gsmx_setup(ctx, inputs, output):
+    x, w1, w2, w3, counts, _for_backward = inputs
+    _y, g, u, h, *quantized = output
+    ctx.save_for_backward(x, w1, w2, w3, counts, g, u, h, *quantized)
+    ctx.mark_non_differentiable(g, u, h, *quantized)
+    ctx.set_materialize_grads(False)
+
+
+def _gsmx_bwd(ctx, dy, *_unused):
+    x, w1, w2, w3, counts, g, u, h, *quantized = ctx.saved_tensors
     if dy is None:
-        return None, None, None, None, None
-    dx, dw1, dw2, dw3 = grouped_swiglu_mxfp8_backward(dy, x, w1, w2, w3, counts, g, u, h)
-    return dx, dw1, dw2, dw3, None
+        return None, None, None, None, None, None
+    dx, dw1, dw2, dw3 = grouped_swiglu_mxfp8_backward(dy, x, w1, w2, w3, counts, g, u, h, *quantized)
+    return dx, dw1, dw2, dw3, None, None
 
 
-grouped_swiglu_mxfp8.register_autograd(_gsmx_bwd, setup_context=_gs_setup)
+grouped_swiglu_mxfp8.register_autograd(_gsmx_bwd, setup_context=_gsmx_setup)
 
 
 # ---------------------------------------------------------------------------
