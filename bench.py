@@ -110,8 +110,41 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
         "moe_reorder_bwd": 4 * r + 4 * n * k + 4 * n * k,
         "moe_router_bwd": 4 * n * k + 8 * n * k + 4 * n * e + 4 * n * e,
     }
-    # fp8 quantizers run on tensors of several sizes per step: time only
+    # the quantizers run on tensors of several sizes per step: bytes per launch come
+    # from the launch's own arguments (launch_bytes)
     return "hbm", (float(nbytes[name]) if name in nbytes else None)
+
+
+def launch_bytes(name: str, a: tuple) -> float | None:
+    """Algorithmic bytes of one quantizer launch from its C-ABI arguments: the bf16
+    input read once, the fp8 codes and scales written once (fp32 scales per row, per
+    column or per (expert, column); e8m0 scales per 32 elements for MXFP8)."""
+    mx = 1.0 + 1.0 / 32.0
+    if name == "moe_fp8_quant_rows":
+        rows, cols = a[1], a[2]
+        return 3.0 * rows * cols + 4.0 * rows
+    if name == "moe_fp8_quant_cols_t":
+        e, ra, cb = a[1], a[2], a[3]
+        return 3.0 * e * ra * cb + 4.0 * e * cb
+    if name == "moe_fp8_quant_tokens_t":
+        rows, e, cols, padded = a[2], a[3], a[4], a[5]
+        return 2.0 * rows * cols + 1.0 * padded * cols + 4.0 * e * cols + 8.0 * e
+    if name == "moe_mxfp8_quant_rows":
+        rows, cols = a[1], a[2]
+        return 2.0 * rows * cols + mx * rows * cols
+    if name == "moe_mxfp8_quant_cols_t":
+        e, ra, cb = a[1], a[2], a[3]
+        return 2.0 * e * ra * cb + mx * e * ra * cb
+    if name == "moe_mxfp8_quant_dual_cols":
+        e, ra, cb = a[1], a[2], a[3]
+        return 2.0 * e * ra * cb + 2.0 * mx * e * ra * cb
+    if name == "moe_mxfp8_quant_tokens_t":
+        rows, e, cols, padded = a[2], a[3], a[4], a[5]
+        return 2.0 * rows * cols + mx * padded * cols + 8.0 * e
+    if name == "moe_mxfp8_quant_dual_tokens":
+        rows, e, cols, padded = a[2], a[3], a[4], a[5]
+        return 2.0 * rows * cols + mx * rows * cols + mx * padded * cols + 8.0 * e
+    return None
 
 
 def make_layer(w: dict, device: torch.device, seed: int):
@@ -298,11 +331,16 @@ def main() -> int:
     ms = (t1 - t0) * 1e3 / args.steps
 
     durations = timer.durations_ms()
+    launch_args = timer.launch_args()
     kernels = {}
     for name, ds in sorted(durations.items()):
         per_step = len(ds) / args.steps
         avg = sum(ds) / len(ds)
         bound, work = kernel_work(name, w)
+        if work is None:
+            lb = [launch_bytes(name, a) for a in launch_args[name]]
+            if all(v is not None for v in lb):
+                work = sum(lb) / len(lb)  # bytes of the average launch, over the average launch time
         if bound == "mfma":
             peak = PEAK_FP8_TFLOPS if name.startswith(("moe_fp8_", "moe_mxfp8_")) else PEAK_BF16_TFLOPS
             achieved, unit = work / (avg * 1e-3) / 1e12, "TFLOP/s"

@@ -130,7 +130,11 @@ class KernelTimer:
         self.events: dict[str, list] = {}
 
     def durations_ms(self) -> dict[str, list[float]]:
-        return {k: [a.elapsed_time(b) for a, b in v] for k, v in self.events.items()}
+        return {k: [a.elapsed_time(b) for a, b, _ in v] for k, v in self.events.items()}
+
+    def launch_args(self) -> dict[str, list[tuple]]:
+        """The C-ABI arguments of every timed launch (ints and pointers), in order."""
+        return {k: [args for _, _, args in v] for k, v in self.events.items()}
 
 
 _timer: KernelTimer | None = None
@@ -155,7 +159,7 @@ def call(name: str, *args) -> None:
     st = fn(*args)
     b.record()
     check(st, name)
-    t.events.setdefault(name, []).append((a, b))
+    t.events.setdefault(name, []).append((a, b, args))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

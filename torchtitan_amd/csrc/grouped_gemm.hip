@@ -422,16 +422,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     const int tmv = T::kRowGrouped ? min(TM, max(0, (seg1 - (row0 + wm * WM) + 15) >> 4)) : TM;
     const int kt_half = (MODE == kBwdDx) ? H / BK : -1;
 
+    // dx = bf16(dg . w1) + bf16(du . w3), the sum of the two bf16 gradients autograd
+    // accumulates into x: after the w1 half of the k range the accumulators are
+    // rounded to bf16 and parked, then restarted for w3. Wave tiles up to 64 x 96
+    // park in registers (2 TM TN VGPRs); wider ones, which have no registers to
+    // spare, park in the dx rows themselves and read them back in the epilogue.
+    constexpr bool kParkRegs = TM * TN <= 24;
+    uint32_t park[kParkRegs ? TM : 1][kParkRegs ? TN : 1][2];
     auto park_dx_half = [&]() {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const int n = nt * BN + wn * WN + j * 16 + nq;
-          if (r < seg1 && (!TAIL || n < D)) {
-            *(uint2*)(p.out_dx + (int64_t)r * D + n) =
-                make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3]));
+          const uint32_t lo = pack_bf2(acc[i][j][0], acc[i][j][1]), hi = pack_bf2(acc[i][j][2], acc[i][j][3]);
+          if constexpr (kParkRegs) {
+            park[i][j][0] = lo;
+            park[i][j][1] = hi;
+          } else {
+            const int n = nt * BN + wn * WN + j * 16 + nq;
+            if (r < seg1 && (!TAIL || n < D)) *(uint2*)(p.out_dx + (int64_t)r * D + n) = make_uint2(lo, hi);
           }
           acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
@@ -532,7 +542,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
               v[3] = round_bf(v[3]) + bf_hi(bw.y);
             }
             if (MODE == kBwdDx && ACT == kSwiGLU) {
-              const uint2 pw = *(const uint2*)dst;
+              uint2 pw;
+              if constexpr (kParkRegs) pw = make_uint2(park[i][j][0], park[i][j][1]);
+              else pw = *(const uint2*)dst;
               v[0] = bf_lo(pw.x) + round_bf(v[0]);
               v[1] = bf_hi(pw.x) + round_bf(v[1]);
               v[2] = bf_lo(pw.y) + round_bf(v[2]);
