@@ -76,6 +76,28 @@ __device__ __forceinline__ uint32_t e4m3(float x) {
   return sign | q;
 }
 
+// The same conversion for four floats on the hardware (gfx950 v_cvt_pk_fp8_f32:
+// OCP e4m3fn, round to nearest even) after fmed3 saturates them at +-448,
+// packed little-endian. Checked against e4m3() on the GPU for every fp32 bit
+// pattern: identical except NaN (which fmed3 turns into 448), so callers use it
+// only for NaN-free data and keep e4m3() for the rest.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, -kFp8Max, kFp8Max),
+                                                 __builtin_amdgcn_fmed3f(b, -kFp8Max, kFp8Max), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(c, -kFp8Max, kFp8Max),
+                                                   __builtin_amdgcn_fmed3f(d, -kFp8Max, kFp8Max), lo, true);
+}
+
+// Nonzero when one of the eight bf16 values of v is a NaN: per 16-bit half,
+// |h| + 0x7f carries into bit 15 exactly when |h| > 0x7f80.
+__device__ __forceinline__ uint32_t has_nan8(uint4 v) {
+  auto w = [](uint32_t x) { return (x & 0x7fff7fffu) + 0x007f007fu; };
+  return (w(v.x) | w(v.y) | w(v.z) | w(v.w)) & 0x80008000u;
+}
+
+// true in every lane when no lane of the wave has a NaN (wave-uniform branch)
+__device__ __forceinline__ bool wave_nan_free(uint32_t nan_flag) { return __ballot(nan_flag != 0u) == 0ull; }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -116,7 +138,11 @@ __device__ __forceinline__ float amax8(uint4 v) {
                fmaxf(fmaxf(fabsf(bf_lo(v.z)), fabsf(bf_hi(v.z))), fmaxf(fabsf(bf_lo(v.w)), fabsf(bf_hi(v.w)))));
 }
 
-__device__ __forceinline__ uint2 quant8(uint4 v, float s) {
+// fast: the wave's data holds no NaN (hardware conversion)
+__device__ __forceinline__ uint2 quant8(uint4 v, float s, bool fast) {
+  if (fast)
+    return make_uint2(e4m3x4(bf_lo(v.x) / s, bf_hi(v.x) / s, bf_lo(v.y) / s, bf_hi(v.y) / s),
+                      e4m3x4(bf_lo(v.z) / s, bf_hi(v.z) / s, bf_lo(v.w) / s, bf_hi(v.w) / s));
   const uint32_t lo = e4m3(bf_lo(v.x) / s) | (e4m3(bf_hi(v.x) / s) << 8) | (e4m3(bf_lo(v.y) / s) << 16) |
                       (e4m3(bf_hi(v.y) / s) << 24);
   const uint32_t hi = e4m3(bf_lo(v.z) / s) | (e4m3(bf_hi(v.z) / s) << 8) | (e4m3(bf_lo(v.w) / s) << 16) |
@@ -124,7 +150,10 @@ __device__ __forceinline__ uint2 quant8(uint4 v, float s) {
   return make_uint2(lo, hi);
 }
 
-__device__ __forceinline__ uint2 mx_quant8(uint4 v, float f) {
+__device__ __forceinline__ uint2 mx_quant8(uint4 v, float f, bool fast) {
+  if (fast)
+    return make_uint2(e4m3x4(bf_lo(v.x) * f, bf_hi(v.x) * f, bf_lo(v.y) * f, bf_hi(v.y) * f),
+                      e4m3x4(bf_lo(v.z) * f, bf_hi(v.z) * f, bf_lo(v.w) * f, bf_hi(v.w) * f));
   const uint32_t lo = e4m3(bf_lo(v.x) * f) | (e4m3(bf_hi(v.x) * f) << 8) | (e4m3(bf_lo(v.y) * f) << 16) |
                       (e4m3(bf_hi(v.y) * f) << 24);
   const uint32_t hi = e4m3(bf_lo(v.z) * f) | (e4m3(bf_hi(v.z) * f) << 8) | (e4m3(bf_lo(v.w) * f) << 16) |
@@ -144,6 +173,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
     const uint16_t* xr = x + r * K;
     uint8_t* qr = q + r * K;
     float amax = 0.f;
+    uint32_t nan = 0;
     if constexpr (CPL > 0) {
       uint4 v[CPL];
 #pragma unroll
@@ -151,19 +181,26 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
         const int c = lane + 64 * i;
         v[i] = c < cpr ? *(const uint4*)(xr + c * 8) : make_uint4(0, 0, 0, 0);
         amax = fmaxf(amax, amax8(v[i]));
+        nan |= has_nan8(v[i]);
       }
       const float s = scale_of(wave_max(amax));
+      const bool fast = wave_nan_free(nan);
       if (lane == 0) scale[r] = s;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = lane + 64 * i;
-        if (c < cpr) *(uint2*)(qr + c * 8) = quant8(v[i], s);
+        if (c < cpr) *(uint2*)(qr + c * 8) = quant8(v[i], s, fast);
       }
     } else {
-      for (int c = lane; c < cpr; c += 64) amax = fmaxf(amax, amax8(*(const uint4*)(xr + c * 8)));
+      for (int c = lane; c < cpr; c += 64) {
+        const uint4 v = *(const uint4*)(xr + c * 8);
+        amax = fmaxf(amax, amax8(v));
+        nan |= has_nan8(v);
+      }
       const float s = scale_of(wave_max(amax));
+      const bool fast = wave_nan_free(nan);
       if (lane == 0) scale[r] = s;
-      for (int c = lane; c < cpr; c += 64) *(uint2*)(qr + c * 8) = quant8(*(const uint4*)(xr + c * 8), s);
+      for (int c = lane; c < cpr; c += 64) *(uint2*)(qr + c * 8) = quant8(*(const uint4*)(xr + c * 8), s, fast);
     }
   }
 }
@@ -236,7 +273,9 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
   };
   if (n_out > 0) load(0);
   for (int a0 = 0; a0 < n_out; a0 += kTRows) {
+    const uint32_t nan = has_nan8(v[0]) | has_nan8(v[1]) | has_nan8(v[2]) | has_nan8(v[3]);
     if constexpr (ROWS) {
+      const bool rows_fast = wave_nan_free(nan);
       // lanes t, t ^ 1, t ^ 2, t ^ 3 hold the four 8-column chunks of one 32-column block
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -247,7 +286,7 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
         a = fmaxf(a, __shfl_xor(a, 2));
         const uint32_t e = mx_exponent(a);
         if (a0 + r < n_rows) {
-          *(uint2*)(qr + (int64_t)(a0 + r) * ldr + ch * 8) = mx_quant8(v[i], mx_multiplier(e));
+          *(uint2*)(qr + (int64_t)(a0 + r) * ldr + ch * 8) = mx_quant8(v[i], mx_multiplier(e), rows_fast);
           if ((ch & 3) == 0) sr[(int64_t)(a0 + r) * ldsr + (ch >> 2)] = (uint8_t)e;
         }
       }
@@ -258,30 +297,50 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       const int c = t + i * 256;
       *(uint4*)(s_tile + (c >> 3) * 32 + (c & 7) * 4) = v[i];
     }
-    __syncthreads();
+    const bool fast = !__syncthreads_or(nan != 0u);  // block-uniform: the tile holds no NaN
     if (a0 + kTRows < n_out) load(a0 + kTRows);
     const int rb = a0 + j * 32;
     if (rb < n_out) {
       const uint16_t* xs = (const uint16_t*)s_tile + j * 32 * 64 + col;  // row k of the block at xs[64 k]
       float f;
       uint32_t e = 0;
-      if constexpr (MX) {
+      uint32_t o[8];
+      if (fast) {
+        float xv[32];
         float am = 0.f;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) am = fmaxf(am, fabsf(bf2f(xs[64 * k])));
-        e = mx_exponent(am);
-        f = mx_multiplier(e);
+        for (int k = 0; k < 32; ++k) {
+          xv[k] = bf2f(xs[64 * k]);
+          am = fmaxf(am, fabsf(xv[k]));
+        }
+        if constexpr (MX) {
+          e = mx_exponent(am);
+          f = mx_multiplier(e);
+        } else {
+          f = s_col[col];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          o[q] = MX ? e4m3x4(xv[4 * q] * f, xv[4 * q + 1] * f, xv[4 * q + 2] * f, xv[4 * q + 3] * f)
+                    : e4m3x4(xv[4 * q] / f, xv[4 * q + 1] / f, xv[4 * q + 2] / f, xv[4 * q + 3] / f);
       } else {
-        f = s_col[col];
-      }
-      uint32_t o[8];
+        if constexpr (MX) {
+          float am = 0.f;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        o[q] = 0;
+          for (int k = 0; k < 32; ++k) am = fmaxf(am, fabsf(bf2f(xs[64 * k])));
+          e = mx_exponent(am);
+          f = mx_multiplier(e);
+        } else {
+          f = s_col[col];
+        }
 #pragma unroll
-        for (int bq = 0; bq < 4; ++bq) {
-          const float xv = bf2f(xs[64 * (4 * q + bq)]);
-          o[q] |= (MX ? e4m3(xv * f) : e4m3(xv / f)) << (8 * bq);
+        for (int q = 0; q < 8; ++q) {
+          o[q] = 0;
+#pragma unroll
+          for (int bq = 0; bq < 4; ++bq) {
+            const float xv = bf2f(xs[64 * (4 * q + bq)]);
+            o[q] |= (MX ? e4m3(xv * f) : e4m3(xv / f)) << (8 * bq);
+          }
         }
       }
       uint8_t* d = out + (int64_t)col * ldo + rb;
@@ -388,8 +447,9 @@ __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint4* __restr
       a = fmaxf(a, __shfl_xor(a, 1));
       a = fmaxf(a, __shfl_xor(a, 2));
       const uint32_t e = mx_exponent(a);
+      const bool fast = wave_nan_free(has_nan8(v[u]));
       if (c < n_chunks) {
-        q[c] = mx_quant8(v[u], mx_multiplier(e));
+        q[c] = mx_quant8(v[u], mx_multiplier(e), fast);
         if ((c & 3) == 0) scale[c >> 2] = (uint8_t)e;
       }
     }
