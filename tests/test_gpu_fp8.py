@@ -237,3 +237,38 @@ def test_fp8_grouped_swiglu_fwd_bwd(dev, name):
              "dw2": _rel(b.grad, w2r.grad), "dw3": _rel(c.grad, w3r.grad)}
     print(f"[case] {name} vs fp32 reference: {loose}", flush=True)
     assert all(v <= BF16_TOL for v in loose.values()), loose
+
+
+def test_fp8_quantizers_nan_elements(dev):
+    """A NaN element quantizes to 0x7f and sends only its own wave (row-wise) or
+    LDS tile (transposed) to the software conversion: every row and column
+    without a NaN still matches the oracle bit for bit. (The NaN row's or
+    column's scale is not compared: the kernels' amax skips NaN, torch's
+    propagates it.)"""
+    banner("fp8 quantizers with NaN elements")
+    from torchtitan_amd import ops
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(256, 512, generator=g).bfloat16()
+    x[13, 5] = float("nan")
+    q, _ = ops._quant_rows(x.to(dev), 512)
+    q = q.cpu()
+    rq, _ = R.quant_fp8_rows(x)
+    keep = torch.ones(256, dtype=torch.bool)
+    keep[13] = False
+    assert q[13, 5].item() == 0x7F
+    assert torch.equal(q[keep], rq.view(torch.uint8)[keep])
+    # token groups, transposed: the NaN's tile takes the software path
+    counts = torch.tensor([100, 0, 156], dtype=torch.int64)
+    xt = torch.randn(256, 128, generator=g).bfloat16()
+    xt[40, 70] = float("nan")
+    rpad = ops._padded_rows(256, 3)
+    q2, _ = ops._quant_tokens_t(xt.to(dev), counts.to(dev), 3, rpad)
+    q2 = q2.cpu()
+    assert q2[70, 40].item() == 0x7F
+    cols = torch.ones(128, dtype=torch.bool)
+    cols[70] = False
+    rq0, _ = R.quant_fp8_rows(xt[0:100].t())
+    rq2, _ = R.quant_fp8_rows(xt[100:256].t())
+    assert torch.equal(q2[cols, 0:100], rq0.view(torch.uint8)[cols])
+    assert torch.equal(q2[:, 112:268], rq2.view(torch.uint8))

@@ -279,3 +279,51 @@ def test_mxfp8_grouped_swiglu_fwd_bwd(dev, name, for_backward):
              "dw2": _rel(b.grad, w2r.grad), "dw3": _rel(c.grad, w3r.grad)}
     print(f"[case] {name} vs fp32 reference: {loose}", flush=True)
     assert all(v <= BF16_TOL for v in loose.values()), loose
+
+
+def test_mxfp8_quantizers_nan_elements(dev):
+    """A NaN element quantizes to 0x7f and sends only its own wave (row-wise) or
+    LDS tile (transposed) to the software conversion: every 32-block without a
+    NaN still matches the oracle bit for bit (the NaN's own block is not
+    compared: its scale skips the NaN here, torch's amax propagates it)."""
+    banner("mxfp8 quantizers with NaN elements")
+    from torchtitan_amd import ops
+
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(256, 128, generator=g).bfloat16()
+    x[13, 5] = float("nan")
+    x[200, 70] = float("nan")
+    q, s = ops._mx_quant_rows(x.to(dev), 128)
+    q, s = q.cpu(), s.cpu()
+    rq, rs = R.quant_mxfp8(x)
+    rq = rq.view(torch.uint8)
+    assert q[13, 5].item() == 0x7F and q[200, 70].item() == 0x7F
+    blk = torch.ones(256, 4, dtype=torch.bool)
+    blk[13, 0] = False
+    blk[200, 2] = False
+    assert torch.equal(s[blk], rs[blk])
+    el = blk.repeat_interleave(32, dim=1)
+    assert torch.equal(q[el], rq[el])
+    # token groups, transposed (and the dual kernel's row-wise layout from the same read)
+    counts = torch.tensor([100, 0, 156], dtype=torch.int64)
+    rpad = ops._mx_padded_rows(256, 3)
+    segs = [(0, 100), (100, 0), (100, 156)]
+    rq2, rs2, _ = _tokens_t(x, segs, rpad)
+    for qt, st_ in (ops._mx_quant_tokens_t(x.to(dev), counts.to(dev), 3, rpad),
+                    ops._mx_dual_tokens(x.to(dev), counts.to(dev), 3, rpad)[2:]):
+        qt, st_ = qt.cpu(), st_.cpu()
+        assert qt[5, 13].item() == 0x7F and qt[70, 128 + 100].item() == 0x7F
+        ok = torch.ones(128, rpad // 32, dtype=torch.bool)  # (column, k-block) pairs without a NaN
+        ok[5, 0] = False
+        ok[70, (128 + 100) // 32] = False
+        used = (128 + 160) // 32
+        ok[:, used:] = False
+        assert torch.equal(st_.t()[ok], rs2.t()[ok])
+        el = ok.repeat_interleave(32, dim=1)
+        assert torch.equal(qt[el], rq2[el])
+    qr, sr, _, _ = ops._mx_dual_tokens(x.to(dev), counts.to(dev), 3, rpad)
+    qr, sr = qr.cpu(), sr.cpu()
+    assert qr[13, 5].item() == 0x7F and qr[200, 70].item() == 0x7F
+    assert torch.equal(sr[blk], rs[blk])
+    el = blk.repeat_interleave(32, dim=1)
+    assert torch.equal(qr[el], rq[el])
