@@ -52,58 +52,73 @@ __global__ __launch_bounds__(256) void hist_kernel(const int64_t* __restrict__ i
   }
 }
 
-// Single block of 256 threads; thread t owns experts 4t..4t+3.
-// block_hist[b][e] -> block_base[b][e] = start[e] + sum_{b'<b} hist[b'][e]
-// The per-block counts are read in batches of kScanBatch independent loads so
-// their latencies overlap instead of adding up block after block.
+// Single block of 1024 threads. block_hist[b][e] -> counts[e], offsets[e]
+// (inclusive ends) and block_base[b][e] = start[e] + sum_{b' < b} hist[b'][e].
+// Thread t handles expert t % Ep for the G = 1024 / Ep groups of consecutive
+// blocks (Ep = 256, 512 or 1024 >= E), so each thread reads one short run of
+// blocks, in batches of kScanBatch independent loads.
 constexpr int kScanBatch = 16;
+constexpr int kScanThreads = 1024;
 
-__global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ block_hist, int n_blocks,
-                                                   int E, int32_t* __restrict__ block_base,
-                                                   int64_t* __restrict__ counts,
-                                                   int32_t* __restrict__ offsets) {
-  __shared__ int tmp[8];
-  int tot[4], start[4];
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(const int32_t* __restrict__ block_hist, int n_blocks,
+                                                            int E, int32_t* __restrict__ block_base,
+                                                            int64_t* __restrict__ counts,
+                                                            int32_t* __restrict__ offsets) {
+  __shared__ int s_part[kScanThreads];
+  __shared__ int s_tot[kMaxExperts];
+  __shared__ int s_start[kMaxExperts];
+  __shared__ int tmp[kScanThreads / 64];
+  const int G = E <= 256 ? 4 : (E <= 512 ? 2 : 1);
+  const int Ep = kScanThreads / G;
+  const int t = threadIdx.x, e = t % Ep, g = t / Ep;
+  const int chunk = (n_blocks + G - 1) / G;
+  const int b_lo = g * chunk, b_hi = min(n_blocks, b_lo + chunk);
+  auto sweep = [&](int run, bool write) {
+    for (int b0 = b_lo; b0 < b_hi; b0 += kScanBatch) {
+      int v[kScanBatch];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = threadIdx.x * 4 + i;
-    int run = 0;
-    if (e < E) {
-      for (int b0 = 0; b0 < n_blocks; b0 += kScanBatch) {
-        int v[kScanBatch];
+      for (int j = 0; j < kScanBatch; ++j) v[j] = (b0 + j < b_hi) ? block_hist[(int64_t)(b0 + j) * E + e] : 0;
 #pragma unroll
-        for (int j = 0; j < kScanBatch; ++j)
-          v[j] = (b0 + j < n_blocks) ? block_hist[(int64_t)(b0 + j) * E + e] : 0;
-#pragma unroll
-        for (int j = 0; j < kScanBatch; ++j) {
-          if (block_base && b0 + j < n_blocks) block_base[(int64_t)(b0 + j) * E + e] = run;
-          run += v[j];
-        }
+      for (int j = 0; j < kScanBatch; ++j) {
+        if (write && b0 + j < b_hi) block_base[(int64_t)(b0 + j) * E + e] = run;
+        run += v[j];
       }
     }
-    tot[i] = run;
+    return run;
+  };
+  s_part[t] = (e < E) ? sweep(0, false) : 0;
+  __syncthreads();
+  int pre = 0, tot = 0;
+  if (e < E) {
+    for (int gg = 0; gg < G; ++gg) {
+      const int v = s_part[gg * Ep + e];
+      if (gg < g) pre += v;
+      tot += v;
+    }
+    if (g == 0) s_tot[e] = tot;
   }
-  block_exclusive_scan4(tot, start, tmp);
+  __syncthreads();
+  // exclusive scan over the experts: thread t < 256 owns experts 4t .. 4t + 3
+  int v4[4], o4[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int e = threadIdx.x * 4 + i;
-    if (e < E) {
-      if (counts) counts[e] = tot[i];
-      if (offsets) offsets[e] = start[i] + tot[i];
-    }
+    const int ee = 4 * t + i;
+    v4[i] = (t < kMaxExperts / 4 && ee < E) ? s_tot[ee] : 0;
   }
-  if (block_base) {
-    // add the expert starts to every block's base (coalesced over experts)
-    __shared__ int s_start[kMaxExperts];
+  block_exclusive_scan4(v4, o4, tmp);
+  if (t < kMaxExperts / 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = threadIdx.x * 4 + i;
-      if (e < E) s_start[e] = start[i];
+      const int ee = 4 * t + i;
+      if (ee < E) {
+        s_start[ee] = o4[i];
+        if (counts) counts[ee] = v4[i];
+        if (offsets) offsets[ee] = o4[i] + v4[i];
+      }
     }
-    __syncthreads();
-    const int64_t total = (int64_t)n_blocks * E;
-    for (int64_t i = threadIdx.x; i < total; i += blockDim.x) block_base[i] += s_start[i % E];
   }
+  __syncthreads();
+  if (block_base && e < E) sweep(s_start[e] + pre, true);
 }
 
 struct ScatterParams {
@@ -418,7 +433,7 @@ MOE_API int moe_histogram(const int64_t* selected_experts, int64_t n_tokens, int
   if (nb > 0)
     hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
                        top_k, n_experts, block_hist);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, stream, block_hist, nb, n_experts,
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_hist, nb, n_experts,
                      (int32_t*)nullptr, counts, offsets);
   return launch_status();
 }
@@ -437,7 +452,7 @@ MOE_API int moe_reorder(const int64_t* selected_experts, const float* top_scores
   if (nb > 0)
     hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
                        top_k, n_experts, block_hist);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), 0, stream, block_hist, nb, n_experts,
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_hist, nb, n_experts,
                      block_base, counts, offsets);
   if (nb > 0) {
     ScatterParams p{selected_experts, top_scores, block_base, n_tokens, top_k, n_experts,
