@@ -176,6 +176,23 @@ __device__ __forceinline__ bf16x8_t frag_km(const uint16_t* tile, int row0, int 
 
 __device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a segment
 
+// Epilogue stores in 64-byte row pieces. An accumulator tile leaves lane (r, g),
+// r = lane % 16, g = lane / 16, with 4 consecutive columns 4g .. 4g + 3 of row r
+// in each 16-column block; for two adjacent blocks (lo, hi) packed to bf16, this
+// returns the 8 columns 8g .. 8g + 7 of the 32-column span [lo | hi] of row r,
+// gathered from the lanes of the same row, so that the four lanes of a row store
+// 64 contiguous bytes with one 16-byte store each (instead of 32 bytes per block).
+__device__ __forceinline__ uint4 span64(uint2 lo, uint2 hi, int lane) {
+  const int g = lane >> 4;
+  const int s1 = (lane & 15) + 16 * ((2 * g) & 3), s2 = s1 + 16;
+  const uint32_t l0 = __shfl(lo.x, s1), l1 = __shfl(lo.y, s1), l2 = __shfl(lo.x, s2), l3 = __shfl(lo.y, s2);
+  const uint32_t h0 = __shfl(hi.x, s1), h1 = __shfl(hi.y, s1), h2 = __shfl(hi.x, s2), h3 = __shfl(hi.y, s2);
+  return g < 2 ? make_uint4(l0, l1, l2, l3) : make_uint4(h0, h1, h2, h3);
+}
+__device__ __forceinline__ uint2 pack4(const float (&v)[4]) {
+  return make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+}
+
 // TAIL: the n extent (and, for dW, the m extent) is not a multiple of the tile;
 // compiled only for such shapes so that whole-tile shapes keep the tighter code.
 template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT, bool TAIL>
@@ -189,6 +206,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
   constexpr int CPW = CPW_P + CPW_Q;
   constexpr int CHP = BM / 8, CHQ = BN / 8;          // 16-byte chunks per k-row (k-major tiles)
   static_assert(BM % 64 == 0 && BN % 64 == 0 && CPW <= 30, "tile");
+  static_assert(TN % 2 == 0 && (MODE != kFwdGateUp || TN % 4 == 0), "epilogue block pairs");
   __shared__ __attribute__((aligned(1024))) uint16_t sP[NS][BM * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sQ[NS][BN * BK];
   __shared__ int s_seg[kGemmMaxE + 1];
@@ -487,38 +505,53 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     else run(std::false_type{});
 
     // ---- epilogue: lane holds C[m = .. + ml][n = .. + nq + 0..3] ----
+    // Each lane produces 4 columns per 16-column block; pairs of blocks are stored
+    // as 64-byte row pieces (span64), at column 32 jp + 8 (lane / 16) of the wave's span.
+    const int g8 = 8 * (lane >> 4);
     if (MODE == kFwdGateUp) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
 #pragma unroll
-          for (int jj = 0; jj < TN / 2; ++jj) {
-            const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nq;
-            if (TAIL && hc >= H) continue;
-            float gv[4], uv[4], hv[4];
-            if constexpr (ACT == kOssGLU) {
-              // h1 = bf16(x . mlp1^T) + bias (bf16 add), then the clamped SwiGLU
-              const uint4 bw = *(const uint4*)(p.b1 + e64 * 2 * H + 2 * hc);  // (glu, linear) x 4 columns
-              const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
+          for (int jp = 0; jp < TN / 4; ++jp) {
+            uint2 pg[2], pu[2], ph[2];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                gv[q] = round_bf(round_bf(acc[i][2 * jj][q]) + bf_lo(bb[q]));
-                uv[q] = round_bf(round_bf(acc[i][2 * jj + 1][q]) + bf_hi(bb[q]));
-                hv[q] = oss_glu(gv[q], uv[q], p.limit, p.alpha);
-              }
-            } else {
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int jj = 2 * jp + h2;
+              const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nq;
+              float gv[4], uv[4], hv[4];
+              if constexpr (ACT == kOssGLU) {
+                // h1 = bf16(x . mlp1^T) + bias (bf16 add), then the clamped SwiGLU
+                uint4 bw = make_uint4(0, 0, 0, 0);  // (glu, linear) x 4 columns
+                if (!TAIL || hc < H) bw = *(const uint4*)(p.b1 + e64 * 2 * H + 2 * hc);
+                const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                gv[q] = round_bf(acc[i][2 * jj][q]);
-                uv[q] = round_bf(acc[i][2 * jj + 1][q]);
-                hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+                for (int q = 0; q < 4; ++q) {
+                  gv[q] = round_bf(round_bf(acc[i][2 * jj][q]) + bf_lo(bb[q]));
+                  uv[q] = round_bf(round_bf(acc[i][2 * jj + 1][q]) + bf_hi(bb[q]));
+                  hv[q] = oss_glu(gv[q], uv[q], p.limit, p.alpha);
+                }
+              } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  gv[q] = round_bf(acc[i][2 * jj][q]);
+                  uv[q] = round_bf(acc[i][2 * jj + 1][q]);
+                  hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+                }
               }
+              pg[h2] = pack4(gv);
+              pu[h2] = pack4(uv);
+              ph[h2] = pack4(hv);
             }
+            const int hc = nt * (BN / 2) + wn * (WN / 2) + jp * 32 + g8;
+            const uint4 sg = span64(pg[0], pg[1], lane), su = span64(pu[0], pu[1], lane),
+                        sh = span64(ph[0], ph[1], lane);
+            if (TAIL && hc >= H) continue;
             const int64_t off = (int64_t)r * H + hc;
-            *(uint2*)(p.out_g + off) = make_uint2(pack_bf2(gv[0], gv[1]), pack_bf2(gv[2], gv[3]));
-            *(uint2*)(p.out_u + off) = make_uint2(pack_bf2(uv[0], uv[1]), pack_bf2(uv[2], uv[3]));
-            *(uint2*)(p.out_h + off) = make_uint2(pack_bf2(hv[0], hv[1]), pack_bf2(hv[2], hv[3]));
+            *(uint4*)(p.out_g + off) = sg;
+            *(uint4*)(p.out_u + off) = su;
+            *(uint4*)(p.out_h + off) = sh;
           }
         }
       }
@@ -529,28 +562,36 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int n = nt * BN + wn * WN + j * 16 + nq;
+          for (int jp = 0; jp < TN / 2; ++jp) {
+            uint2 pv[2];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int j = 2 * jp + h2;
+              const int n = nt * BN + wn * WN + j * 16 + nq;
+              const bool in = !TAIL || n < D;
+              float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+              if (MODE == kFwdDown && ACT == kOssGLU) {  // bf16(h . mlp2^T) + mlp2_bias (bf16 add)
+                const uint2 bw = in ? *(const uint2*)(p.b2 + e64 * D + n) : make_uint2(0, 0);
+                v[0] = round_bf(v[0]) + bf_lo(bw.x);
+                v[1] = round_bf(v[1]) + bf_hi(bw.x);
+                v[2] = round_bf(v[2]) + bf_lo(bw.y);
+                v[3] = round_bf(v[3]) + bf_hi(bw.y);
+              }
+              if (MODE == kBwdDx && ACT == kSwiGLU) {
+                uint2 pw = make_uint2(0, 0);
+                if constexpr (kParkRegs) pw = make_uint2(park[i][j][0], park[i][j][1]);
+                else if (in) pw = *(const uint2*)(outp + (int64_t)r * D + n);
+                v[0] = bf_lo(pw.x) + round_bf(v[0]);
+                v[1] = bf_hi(pw.x) + round_bf(v[1]);
+                v[2] = bf_lo(pw.y) + round_bf(v[2]);
+                v[3] = bf_hi(pw.y) + round_bf(v[3]);
+              }
+              pv[h2] = pack4(v);
+            }
+            const int n = nt * BN + wn * WN + jp * 32 + g8;
+            const uint4 sv = span64(pv[0], pv[1], lane);
             if (TAIL && n >= D) continue;
-            uint16_t* dst = outp + (int64_t)r * D + n;
-            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            if (MODE == kFwdDown && ACT == kOssGLU) {  // bf16(h . mlp2^T) + mlp2_bias (bf16 add)
-              const uint2 bw = *(const uint2*)(p.b2 + e64 * D + n);
-              v[0] = round_bf(v[0]) + bf_lo(bw.x);
-              v[1] = round_bf(v[1]) + bf_hi(bw.x);
-              v[2] = round_bf(v[2]) + bf_lo(bw.y);
-              v[3] = round_bf(v[3]) + bf_hi(bw.y);
-            }
-            if (MODE == kBwdDx && ACT == kSwiGLU) {
-              uint2 pw;
-              if constexpr (kParkRegs) pw = make_uint2(park[i][j][0], park[i][j][1]);
-              else pw = *(const uint2*)dst;
-              v[0] = bf_lo(pw.x) + round_bf(v[0]);
-              v[1] = bf_hi(pw.x) + round_bf(v[1]);
-              v[2] = bf_lo(pw.y) + round_bf(v[2]);
-              v[3] = bf_hi(pw.y) + round_bf(v[3]);
-            }
-            *(uint2*)dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+            *(uint4*)(outp + (int64_t)r * D + n) = sv;
           }
         }
       }
@@ -560,12 +601,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
+          for (int jp = 0; jp < TN / 2; ++jp) {
+            uint2 pdg[2], pdu[2];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+            const int j = 2 * jp + h2;
             const int hh = nt * BN + wn * WN + j * 16 + nq;
-            if (TAIL && hh >= H) continue;
+            const bool in = !TAIL || hh < H;
             const int64_t off = (int64_t)r * H + hh;
-            const uint2 gw = *(const uint2*)(p.g + off);
-            const uint2 uw = *(const uint2*)(p.u + off);
+            const uint2 gw = in ? *(const uint2*)(p.g + off) : make_uint2(0, 0);
+            const uint2 uw = in ? *(const uint2*)(p.u + off) : make_uint2(0, 0);
             const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
             const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
             float dg[4], du[4];
@@ -598,9 +643,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
                 dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
               }
             }
+            pdg[h2] = pack4(dg);
+            pdu[h2] = pack4(du);
+            }
+            const int hh = nt * BN + wn * WN + jp * 32 + g8;
+            const uint4 sdg = span64(pdg[0], pdg[1], lane), sdu = span64(pdu[0], pdu[1], lane);
+            if (TAIL && hh >= H) continue;
             const int64_t o2 = (int64_t)r * (2 * H) + hh;
-            *(uint2*)(p.out_dgu + o2) = make_uint2(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]));
-            *(uint2*)(p.out_dgu + o2 + H) = make_uint2(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]));
+            *(uint4*)(p.out_dgu + o2) = sdg;
+            *(uint4*)(p.out_dgu + o2 + H) = sdu;
           }
         }
       }
@@ -616,11 +667,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         else
           rowp = p.out_dw2 + (e64 * D + m) * (int64_t)H;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int n = nt * BN + wn * WN + j * 16 + nq;
+        for (int jp = 0; jp < TN / 2; ++jp) {
+          const float lo[4] = {acc[i][2 * jp][0], acc[i][2 * jp][1], acc[i][2 * jp][2], acc[i][2 * jp][3]};
+          const float hi[4] = {acc[i][2 * jp + 1][0], acc[i][2 * jp + 1][1], acc[i][2 * jp + 1][2],
+                               acc[i][2 * jp + 1][3]};
+          const uint4 sv = span64(pack4(lo), pack4(hi), lane);
+          const int n = nt * BN + wn * WN + jp * 32 + g8;
           if (TAIL && n >= Ntot) continue;
-          *(uint2*)(rowp + n) =
-              make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]), pack_bf2(acc[i][j][2], acc[i][j][3]));
+          *(uint4*)(rowp + n) = sv;
         }
       }
     }
