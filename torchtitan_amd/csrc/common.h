@@ -47,6 +47,24 @@ __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w <<
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
+// Epilogue stores in 64-byte row pieces. An accumulator tile leaves lane (r, g),
+// r = lane % 16, g = lane / 16, with 4 consecutive columns 4g .. 4g + 3 of row r
+// in each 16-column block; for two adjacent blocks (lo, hi) packed to bf16, this
+// returns the 8 columns 8g .. 8g + 7 of the 32-column span [lo | hi] of row r,
+// gathered from the lanes of the same row, so that the four lanes of a row store
+// 64 contiguous bytes with one 16-byte store each (instead of 32 bytes per block).
+__device__ __forceinline__ uint4 span64(uint2 lo, uint2 hi, int lane) {
+  const int g = lane >> 4;
+  const int s1 = (lane & 15) + 16 * ((2 * g) & 3), s2 = s1 + 16;
+  const uint32_t l0 = __shfl(lo.x, s1), l1 = __shfl(lo.y, s1), l2 = __shfl(lo.x, s2), l3 = __shfl(lo.y, s2);
+  const uint32_t h0 = __shfl(hi.x, s1), h1 = __shfl(hi.y, s1), h2 = __shfl(hi.x, s2), h3 = __shfl(hi.y, s2);
+  return g < 2 ? make_uint4(l0, l1, l2, l3) : make_uint4(h0, h1, h2, h3);
+}
+__device__ __forceinline__ uint2 pack4(const float (&v)[4]) {
+  return make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+}
+
+
 // ---------------------------------------------------------------------------
 // Order-preserving map of fp32 onto uint32 used for top-k selection: larger
 // key == larger value, -0.0 sorts below +0.0 and every NaN is the largest key.

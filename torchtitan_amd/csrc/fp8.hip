@@ -588,6 +588,7 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
   constexpr int CPW_P = BM / 8 / 4, CPW_Q = BN / 8 / 4;  // 1 KB copies (8 rows x 128 B) per wave and stage
   constexpr int PAD = MX ? kMxPad : kPad;
   static_assert(!MX || (BM == 128 && BN == 128), "the MX scale copies assume 128 x 128 tiles");
+  static_assert(TN % 2 == 0 && (MODE != kGateUp || TN % 4 == 0), "epilogue block pairs");
   __shared__ __attribute__((aligned(1024))) uint8_t sP[2][BM * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ[2][BN * 128];
   // MX scales of a stage: row-grouped, P row m's 4 k-blocks at 4 m and Q row n's
@@ -856,7 +857,10 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
       compute(kt & 1);
     }
 
-    // ---- epilogues: lane holds C[m = .. + ml][n = .. + nql + 0..3] ----
+    // ---- epilogues: lane holds C[m = .. + ml][n = .. + nql + 0..3]; pairs of
+    // 16-column blocks are stored as 64-byte row pieces (span64) at column
+    // 32 jp + 8 (lane / 16) of the wave's span ----
+    const int g8 = 8 * g4;
     if (MODE == kGateUp) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -864,19 +868,29 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         if (r < seg1) {
           const float sx = MX ? 1.f : p.sp[r];
 #pragma unroll
-          for (int jj = 0; jj < TN / 2; ++jj) {
-            const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nql;
-            float gv[4], uv[4], hv[4];
+          for (int jp = 0; jp < TN / 4; ++jp) {
+            uint2 pg[2], pu[2], ph[2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              gv[q] = round_bf(MX ? acc[i][2 * jj][q] : (acc[i][2 * jj][q] * sx) * p.sq[e64 * H + hc + q]);
-              uv[q] = round_bf(MX ? acc[i][2 * jj + 1][q] : (acc[i][2 * jj + 1][q] * sx) * p.sq2[e64 * H + hc + q]);
-              hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int jj = 2 * jp + h2;
+              const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nql;
+              float gv[4], uv[4], hv[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                gv[q] = round_bf(MX ? acc[i][2 * jj][q] : (acc[i][2 * jj][q] * sx) * p.sq[e64 * H + hc + q]);
+                uv[q] = round_bf(MX ? acc[i][2 * jj + 1][q] : (acc[i][2 * jj + 1][q] * sx) * p.sq2[e64 * H + hc + q]);
+                hv[q] = round_bf(silu_f(gv[q])) * uv[q];
+              }
+              pg[h2] = pack4(gv);
+              pu[h2] = pack4(uv);
+              ph[h2] = pack4(hv);
             }
-            const int64_t off = (int64_t)r * H + hc;
-            *(uint2*)(p.o0 + off) = make_uint2(pack_bf2(gv[0], gv[1]), pack_bf2(gv[2], gv[3]));
-            *(uint2*)(p.o1 + off) = make_uint2(pack_bf2(uv[0], uv[1]), pack_bf2(uv[2], uv[3]));
-            *(uint2*)(p.o2 + off) = make_uint2(pack_bf2(hv[0], hv[1]), pack_bf2(hv[2], hv[3]));
+            const int64_t off = (int64_t)r * H + nt * (BN / 2) + wn * (WN / 2) + jp * 32 + g8;
+            const uint4 sg = span64(pg[0], pg[1], lane), su = span64(pu[0], pu[1], lane),
+                        sh = span64(ph[0], ph[1], lane);
+            *(uint4*)(p.o0 + off) = sg;
+            *(uint4*)(p.o1 + off) = su;
+            *(uint4*)(p.o2 + off) = sh;
           }
         }
       }
@@ -887,26 +901,32 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         if (r < seg1) {
           const float sp = MX ? 1.f : ((MODE == kDx) ? p.sp[(int64_t)r * 2 + 1] : p.sp[r]);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int n = nt * BN + wn * WN + j * 16 + nql;
-            uint16_t* dst = p.o0 + (int64_t)r * D + n;
-            float v[4];
-            if (MX) {
+          for (int jp = 0; jp < TN / 2; ++jp) {
+            uint2 pv[2];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] = acc[i][j][q];
-            } else {
-              const float* sq = (MODE == kDx) ? p.sq + e64 * 2 * D + D + n : p.sq + e64 * D + n;
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int j = 2 * jp + h2;
+              const int n = nt * BN + wn * WN + j * 16 + nql;
+              float v[4];
+              if (MX) {
 #pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * sq[q];
+                for (int q = 0; q < 4; ++q) v[q] = acc[i][j][q];
+              } else {
+                const float* sq = (MODE == kDx) ? p.sq + e64 * 2 * D + D + n : p.sq + e64 * D + n;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * sq[q];
+              }
+              if (MODE == kDx) {
+                const uint2 pw = *(const uint2*)(p.o0 + (int64_t)r * D + n);
+                v[0] = bf_lo(pw.x) + round_bf(v[0]);
+                v[1] = bf_hi(pw.x) + round_bf(v[1]);
+                v[2] = bf_lo(pw.y) + round_bf(v[2]);
+                v[3] = bf_hi(pw.y) + round_bf(v[3]);
+              }
+              pv[h2] = pack4(v);
             }
-            if (MODE == kDx) {
-              const uint2 pw = *(const uint2*)dst;
-              v[0] = bf_lo(pw.x) + round_bf(v[0]);
-              v[1] = bf_hi(pw.x) + round_bf(v[1]);
-              v[2] = bf_lo(pw.y) + round_bf(v[2]);
-              v[3] = bf_hi(pw.y) + round_bf(v[3]);
-            }
-            *(uint2*)dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+            const uint4 sv = span64(pv[0], pv[1], lane);
+            *(uint4*)(p.o0 + (int64_t)r * D + nt * BN + wn * WN + jp * 32 + g8) = sv;
           }
         }
       }
@@ -917,26 +937,34 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         if (r < seg1) {
           const float sp = MX ? 1.f : p.sp[r];
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int hh = nt * BN + wn * WN + j * 16 + nql;
-            const int64_t off = (int64_t)r * H + hh;
-            const uint2 gw = *(const uint2*)(p.g + off);
-            const uint2 uw = *(const uint2*)(p.u + off);
-            const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
-            const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
-            float dg[4], du[4];
+          for (int jp = 0; jp < TN / 2; ++jp) {
+            uint2 pdg[2], pdu[2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float dh = round_bf(MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * H + hh + q]);
-              const float sl = round_bf(silu_f(gv[q]));
-              const float dsl = round_bf(dh * uv[q]);
-              du[q] = dh * sl;
-              const float sg = 1.0f / (1.0f + expf(-gv[q]));
-              dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int j = 2 * jp + h2;
+              const int hh = nt * BN + wn * WN + j * 16 + nql;
+              const int64_t off = (int64_t)r * H + hh;
+              const uint2 gw = *(const uint2*)(p.g + off);
+              const uint2 uw = *(const uint2*)(p.u + off);
+              const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
+              const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
+              float dg[4], du[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const float dh = round_bf(MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * H + hh + q]);
+                const float sl = round_bf(silu_f(gv[q]));
+                const float dsl = round_bf(dh * uv[q]);
+                du[q] = dh * sl;
+                const float sg = 1.0f / (1.0f + expf(-gv[q]));
+                dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
+              }
+              pdg[h2] = pack4(dg);
+              pdu[h2] = pack4(du);
             }
-            const int64_t o2 = (int64_t)r * (2 * H) + hh;
-            *(uint2*)(p.o0 + o2) = make_uint2(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]));
-            *(uint2*)(p.o0 + o2 + H) = make_uint2(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]));
+            const int64_t o2 = (int64_t)r * (2 * H) + nt * BN + wn * WN + jp * 32 + g8;
+            const uint4 sdg = span64(pdg[0], pdg[1], lane), sdu = span64(pdu[0], pdu[1], lane);
+            *(uint4*)(p.o0 + o2) = sdg;
+            *(uint4*)(p.o0 + o2 + H) = sdu;
           }
         }
       }
@@ -952,13 +980,19 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
         else
           rowp = p.o0 + (e64 * D + m) * (int64_t)H;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int n = nt * BN + wn * WN + j * 16 + nql;
-          float v[4];
+        for (int jp = 0; jp < TN / 2; ++jp) {
+          uint2 pv[2];
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v[q] = (nk > 0) ? (MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * Ntot + n + q]) : 0.f;
-          *(uint2*)(rowp + n) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int j = 2 * jp + h2;
+            const int n = nt * BN + wn * WN + j * 16 + nql;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              v[q] = (nk > 0) ? (MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * Ntot + n + q]) : 0.f;
+            pv[h2] = pack4(v);
+          }
+          *(uint4*)(rowp + nt * BN + wn * WN + jp * 32 + g8) = span64(pv[0], pv[1], lane);
         }
       }
     }
