@@ -250,10 +250,12 @@ constexpr int kTRows = 128;  // slab rows transposed per pass
 //    row-wise MX layout, blocks of 32 columns): row r's 64 values go to
 //    qr + r * ldr and its two block scales to sr + r * ldsr.
 // A pass moves 128 rows (four 16-byte loads per thread) through s_tile
-// (128 row-major rows of 128 bytes, written with 16-byte stores); thread
-// (c, j) then reads column c of rows [32 j, 32 j + 32) as 2-byte reads (a wave
-// reads one row at a time: conflict-free). The next pass's loads are issued as
-// soon as the tile is in LDS.
+// (128 row-major rows of 128 bytes, written with 16-byte stores, the 16-byte
+// chunk c of row r at c ^ ((r / 16) % 8)). Each thread then quantizes two units
+// of 16 rows of one column (2-byte reads; the swizzle keeps the eight row
+// groups a wave reads at once in distinct banks) and stores their 16 bytes, so
+// that 8 consecutive lanes write 128 contiguous bytes of one output row. The
+// next pass's loads are issued as soon as the tile is in LDS.
 template <bool MX, bool ROWS>
 __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows, int n_out,
                                              uint8_t* __restrict__ out, int64_t ldo, uint8_t* __restrict__ sc,
@@ -261,7 +263,6 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
                                              uint8_t* __restrict__ qr = nullptr, int64_t ldr = 0,
                                              uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0) {
   const int t = threadIdx.x;
-  const int col = t & 63, j = t >> 6;
   uint4 v[4];
   auto load = [&](int a0) {
 #pragma unroll
@@ -295,58 +296,54 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * 256;
-      *(uint4*)(s_tile + (c >> 3) * 32 + (c & 7) * 4) = v[i];
+      const int r = c >> 3;
+      *(uint4*)(s_tile + r * 32 + (((c & 7) ^ ((r >> 4) & 7)) * 4)) = v[i];
     }
     const bool fast = !__syncthreads_or(nan != 0u);  // block-uniform: the tile holds no NaN
     if (a0 + kTRows < n_out) load(a0 + kTRows);
-    const int rb = a0 + j * 32;
-    if (rb < n_out) {
-      const uint16_t* xs = (const uint16_t*)s_tile + j * 32 * 64 + col;  // row k of the block at xs[64 k]
+    // unit (column cc, rows 16 kq .. 16 kq + 15 of the pass): 8 consecutive lanes cover one
+    // output row's 128 bytes, so every store instruction writes 8 rows x 128 contiguous bytes
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int u = t + 256 * h;
+      const int cc = u >> 3, kq = u & 7;
+      const int rb = a0 + 16 * kq;
+      // column cc of pass rows 16 kq + s sits in chunk (cc / 8) ^ kq of its row
+      const uint16_t* xs = (const uint16_t*)s_tile + (16 * kq) * 64 + (((cc >> 3) ^ kq) * 8) + (cc & 7);
+      float xv[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) xv[k] = bf2f(xs[64 * k]);
       float f;
       uint32_t e = 0;
-      uint32_t o[8];
-      if (fast) {
-        float xv[32];
+      if constexpr (MX) {
         float am = 0.f;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-          xv[k] = bf2f(xs[64 * k]);
-          am = fmaxf(am, fabsf(xv[k]));
-        }
-        if constexpr (MX) {
-          e = mx_exponent(am);
-          f = mx_multiplier(e);
-        } else {
-          f = s_col[col];
-        }
+        for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(xv[k]));
+        am = fmaxf(am, __shfl_xor(am, 1));  // the 32-row block is lanes kq, kq ^ 1
+        e = mx_exponent(am);
+        f = mx_multiplier(e);
+      } else {
+        f = s_col[cc];
+      }
+      uint32_t o[4];
+      if (fast) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
+        for (int q = 0; q < 4; ++q)
           o[q] = MX ? e4m3x4(xv[4 * q] * f, xv[4 * q + 1] * f, xv[4 * q + 2] * f, xv[4 * q + 3] * f)
                     : e4m3x4(xv[4 * q] / f, xv[4 * q + 1] / f, xv[4 * q + 2] / f, xv[4 * q + 3] / f);
       } else {
-        if constexpr (MX) {
-          float am = 0.f;
 #pragma unroll
-          for (int k = 0; k < 32; ++k) am = fmaxf(am, fabsf(bf2f(xs[64 * k])));
-          e = mx_exponent(am);
-          f = mx_multiplier(e);
-        } else {
-          f = s_col[col];
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < 4; ++q) {
           o[q] = 0;
 #pragma unroll
-          for (int bq = 0; bq < 4; ++bq) {
-            const float xv = bf2f(xs[64 * (4 * q + bq)]);
-            o[q] |= (MX ? e4m3(xv * f) : e4m3(xv / f)) << (8 * bq);
-          }
+          for (int bq = 0; bq < 4; ++bq) o[q] |= (MX ? e4m3(xv[4 * q + bq] * f) : e4m3(xv[4 * q + bq] / f)) << (8 * bq);
         }
       }
-      uint8_t* d = out + (int64_t)col * ldo + rb;
-      *(uint4*)d = make_uint4(o[0], o[1], o[2], o[3]);
-      if (rb + 32 <= n_out) *(uint4*)(d + 16) = make_uint4(o[4], o[5], o[6], o[7]);
-      if constexpr (MX) sc[(int64_t)col * sc_b + (int64_t)(rb / kMxBlock) * sc_k] = (uint8_t)e;
+      if (rb < n_out) {
+        *(uint4*)(out + (int64_t)cc * ldo + rb) = make_uint4(o[0], o[1], o[2], o[3]);
+        if constexpr (MX)
+          if ((kq & 1) == 0) sc[(int64_t)cc * sc_b + (int64_t)(rb / kMxBlock) * sc_k] = (uint8_t)e;
+      }
     }
   }
 }
