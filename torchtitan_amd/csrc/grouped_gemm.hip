@@ -546,6 +546,25 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         if (r < seg1) {
 #pragma unroll
           for (int jp = 0; jp < TN / 2; ++jp) {
+            if constexpr (MODE == kBwdDx && ACT == kSwiGLU && !kParkRegs) {
+              // the w3 half, rounded to bf16, in the span layout; the parked w1 half is
+              // read back from the dx rows as 16-byte pieces
+              const float lo[4] = {acc[i][2 * jp][0], acc[i][2 * jp][1], acc[i][2 * jp][2], acc[i][2 * jp][3]};
+              const float hi[4] = {acc[i][2 * jp + 1][0], acc[i][2 * jp + 1][1], acc[i][2 * jp + 1][2],
+                                   acc[i][2 * jp + 1][3]};
+              const uint4 sv = span64(pack4(lo), pack4(hi), lane);
+              const int n = nt * BN + wn * WN + jp * 32 + g8;
+              if (TAIL && n >= D) continue;
+              uint16_t* dst = outp + (int64_t)r * D + n;
+              const uint4 pw = *(const uint4*)dst;
+              const uint32_t a4[4] = {sv.x, sv.y, sv.z, sv.w}, b4[4] = {pw.x, pw.y, pw.z, pw.w};
+              uint32_t o4[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                o4[q] = pack_bf2(bf_lo(b4[q]) + bf_lo(a4[q]), bf_hi(b4[q]) + bf_hi(a4[q]));
+              *(uint4*)dst = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+              continue;
+            }
             uint2 pv[2];
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
@@ -560,10 +579,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
                 v[2] = round_bf(v[2]) + bf_lo(bw.y);
                 v[3] = round_bf(v[3]) + bf_hi(bw.y);
               }
-              if (MODE == kBwdDx && ACT == kSwiGLU) {
-                uint2 pw = make_uint2(0, 0);
-                if constexpr (kParkRegs) pw = make_uint2(park[i][j][0], park[i][j][1]);
-                else if (in) pw = *(const uint2*)(outp + (int64_t)r * D + n);
+              if constexpr (MODE == kBwdDx && ACT == kSwiGLU && kParkRegs) {
+                const uint2 pw = make_uint2(park[i][j][0], park[i][j][1]);
                 v[0] = bf_lo(pw.x) + round_bf(v[0]);
                 v[1] = bf_hi(pw.x) + round_bf(v[1]);
                 v[2] = bf_lo(pw.y) + round_bf(v[2]);
@@ -579,32 +596,37 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         }
       }
     } else if (MODE == kBwdDgu) {
+      // dh = bf16(dy . w2) is gathered into the 64-byte span layout first, so g and u
+      // are read, and dg and du written, as 16-byte pieces of 64 contiguous bytes per row
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
 #pragma unroll
           for (int jp = 0; jp < TN / 2; ++jp) {
-            uint2 pdg[2], pdu[2];
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-            const int j = 2 * jp + h2;
-            const int hh = nt * BN + wn * WN + j * 16 + nq;
-            const bool in = !TAIL || hh < H;
+            const float lo[4] = {acc[i][2 * jp][0], acc[i][2 * jp][1], acc[i][2 * jp][2], acc[i][2 * jp][3]};
+            const float hi[4] = {acc[i][2 * jp + 1][0], acc[i][2 * jp + 1][1], acc[i][2 * jp + 1][2],
+                                 acc[i][2 * jp + 1][3]};
+            const uint4 sdh = span64(pack4(lo), pack4(hi), lane);
+            const int hh = nt * BN + wn * WN + jp * 32 + g8;
+            if (TAIL && hh >= H) continue;
             const int64_t off = (int64_t)r * H + hh;
-            const uint2 gw = in ? *(const uint2*)(p.g + off) : make_uint2(0, 0);
-            const uint2 uw = in ? *(const uint2*)(p.u + off) : make_uint2(0, 0);
-            const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
-            const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
-            float dg[4], du[4];
-            if constexpr (ACT == kOssGLU) {
-              // autograd of oss_glu, each bf16 op's gradient rounded to bf16
-              const float L = p.limit, al = p.alpha;
+            const uint4 gw = *(const uint4*)(p.g + off);
+            const uint4 uw = *(const uint4*)(p.u + off);
+            const uint32_t dhw[4] = {sdh.x, sdh.y, sdh.z, sdh.w};
+            const uint32_t gww[4] = {gw.x, gw.y, gw.z, gw.w};
+            const uint32_t uww[4] = {uw.x, uw.y, uw.z, uw.w};
+            float dg[8], du[8];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const float dh = round_bf(acc[i][j][q]);
-                const float xg = gv[q] > L ? L : gv[q];
-                const float xl = uv[q] < -L ? -L : (uv[q] > L ? L : uv[q]);
+            for (int q = 0; q < 8; ++q) {
+              const float dh = (q & 1) ? bf_hi(dhw[q >> 1]) : bf_lo(dhw[q >> 1]);
+              const float gv = (q & 1) ? bf_hi(gww[q >> 1]) : bf_lo(gww[q >> 1]);
+              const float uv = (q & 1) ? bf_hi(uww[q >> 1]) : bf_lo(uww[q >> 1]);
+              if constexpr (ACT == kOssGLU) {
+                // autograd of oss_glu, each bf16 op's gradient rounded to bf16
+                const float L = p.limit, al = p.alpha;
+                const float xg = gv > L ? L : gv;
+                const float xl = uv < -L ? -L : (uv > L ? L : uv);
                 const float s = round_bf(sigmoid_f(round_bf(xg * al)));
                 const float og = round_bf(xg * s);
                 const float da = round_bf(dh * round_bf(xl + 1.0f));  // d(glu output)
@@ -612,29 +634,21 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
                 const float ds = round_bf(da * xg);                    // d(sigmoid output)
                 const float dz = round_bf((ds * (1.0f - s)) * s);      // sigmoid_backward
                 const float dxg = round_bf(da * s) + round_bf(dz * al);
-                dg[q] = gv[q] <= L ? dxg : 0.f;                        // clamp(max=L) backward
-                du[q] = (uv[q] >= -L && uv[q] <= L) ? dl : 0.f;        // clamp(-L, L) backward
-              }
-            } else {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const float dh = round_bf(acc[i][j][q]);
-                const float sl = round_bf(silu_f(gv[q]));
-                const float dsl = round_bf(dh * uv[q]);
+                dg[q] = gv <= L ? dxg : 0.f;                           // clamp(max=L) backward
+                du[q] = (uv >= -L && uv <= L) ? dl : 0.f;              // clamp(-L, L) backward
+              } else {
+                const float sl = round_bf(silu_f(gv));
+                const float dsl = round_bf(dh * uv);
                 du[q] = dh * sl;
-                const float sg = 1.0f / (1.0f + expf(-gv[q]));
-                dg[q] = dsl * sg * (1.0f + gv[q] * (1.0f - sg));
+                const float sg = 1.0f / (1.0f + expf(-gv));
+                dg[q] = dsl * sg * (1.0f + gv * (1.0f - sg));
               }
             }
-            pdg[h2] = pack4(dg);
-            pdu[h2] = pack4(du);
-            }
-            const int hh = nt * BN + wn * WN + jp * 32 + g8;
-            const uint4 sdg = span64(pdg[0], pdg[1], lane), sdu = span64(pdu[0], pdu[1], lane);
-            if (TAIL && hh >= H) continue;
             const int64_t o2 = (int64_t)r * (2 * H) + hh;
-            *(uint4*)(p.out_dgu + o2) = sdg;
-            *(uint4*)(p.out_dgu + o2 + H) = sdu;
+            *(uint4*)(p.out_dgu + o2) = make_uint4(pack_bf2(dg[0], dg[1]), pack_bf2(dg[2], dg[3]),
+                                                   pack_bf2(dg[4], dg[5]), pack_bf2(dg[6], dg[7]));
+            *(uint4*)(p.out_dgu + o2 + H) = make_uint4(pack_bf2(du[0], du[1]), pack_bf2(du[2], du[3]),
+                                                       pack_bf2(du[4], du[5]), pack_bf2(du[6], du[7]));
           }
         }
       }
