@@ -434,18 +434,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
+        if constexpr (kParkRegs) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const uint32_t lo = pack_bf2(acc[i][j][0], acc[i][j][1]), hi = pack_bf2(acc[i][j][2], acc[i][j][3]);
-          if constexpr (kParkRegs) {
-            park[i][j][0] = lo;
-            park[i][j][1] = hi;
-          } else {
-            const int n = nt * BN + wn * WN + j * 16 + nq;
-            if (r < seg1 && (!TAIL || n < D)) *(uint2*)(p.out_dx + (int64_t)r * D + n) = make_uint2(lo, hi);
+          for (int j = 0; j < TN; ++j) {
+            park[i][j][0] = pack_bf2(acc[i][j][0], acc[i][j][1]);
+            park[i][j][1] = pack_bf2(acc[i][j][2], acc[i][j][3]);
           }
-          acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        } else {
+          // 64-byte row pieces of the dx rows (read back the same way in the epilogue)
+#pragma unroll
+          for (int jp = 0; jp < TN / 2; ++jp) {
+            const float lo[4] = {acc[i][2 * jp][0], acc[i][2 * jp][1], acc[i][2 * jp][2], acc[i][2 * jp][3]};
+            const float hi[4] = {acc[i][2 * jp + 1][0], acc[i][2 * jp + 1][1], acc[i][2 * jp + 1][2],
+                                 acc[i][2 * jp + 1][3]};
+            const uint4 sv = span64(pack4(lo), pack4(hi), lane);
+            const int n = nt * BN + wn * WN + jp * 32 + 8 * (lane >> 4);
+            if (r < seg1 && (!TAIL || n < D)) *(uint4*)(p.out_dx + (int64_t)r * D + n) = sv;
+          }
         }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     };
 
