@@ -31,13 +31,20 @@ inline int launch_status() {
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32. The narrowing conversion is round-to-nearest-even with NaN
 // mapped to the canonical quiet NaN 0x7FC0, which is what torch's bf16 casts do.
+// It runs on gfx950's v_cvt_pk_bf16_f32 (what clang emits for a float -> __bf16
+// conversion) after NaNs are replaced by the canonical one; checked on the GPU
+// against the integer formulation (u + 0x7fff + ((u >> 16) & 1)) >> 16, NaN ->
+// 0x7fc0, for every fp32 bit pattern, alone and packed in pairs.
 // ---------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
 
+__device__ __forceinline__ float nan_canon(float f) { return f != f ? __uint_as_float(0x7fc00000u) : f; }
+
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return (f != f) ? 0x7fc0u : r;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)nan_canon(f));
 }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
@@ -45,7 +52,10 @@ __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 // lo/hi bf16 of a packed dword
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  const f32x2_t v = {nan_canon(lo), nan_canon(hi)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 
 // Epilogue stores in 64-byte row pieces. An accumulator tile leaves lane (r, g),
 // r = lane % 16, g = lane / 16, with 4 consecutive columns 4g .. 4g + 3 of row r
