@@ -507,7 +507,8 @@ def _deterministic_scatter_add(out: torch.Tensor, index: torch.Tensor, src: torc
         torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
 
 
-def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None) -> torch.Tensor:
+def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: dict | None = None,
+                              logit_values: torch.Tensor | None = None) -> torch.Tensor:
     """MoE.forward (moe.py:380-477) with the router (moe.py:211-274), the
     reorderer (moe.py:291-332), _run_experts_grouped_mm (moe.py:53-70) and the
     shared FeedForward (feed_forward.py:53-54) written as the same torch calls
@@ -518,7 +519,12 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: d
       * torch._grouped_mm in bf16, or the per-expert matmul loop when
         cfg.use_grouped_mm is False.
     This is the reference's CPU MoE path used as the CPU baseline, and, run on
-    the GPU, the op-for-op reference the fused kernels are compared against."""
+    the GPU, the op-for-op reference the fused kernels are compared against.
+
+    logit_values ([N, E] fp32, optional) replaces the values of the gate logits
+    while their gradient still flows through the autocast gate: a caller whose
+    logits differ from this GEMM's by fp32 summation order routes both sides on
+    the same values (the difference is asserted to be that small)."""
     rc = cfg.router
     bs, slen, dim = x.shape
     x2 = x.view(-1, dim)
@@ -529,6 +535,15 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: d
         warnings.simplefilter("ignore")
         with torch.autocast(device_type=x.device.type, dtype=torch.float32):
             logits = F.linear(x2, gate_w, params.get("gate_bias"))
+    if logit_values is not None:
+        fix = logit_values.detach().float()
+        d = fix - logits.detach()
+        tol = 1e-5 * logits.detach().abs().max().clamp_min(1e-30)
+        if not bool(d.abs().max() <= tol):
+            raise AssertionError(f"logit_values differ from the fp32 gate GEMM by {d.abs().max().item():.3e}")
+        logits = logits + d
+        if not torch.equal(logits.detach(), fix):
+            raise AssertionError("logit_values not reproduced exactly")
     top_scores, idx, _counts, _scores = router_forward_torch(logits, params.get("expert_bias"), rc)
     flat = idx.view(-1)
     counts = _histc_counts(flat, rc.num_experts)

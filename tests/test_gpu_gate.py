@@ -1,0 +1,119 @@
+"""Router gate logits in fp32 (torchtitan/models/common/moe.py:230-232) on the GPU.
+
+For bf16 x and W the layer computes the gate on bf16 GEMMs with fp32
+accumulation (moe._GateF32) instead of the fp32 GEMM under autocast. Both are
+checked against the fp64 product of the same values:
+  * logits: the error of the bf16-GEMM path is at most 2x the fp32 path's
+    (plus 1e-6 of the largest logit): both are fp32 sums of the same exact
+    products, in different orders;
+  * dx, dW (rounded to bf16): equal to bf16(fp64 gradient) wherever the fp32
+    path is, except at most 1e-3 of the elements, which may sit on a bf16
+    rounding boundary; the worst error, in bf16 ulps of the true value, at
+    most twice the fp32 path's (where the sum cancels to a value far below its
+    terms both are many ulps off) or one ulp;
+  * bias gradient: the fp32 column sum of the logit gradient.
+The upstream gradient spans six decades, so the second and third bf16 terms of
+its split carry weight.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests.conftest import banner
+from torchtitan_amd import Linear
+from torchtitan_amd.moe import gate_logits_f32
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "kimi_dim2304_e256": (4096, 2304, 256, False),
+    "gptoss_dim2880_e32_bias": (2048, 2880, 32, True),
+    "ragged_n1000_dim768_e64": (1000, 768, 64, False),
+}
+
+
+def _ulp_bf16(t: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values around |t| (fp32 tensor)."""
+    e = torch.floor(torch.log2(t.abs().clamp_min(2.0 ** -126)))
+    return torch.exp2(e - 7)
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_gate_logits_f32_vs_fp64(case):
+    n, d, e, bias = CASES[case]
+    banner(f"gate {case}: n={n} dim={d} experts={e} bias={bias}")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    gate = Linear(Linear.Config(in_features=d, out_features=e, bias=bias)).to(dev)
+    with torch.no_grad():
+        gate.weight.data = (torch.randn(e, d, generator=g, device=dev) * 0.02).bfloat16()
+        if bias:
+            gate.bias.data = (torch.randn(e, generator=g, device=dev) * 0.1).bfloat16()
+    x = torch.randn(n, d, generator=g, device=dev).bfloat16()
+    mag = torch.exp(torch.empty(n, e, device=dev).uniform_(-7.0, 7.0, generator=g))
+    up = torch.randn(n, e, generator=g, device=dev) * mag
+
+    def run(fast: bool):
+        xs = x.clone().requires_grad_(True)
+        gate.zero_grad(set_to_none=True)
+        if fast:
+            y = gate_logits_f32(xs, gate)
+        else:
+            with torch.autocast(device_type="cuda", dtype=torch.float32):
+                y = gate(xs)
+        y.backward(up)
+        return y.detach(), xs.grad, gate.weight.grad, gate.bias.grad if bias else None
+
+    y_f, dx_f, dw_f, db_f = run(True)
+    y_r, dx_r, dw_r, db_r = run(False)
+    assert y_f.dtype == torch.float32 and dx_f.dtype == torch.bfloat16 and dw_f.dtype == torch.bfloat16
+
+    xd, wd, upd = x.double(), gate.weight.detach().double(), up.double()
+    y_t = xd @ wd.t()
+    if bias:
+        y_t = y_t + gate.bias.detach().double()
+    err_f = (y_f.double() - y_t).abs().max().item()
+    err_r = (y_r.double() - y_t).abs().max().item()
+    scale = y_t.abs().max().item()
+    print(f"[case] {case}: logits max err fast {err_f:.3e} fp32-autocast {err_r:.3e} (max |logit| {scale:.3e})",
+          flush=True)
+    assert err_f <= 2 * err_r + 1e-6 * scale
+
+    for name, got, ref, truth in (
+        ("dx", dx_f, dx_r, upd @ wd),
+        ("dW", dw_f, dw_r, upd.t() @ xd),
+    ):
+        t32 = truth.float()
+        tb = t32.bfloat16().float()
+        diff_f = (got.float() != tb)
+        diff_r = (ref.float() != tb)
+        frac_f = diff_f.float().mean().item()
+        frac_r = diff_r.float().mean().item()
+        worst_f = ((got.float() - t32).abs() / _ulp_bf16(t32)).max().item()
+        worst_r = ((ref.float() - t32).abs() / _ulp_bf16(t32)).max().item()
+        print(f"[case] {case}: {name} elements != bf16(fp64): fast {frac_f:.2e} fp32-autocast {frac_r:.2e}; "
+              f"worst ulp fast {worst_f:.2f} fp32-autocast {worst_r:.2f}", flush=True)
+        assert frac_f <= frac_r + 1e-3
+        assert worst_f <= max(1.0, 2 * worst_r)
+    if bias:
+        assert torch.allclose(db_f.float(), upd.sum(0).float(), rtol=1e-2, atol=0)
+        assert torch.equal(db_f, db_r) or (db_f.float() - db_r.float()).abs().max() <= _ulp_bf16(
+            upd.sum(0).float()).max()
+
+
+def test_gate_logits_fallback_paths():
+    """fp32 weights, or an outer autocast, keep the reference's autocast region."""
+    dev = torch.device("cuda:0")
+    gate = Linear(Linear.Config(in_features=256, out_features=16)).to(dev)
+    x = torch.randn(64, 256, device=dev).bfloat16()
+    y = gate_logits_f32(x, gate)  # fp32 weight
+    with torch.autocast(device_type="cuda", dtype=torch.float32):
+        ref = gate(x)
+    assert torch.equal(y, ref)
+    gate.weight.data = gate.weight.data.bfloat16()
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        y2 = gate_logits_f32(x, gate)
+    with torch.autocast(device_type="cuda", dtype=torch.float32):
+        ref2 = F.linear(x, gate.weight)
+    assert y2.dtype == torch.float32 and torch.equal(y2, ref2)

@@ -190,3 +190,19 @@ def test_load_balancing_hook_registration_follows_reference_rules():
     assert len(_moe_blocks([Model(1e-3)])) == 2
     # a model without a `layers` dict: every MoE module
     assert len(_moe_blocks([torch.nn.Sequential(_cfg(hs=0).build())])) == 1
+
+
+def test_gate_gradient_split_is_exact():
+    """The gate backward's three bf16 terms add back to the fp32 gradient exactly
+    (8 + 8 + 8 significand bits), over twelve decades and both signs; two terms
+    would not."""
+    from torchtitan_amd.moe import _bf16_terms
+
+    g = torch.Generator().manual_seed(3)
+    d = torch.randn(512, 64, generator=g) * torch.exp(torch.empty(512, 64).uniform_(-14.0, 14.0, generator=g))
+    d[0, :4] = torch.tensor([0.0, -0.0, 1.0 + 2.0 ** -23, -(2.0 - 2.0 ** -23)])
+    t = _bf16_terms(d)
+    assert t.dtype == torch.bfloat16 and t.shape == (512, 192)
+    hi, mid, lo = (t[:, i * 64:(i + 1) * 64].float() for i in range(3))
+    assert torch.equal((hi + mid) + lo, d)
+    assert not torch.equal(hi + mid, d)

@@ -127,6 +127,67 @@ class GroupedExperts(Module):
         return _run_experts_for_loop(w1, w2, w3, x, num_tokens_per_expert)
 
 
+def _bf16_terms(d: torch.Tensor) -> torch.Tensor:
+    """[N, C] fp32 -> [N, 3C] bf16 (hi | mid | lo) with hi + mid + lo == d: each
+    term takes the next 8 significand bits of what the previous ones left, so
+    three cover fp32's 24."""
+    hi = d.bfloat16()
+    r = d - hi.float()
+    mid = r.bfloat16()
+    lo = (r - mid.float()).bfloat16()
+    return torch.cat([hi, mid, lo], dim=1)
+
+
+class _GateF32(torch.autograd.Function):
+    """fp32(x) @ fp32(W)^T (+ fp32(b)) for bf16 x and W, on bf16 GEMMs with fp32
+    accumulation and fp32 output.
+
+    A product of two bf16 values is exact in fp32, so the forward equals the fp32
+    GEMM of the reference's autocast region (moe.py:230-232) up to summation
+    order. In the backward the fp32 logit gradient is split exactly into three
+    bf16 terms (_bf16_terms), and dx, dW are bf16 GEMMs over the 3x longer sum,
+    again exact products accumulated in fp32; they are rounded to x's and W's
+    dtype once, as autocast's casts do."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
+        logits = torch.mm(x, w.t(), out_dtype=torch.float32)
+        if b is not None:
+            logits += b.float()
+        ctx.save_for_backward(x, w)
+        ctx.has_bias = b is not None
+        ctx.b_dtype = b.dtype if b is not None else None
+        return logits
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        x, w = ctx.saved_tensors
+        d3 = _bf16_terms(grad.float().contiguous())
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(d3, torch.cat([w, w, w], dim=0), out_dtype=torch.float32).to(x.dtype)
+        if ctx.needs_input_grad[1]:
+            e = w.shape[0]
+            dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
+            dw = ((dw3[:e] + dw3[e:2 * e]) + dw3[2 * e:]).to(w.dtype)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = grad.float().sum(0).to(ctx.b_dtype)
+        return dx, dw, db
+
+
+def gate_logits_f32(x: torch.Tensor, gate: nn.Linear) -> torch.Tensor:
+    """The router's gate in fp32 (moe.py:230-232). bf16 x and W on the GPU take
+    _GateF32; anything else runs the reference's autocast region as is."""
+    w, b = _local(gate.weight), gate.bias
+    b = _local(b) if b is not None else None
+    if (x.is_cuda and x.dim() == 2 and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and (b is None or b.dtype in (torch.bfloat16, torch.float32))
+            and not torch.is_autocast_enabled(x.device.type)):
+        return _GateF32.apply(x.contiguous(), w.contiguous(), b)
+    with torch.autocast(device_type=x.device.type, dtype=torch.float32):
+        return gate(x)
+
+
 class TokenChoiceTopKRouter(Module):
     """Token-choice top-K routing with optional group-limited selection."""
 
@@ -175,9 +236,8 @@ class TokenChoiceTopKRouter(Module):
     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """x [bs*slen, dim] -> (top_scores [N,K] f32, selected_experts_indices [N,K] i64,
         num_tokens_per_expert [E] i64)."""
-        # fp32 gate GEMM on torch, as in the reference (moe.py:231-232)
-        with torch.autocast(device_type=x.device.type, dtype=torch.float32):
-            logits = self.gate(x)
+        # fp32 gate logits, as in the reference (moe.py:230-232)
+        logits = gate_logits_f32(x, self.gate)
         if self.score_func not in ops.SCORE_FUNCS:
             raise NotImplementedError(f"Unknown score function {self.score_func}")
         groups, limited = self._group_config()
