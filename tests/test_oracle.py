@@ -401,6 +401,41 @@ def test_moe_forward_matches_reference_op_sequence(score_before, grouped):
         torch.testing.assert_close(a, b, **tol)
 
 
+def test_reference_ops_logit_values_override():
+    """logit_values replaces the gate logits' values only: the same values give the
+    same output and gradients; values an ulp away keep the gate in the gradient
+    path; values further off than fp32 summation order are refused."""
+    g = torch.Generator().manual_seed(5)
+    bs, slen, d, e, k, h = 2, 16, 32, 8, 2, 48
+    params = {"gate": torch.randn(e, d, generator=g) * 0.1, "w1": torch.randn(e, h, d, generator=g) * 0.05,
+              "w2": torch.randn(e, d, h, generator=g) * 0.05, "w3": torch.randn(e, h, d, generator=g) * 0.05}
+    x = torch.randn(bs, slen, d, generator=g)
+    gout = torch.randn(bs, slen, d, generator=g)
+    rc = R.RouterCfg(num_experts=e, top_k=k, score_func="sigmoid", route_norm=True, route_scale=1.0)
+    cfg = R.MoECfg(router=rc, dim=d, hidden_dim=h, score_before_experts=False, use_grouped_mm=False,
+                   has_shared=False)
+    logits = x.view(-1, d) @ params["gate"].t()
+
+    def run(values):
+        p = {n: t.clone().requires_grad_(True) for n, t in params.items()}
+        xi = x.clone().requires_grad_(True)
+        out = R.moe_forward_reference_ops(p, xi, cfg, logit_values=values)
+        out.backward(gout)
+        return out.detach(), xi.grad, p["gate"].grad
+
+    base = run(None)
+    same = run(logits.clone())
+    for a, b in zip(base, same):
+        assert torch.equal(a, b)
+    nudged = logits.clone()
+    nudged[0, 0] = torch.nextafter(nudged[0, 0], torch.tensor(float("inf")))
+    out_n, dx_n, dgate_n = run(nudged)
+    assert dgate_n is not None and torch.count_nonzero(dgate_n) > 0
+    torch.testing.assert_close(dgate_n, base[2], rtol=1e-4, atol=1e-6)
+    with pytest.raises(AssertionError, match="differ from the fp32 gate GEMM"):
+        run(logits + 1e-3 * logits.abs().max())
+
+
 # ---------------------------------------------------------------------------
 # aux-loss-free bias update: hand-worked closed forms (optimizer.py:416-431)
 # ---------------------------------------------------------------------------
