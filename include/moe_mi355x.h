@@ -227,8 +227,10 @@ int moe_grouped_col_sum(const uint16_t* src, int64_t ld_src, const int64_t* coun
  * torchao's Float8TrainingOpConfig on the experts
  * (torchtitan/components/quantization/float8.py:260-288): dynamic rowwise
  * scales, fp32 accumulation, bf16 outputs, token groups padded to 16
- * (quantization/__init__.py:37-40). Quantization: s = max(amax, 1e-12) / 448,
- * q = e4m3fn(x / s) rounded to nearest even. fp8 tensors are uint8_t*.
+ * (quantization/__init__.py:37-40). Quantization with torchao's power-of-two
+ * scales: s = 2^-j, j = floor(log2(fp32(448 / max(amax, 1e-12)))) (the division
+ * in fp64), q = e4m3fn(x / s) rounded to nearest even (x / s exact, |x / s| <= 448).
+ * fp8 tensors are uint8_t*.
  * ------------------------------------------------------------------------- */
 
 /* Rows of the token-transposed fp8 tensors: n_rows + n_experts * 15 (every
@@ -240,7 +242,7 @@ int moe_fp8_quant_rows(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q
                        moe_stream_t stream);
 
 /* x [E, a, b] bf16 -> per expert e and column j: scale[e*scale_expert_stride + j]
- * = amax over a / 448, and the quantized column written as a row of a values
+ * = the scale of the amax over a, and the quantized column written as a row of a values
  * at q + e*q_expert_stride + j*q_row_stride (a transposed copy). */
 int moe_fp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
                          int64_t q_expert_stride, int64_t q_row_stride, float* scale,

@@ -579,22 +579,37 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: d
 
 
 # ---------------------------------------------------------------------------
-# fp8 e4m3 grouped GEMMs (parity unpinned: the reference delegates to torchao's
-# Float8TrainingOpConfig, torchtitan/components/quantization/float8.py:260-288,
-# which is absent; this restates its published rowwise recipe)
+# fp8 e4m3 grouped GEMMs (parity unpinned against torchao: the reference delegates
+# to torchao's Float8TrainingOpConfig, torchtitan/components/quantization/float8.py:260-288,
+# which is absent; this restates its rowwise recipe with power-of-two scales, pinned
+# by hand-worked scales and an independent e4m3 encoder in tests/test_oracle.py)
 # ---------------------------------------------------------------------------
 
 FP8_MAX = 448.0  # largest finite float8_e4m3fn
 FP8_PAD = 16  # token-group alignment for fp8 grouped GEMMs (quantization/__init__.py:37-40)
 
 
+def fp8_scale(amax: torch.Tensor) -> torch.Tensor:
+    """Rowwise float8 scale of torchao's MoE training (torchao nightly, not vendored:
+    prototype/moe_training `_Float8GroupedMM` calls float8_utils.tensor_to_scale
+    with round_scales_to_power_of_2=True): m = fp32(448 / max(amax, 1e-12))
+    formed in fp64, rounded down to a power of two 2^j. Returns the dequantization
+    multiplier s = 2^-j (torchao passes the reciprocal of its scale to the GEMM).
+    floor(log2 m) is taken from m's exponent; for bf16 inputs m is a power of two
+    or at least 2^-9 below the next one, so a log2-based floor gives the same j."""
+    m = (FP8_MAX / amax.double().clamp_min(1e-12)).float()
+    _, e = torch.frexp(m)
+    return torch.ldexp(torch.ones_like(m), (1 - e).float())
+
+
 def quant_fp8_rows(x: torch.Tensor, dim: int = -1):
     """Dynamic fp8 quantization with one scale per slice along `dim`:
-    s = max(amax, 1e-12) / 448 (fp32), q = e4m3fn(x / s) (round to nearest even).
+    s = fp8_scale(amax), q = e4m3fn(x / s) (x / s is exact, |x / s| <= 448;
+    round to nearest even), which is torchao's to_fp8_saturated(x * 2^j).
     Returns (q float8_e4m3fn, s fp32 with `dim` kept as size 1)."""
     xf = x.float()
-    amax = xf.abs().amax(dim=dim, keepdim=True).clamp_min(1e-12)
-    s = amax / FP8_MAX
+    amax = xf.abs().amax(dim=dim, keepdim=True)
+    s = fp8_scale(amax)
     q = (xf / s).to(torch.float8_e4m3fn)
     return q, s
 

@@ -683,3 +683,79 @@ def test_oss_grouped_mm_matches_for_loop_and_float64():
     assert torch.equal(grouped, loop)
     f64 = R.oss_experts_for_loop(w1.double(), b1.double(), w2.double(), b2.double(), 7.0, x.double(), cnt)
     assert ((grouped.double() - f64).abs().max() / f64.abs().max()).item() < 2e-2
+
+
+# ---------------------------------------------------------------------------
+# fp8 rowwise quantization: power-of-two scales and the e4m3 rounding
+# ---------------------------------------------------------------------------
+
+
+def test_fp8_scale_known_answers():
+    """s = 2^-floor(log2(448 / max(amax, 1e-12))), worked by hand."""
+    amax = torch.tensor([1.0, 448.0, 0.5, 0.0, 3.0, 7.0 * 2.0 ** -10, 1e30, 449.0, 224.0, 223.0])
+    want = torch.tensor([2.0 ** -8,   # 448 / 1 = 448 in [256, 512)
+                         1.0,         # exactly 1
+                         2.0 ** -9,   # 896 in [512, 1024)
+                         2.0 ** -48,  # 448e12 in [2^48, 2^49)
+                         2.0 ** -7,   # 149.3 in [128, 256)
+                         2.0 ** -16,  # exactly 2^16
+                         2.0 ** 91,   # 4.48e-28 in [2^-91, 2^-90)
+                         2.0,         # 0.998 in [0.5, 1)
+                         0.5,         # exactly 2
+                         0.5])        # 2.009 in [2, 4)
+    got = R.fp8_scale(amax)
+    assert torch.equal(got, want), (got, want)
+
+
+def test_fp8_scale_range_and_power_of_two():
+    """Over 30 decades of amax above the 1e-12 floor: s is a power of two and
+    amax / s lies in (224, 448]."""
+    g = torch.Generator().manual_seed(9)
+    amax = torch.exp(torch.empty(20000).uniform_(-27.0, 46.0, generator=g)).bfloat16().float()
+    s = R.fp8_scale(amax)
+    mant, _ = torch.frexp(s)
+    assert torch.all(mant == 0.5)
+    r = amax / s
+    assert torch.all(r <= 448.0) and torch.all(r > 224.0)
+
+
+def _e4m3fn_rne_codes(v: np.ndarray) -> np.ndarray:
+    """Independent OCP e4m3fn encoder for |v| <= 448: the nearest of the 127 finite
+    non-negative codes (bias 7, 3 mantissa bits, subnormals 2^-9 apart), ties to
+    the even code, sign in bit 7."""
+    codes = np.arange(0x7F)
+    ex, m = codes >> 3, codes & 7
+    vals = np.where(ex == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (ex - 7.0))
+    a = np.abs(v.astype(np.float64))[:, None]
+    d = np.abs(vals[None, :] - a)
+    best = d.min(axis=1, keepdims=True)
+    cand = np.where(d == best, codes[None, :], 1 << 10)
+    even = np.where((cand & 1) == 0, cand, 1 << 10).min(axis=1)
+    pick = np.where(even < (1 << 10), even, cand.min(axis=1))
+    return (pick | np.where(np.signbit(v), 0x80, 0)).astype(np.uint8)
+
+
+def test_fp8_cast_matches_independent_e4m3_encoder():
+    """torch's float8_e4m3fn cast, which quant_fp8_rows applies to x / s, equals an
+    independent round-to-nearest-even encoder on every bf16 value in [-448, 448]."""
+    bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    v = bits.float()
+    v = v[torch.isfinite(v) & (v.abs() <= 448.0)]
+    got = v.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    want = _e4m3fn_rne_codes(v.numpy())
+    # -0.0 encodes as 0x80 in both
+    assert np.array_equal(got, want)
+
+
+def test_quant_fp8_rows_rounding_bound():
+    """Each dequantized value q * s is x rounded to the e4m3 grid scaled by s:
+    within half an e4m3 spacing of x / s, and the row's amax lands in (224, 448]."""
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(64, 96, generator=g) * torch.exp(torch.empty(64, 1).uniform_(-20, 20, generator=g))).bfloat16()
+    q, s = R.quant_fp8_rows(x)
+    y = x.float() / s
+    back = q.float()
+    a = y.abs().clamp_min(2.0 ** -6)
+    half_spacing = torch.exp2(torch.floor(torch.log2(a)) - 4)
+    assert torch.all((back - y).abs() <= half_spacing)
+    assert torch.all(y.abs().amax(dim=1) > 224.0) and torch.all(y.abs().amax(dim=1) <= 448.0)

@@ -6,7 +6,7 @@
 // token groups padded to 16 (quantization/__init__.py:37-40). This file
 // restates that recipe for gfx950:
 //
-//  * quantizers (HBM-bound): x -> (q = e4m3fn(x / s), s = max(amax, 1e-12) / 448)
+//  * quantizers (HBM-bound): x -> (q = e4m3fn(x / s), s = 2^-floor(log2(448 / max(amax, 1e-12))))
 //      - moe_fp8_quant_rows: one scale per row of a [rows, K] tensor;
 //      - moe_fp8_quant_cols_t: per expert, one scale per column b of an
 //        [E, A, B] tensor, written transposed as [E, B, A];
@@ -104,7 +104,16 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-__device__ __forceinline__ float scale_of(float amax) { return fmaxf(amax, 1e-12f) / kFp8Max; }
+// Rowwise scale of torchao's float8 MoE training (scales rounded down to powers of
+// two): m = fp32(448 / max(amax, 1e-12)) formed in fp64, j = floor(log2 m) from m's
+// exponent; returns the dequantization multiplier s = 2^-j, so x / s is exact and
+// |x / s| <= 448 before the e4m3 rounding.
+__device__ __forceinline__ float scale_of(float amax) {
+  const float m = (float)(448.0 / fmax((double)amax, 1e-12));
+  int e;
+  (void)frexpf(m, &e);  // m = f 2^e with f in [0.5, 1)
+  return ldexpf(1.0f, 1 - e);
+}
 
 constexpr int kMxBlock = 32;  // MXFP8 scaling block (k elements per e8m0 scale)
 constexpr int kMxPad = 32;    // MXFP8 token-group alignment
