@@ -148,17 +148,6 @@ __device__ __forceinline__ float amax8(uint4 v) {
 }
 
 // fast: the wave's data holds no NaN (hardware conversion)
-__device__ __forceinline__ uint2 quant8(uint4 v, float s, bool fast) {
-  if (fast)
-    return make_uint2(e4m3x4(bf_lo(v.x) / s, bf_hi(v.x) / s, bf_lo(v.y) / s, bf_hi(v.y) / s),
-                      e4m3x4(bf_lo(v.z) / s, bf_hi(v.z) / s, bf_lo(v.w) / s, bf_hi(v.w) / s));
-  const uint32_t lo = e4m3(bf_lo(v.x) / s) | (e4m3(bf_hi(v.x) / s) << 8) | (e4m3(bf_lo(v.y) / s) << 16) |
-                      (e4m3(bf_hi(v.y) / s) << 24);
-  const uint32_t hi = e4m3(bf_lo(v.z) / s) | (e4m3(bf_hi(v.z) / s) << 8) | (e4m3(bf_lo(v.w) / s) << 16) |
-                      (e4m3(bf_hi(v.w) / s) << 24);
-  return make_uint2(lo, hi);
-}
-
 __device__ __forceinline__ uint2 mx_quant8(uint4 v, float f, bool fast) {
   if (fast)
     return make_uint2(e4m3x4(bf_lo(v.x) * f, bf_hi(v.x) * f, bf_lo(v.y) * f, bf_hi(v.y) * f),
@@ -169,6 +158,10 @@ __device__ __forceinline__ uint2 mx_quant8(uint4 v, float f, bool fast) {
                       (e4m3(bf_hi(v.w) * f) << 24);
   return make_uint2(lo, hi);
 }
+
+// q = e4m3fn(x / s): s is a power of two, so x * (1 / s) is the same exact scaling
+__device__ __forceinline__ uint2 quant8(uint4 v, float s, bool fast) { return mx_quant8(v, 1.0f / s, fast); }
+
 
 // One wave per row of x [rows, K] (K % 8 == 0). With CPL > 0 the row (up to
 // 64 * CPL 16-byte chunks) stays in registers between the amax and the
@@ -332,20 +325,19 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
         e = mx_exponent(am);
         f = mx_multiplier(e);
       } else {
-        f = s_col[cc];
+        f = 1.0f / s_col[cc];  // s is a power of two: x * f is x / s exactly
       }
       uint32_t o[4];
       if (fast) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          o[q] = MX ? e4m3x4(xv[4 * q] * f, xv[4 * q + 1] * f, xv[4 * q + 2] * f, xv[4 * q + 3] * f)
-                    : e4m3x4(xv[4 * q] / f, xv[4 * q + 1] / f, xv[4 * q + 2] / f, xv[4 * q + 3] / f);
+          o[q] = e4m3x4(xv[4 * q] * f, xv[4 * q + 1] * f, xv[4 * q + 2] * f, xv[4 * q + 3] * f);
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           o[q] = 0;
 #pragma unroll
-          for (int bq = 0; bq < 4; ++bq) o[q] |= (MX ? e4m3(xv[4 * q + bq] * f) : e4m3(xv[4 * q + bq] / f)) << (8 * bq);
+          for (int bq = 0; bq < 4; ++bq) o[q] |= e4m3(xv[4 * q + bq] * f) << (8 * bq);
         }
       }
       if (rb < n_out) {
