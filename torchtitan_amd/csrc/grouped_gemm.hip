@@ -190,6 +190,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
   constexpr int CHP = BM / 8, CHQ = BN / 8;          // 16-byte chunks per k-row (k-major tiles)
   static_assert(BM % 64 == 0 && BN % 64 == 0 && CPW <= 30, "tile");
   static_assert(TN % 2 == 0 && (MODE != kFwdGateUp || TN % 4 == 0), "epilogue block pairs");
+  // kswz flips chunk bits 1-3: a k-major row must hold whole groups of 16 chunks
+  static_assert((!T::kPT || BM % 128 == 0) && (!T::kQT || BN % 128 == 0), "k-major tile rows");
   __shared__ __attribute__((aligned(1024))) uint16_t sP[NS][BM * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sQ[NS][BN * BK];
   __shared__ int s_seg[kGemmMaxE + 1];
