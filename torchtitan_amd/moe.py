@@ -165,7 +165,7 @@ class _GateF32(torch.autograd.Function):
         d3 = _bf16_terms(grad.float().contiguous())
         dx = dw = db = None
         if ctx.needs_input_grad[0]:
-            dx = torch.mm(d3, torch.cat([w, w, w], dim=0), out_dtype=torch.float32).to(x.dtype)
+            dx = torch.mm(d3, torch.cat([w, w, w], dim=0))  # fp32 accumulation, one rounding to bf16
         if ctx.needs_input_grad[1]:
             e = w.shape[0]
             dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
