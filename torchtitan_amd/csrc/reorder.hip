@@ -179,6 +179,8 @@ __global__ __launch_bounds__(256) void scatter_kernel(ScatterParams p) {
 // 16-byte chunks (8 bf16 or 4 fp32); arithmetic is fp32 and results are
 // rounded to the row type once, as torch's elementwise ops on that dtype do.
 // ---------------------------------------------------------------------------
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 template <typename T> struct Chunk;
 template <> struct Chunk<uint16_t> {
   static constexpr int kN = 8;
@@ -228,7 +230,7 @@ __device__ __forceinline__ float dot_chunk(uint4 a, uint4 b) {
 // out[slot_pos[t,k]] = src[t] (* scores_sorted[slot_pos[t,k]]), all k < K.
 // Used for the permute (moe.py:445-451) and for the backward gather of the
 // combine (scatter_add.py:28-33), which is the same movement unscaled.
-template <typename T>
+template <typename T, bool STREAM>
 __global__ __launch_bounds__(256) void expand_rows_kernel(const T* __restrict__ src, int64_t n_tokens,
                                                           int D, int K,
                                                           const int32_t* __restrict__ slot_pos,
@@ -245,7 +247,10 @@ __global__ __launch_bounds__(256) void expand_rows_kernel(const T* __restrict__ 
     for (int j = 0; j < K; ++j) {
       const int64_t pos = slot_pos[t * K + j];
       const uint4 w = scores_sorted ? scale_chunk<T>(v, scores_sorted[pos]) : v;
-      *(uint4*)(out + pos * D + ch * n) = w;
+      if constexpr (STREAM)
+        __builtin_nontemporal_store(u32x4_t{w.x, w.y, w.z, w.w}, (u32x4_t*)(out + pos * D + ch * n));
+      else
+        *(uint4*)(out + pos * D + ch * n) = w;
     }
   }
 }
@@ -480,11 +485,20 @@ static int check_row_args(int64_t n_tokens, int32_t dim, int32_t top_k, int32_t 
   return kErrInvalidArgument;
 }
 
+// stream: nontemporal stores, for the permute, whose rows the next kernel reads
+// from HBM anyway (measured 0.146 -> 0.123 ms at the Kimi shape); the combine
+// backward keeps ordinary stores (its output is read back at once: 0.118 -> 0.133
+// ms with streamed stores)
 template <typename T>
 static void launch_expand(const void* src, int64_t n_tokens, int dim, int top_k, const int32_t* slot_pos,
-                          const float* scores, void* out, hipStream_t stream) {
-  hipLaunchKernelGGL(expand_rows_kernel<T>, dim3(stream_grid(n_tokens * (dim / Chunk<T>::kN))), dim3(256), 0,
-                     stream, (const T*)src, n_tokens, dim, top_k, slot_pos, scores, (T*)out);
+                          const float* scores, void* out, bool stream_stores, hipStream_t stream) {
+  const dim3 grid(stream_grid(n_tokens * (dim / Chunk<T>::kN)));
+  if (stream_stores)
+    hipLaunchKernelGGL((expand_rows_kernel<T, true>), grid, dim3(256), 0, stream, (const T*)src, n_tokens, dim,
+                       top_k, slot_pos, scores, (T*)out);
+  else
+    hipLaunchKernelGGL((expand_rows_kernel<T, false>), grid, dim3(256), 0, stream, (const T*)src, n_tokens, dim,
+                       top_k, slot_pos, scores, (T*)out);
 }
 
 template <typename T>
@@ -527,9 +541,9 @@ MOE_API int moe_permute(const void* x, const int32_t* slot_pos, const float* sco
   if (n_tokens == 0) return kOk;
   if (!x || !slot_pos || !routed_input) return kErrInvalidArgument;
   if (dtype == MOE_DTYPE_BF16)
-    launch_expand<uint16_t>(x, n_tokens, dim, top_k, slot_pos, scores_sorted, routed_input, stream);
+    launch_expand<uint16_t>(x, n_tokens, dim, top_k, slot_pos, scores_sorted, routed_input, true, stream);
   else
-    launch_expand<float>(x, n_tokens, dim, top_k, slot_pos, scores_sorted, routed_input, stream);
+    launch_expand<float>(x, n_tokens, dim, top_k, slot_pos, scores_sorted, routed_input, true, stream);
   return launch_status();
 }
 
@@ -588,9 +602,9 @@ MOE_API int moe_combine_bwd(const void* grad_out, const void* routed_output, con
   } else {
     if (!slot_pos) return kErrInvalidArgument;
     if (dtype == MOE_DTYPE_BF16)
-      launch_expand<uint16_t>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, stream);
+      launch_expand<uint16_t>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, false, stream);
     else
-      launch_expand<float>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, stream);
+      launch_expand<float>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, false, stream);
   }
   return launch_status();
 }
