@@ -26,8 +26,12 @@ import os
 import statistics
 import sys
 import time
+from types import SimpleNamespace
 
 import torch
+
+# one GPU: no pipeline, context or expert parallelism
+_NO_PARALLEL = SimpleNamespace(pp_enabled=False, cp_enabled=False, ep_enabled=False)
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -189,11 +193,13 @@ def make_layer(w: dict, device: torch.device, seed: int):
     if w.get("fp8"):
         from torchtitan_amd.quantization import Float8GroupedMMConverter
 
-        Float8GroupedMMConverter.Config(fqns=["experts"]).build().convert(moe)
+        Float8GroupedMMConverter.Config(fqns=["experts"]).build(
+            parallel_dims=_NO_PARALLEL, model_compile_enabled=False).convert(moe)
     if w.get("mxfp8"):
         from torchtitan_amd.quantization import MXFP8Converter
 
-        MXFP8Converter.Config(fqns=["experts"]).build().convert(moe)
+        MXFP8Converter.Config(fqns=["experts"]).build(
+            parallel_dims=_NO_PARALLEL, model_compile_enabled=False).convert(moe)
     return moe
 
 

@@ -12,6 +12,9 @@
  * Shape symbols: N tokens, D model dim, E routed experts, K top-k, H expert
  * hidden dim, R = N*K routed rows.
  *
+ * Routing limits taken together (router, histogram and reorder): E <= 512,
+ * K <= 32. The grouped GEMMs take E <= 1024.
+ *
  * Reference citations are to QIU023/torchtitan (file:line).
  */
 #ifndef MOE_MI355X_H
@@ -45,7 +48,8 @@ typedef struct ihipStream_t* moe_stream_t; /* == hipStream_t */
  * Replaces TokenChoiceTopKRouter.forward, torchtitan/models/common/moe.py:211-266
  * (with _get_node_limited_routing_scores :169-209 and
  * _debug_force_load_balance_routing :152-167). The gate itself (moe.py:231-232)
- * stays torch's fp32 GEMM.
+ * is not here: the caller passes fp32 logits (the reference's fp32 GEMM under
+ * autocast by default).
  * logits [N,E] fp32, expert_bias [E] fp32 or NULL -> scores [N,E] fp32 (saved
  * for backward), top_scores [N,K] fp32, selected_experts [N,K] int64.
  * n_expert_groups <= 0 disables group limiting. E <= 512, K <= 64. */

@@ -581,8 +581,10 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: d
 # ---------------------------------------------------------------------------
 # fp8 e4m3 grouped GEMMs (parity unpinned against torchao: the reference delegates
 # to torchao's Float8TrainingOpConfig, torchtitan/components/quantization/float8.py:260-288,
-# which is absent; this restates its rowwise recipe with power-of-two scales, pinned
-# by hand-worked scales and an independent e4m3 encoder in tests/test_oracle.py)
+# which is absent; this restates its rowwise recipe with power-of-two scales. The
+# scale and cast are pinned by hand-worked scales and an independent e4m3 encoder,
+# the expert GEMMs by e4m3-grid operands whose products must be exact, with
+# planted scale-axis mistakes that those pins catch, in tests/test_oracle.py)
 # ---------------------------------------------------------------------------
 
 FP8_MAX = 448.0  # largest finite float8_e4m3fn

@@ -5,11 +5,14 @@ with device-generated parameters, run it and the reference op sequence
 from __future__ import annotations
 
 from dataclasses import dataclass
+from types import SimpleNamespace
 
 import torch
 
 from oracle import moe_ref as R
-from torchtitan_amd.moe import gate_logits_f32
+
+# one GPU: no pipeline, context or expert parallelism
+_NO_PARALLEL = SimpleNamespace(pp_enabled=False, cp_enabled=False, ep_enabled=False)
 
 
 @dataclass
@@ -75,11 +78,13 @@ def build_layer(sh: LayerShape, dev: torch.device, seed: int):
     if sh.fp8:
         from torchtitan_amd.quantization import Float8GroupedMMConverter
 
-        Float8GroupedMMConverter.Config(fqns=["experts"]).build().convert(moe)
+        Float8GroupedMMConverter.Config(fqns=["experts"]).build(
+            parallel_dims=_NO_PARALLEL, model_compile_enabled=False).convert(moe)
     if sh.mxfp8:
         from torchtitan_amd.quantization import MXFP8Converter
 
-        MXFP8Converter.Config(fqns=["experts"]).build().convert(moe)
+        MXFP8Converter.Config(fqns=["experts"]).build(
+            parallel_dims=_NO_PARALLEL, model_compile_enabled=False).convert(moe)
     x = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
     g = torch.randn(sh.bs, sh.slen, d, generator=gen, device=dev).bfloat16()
     return moe, x, g
@@ -91,10 +96,9 @@ def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
 
 
 def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape) -> dict:
-    """Runs both sides forward + backward and returns {name: (rel_err, bit_identical)};
-    asserts that routing (indices, counts, top scores) is bit-exact on the same
-    gate logits, and that those logits are the fp32 gate GEMM's to fp32
-    summation order."""
+    """Runs both sides forward + backward from the same x and returns
+    {name: (rel_err, bit_identical)}; asserts that routing (indices, counts, top
+    scores) is bit-exact, each side running its own fp32 gate."""
     d = sh.dim
     xa = x.clone().requires_grad_(True)
     out = moe(xa)
@@ -118,19 +122,21 @@ def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape
     mc = R.MoECfg(router=rc, dim=d, hidden_dim=sh.hidden, score_before_experts=sh.score_before,
                   use_grouped_mm=True, has_shared=bool(sh.shared_hidden),
                   expert_kind="gptoss" if sh.gptoss else "swiglu", swiglu_limit=sh.swiglu_limit)
-    # the layer's gate logits agree with the fp32 autocast GEMM to fp32 summation
-    # order (checked inside the oracle); both sides route on these values
+    # each side computes its own gate logits from the same x: the layer with the
+    # reference's fp32 autocast call (its default), the oracle with the same call
+    # written out; routing must then agree bit for bit
     x2 = x.view(-1, d)
-    with torch.no_grad():
-        logits = gate_logits_f32(x2, moe.router.gate)
     xb = x.clone().requires_grad_(True)
     aux = {}
-    ref = R.moe_forward_reference_ops(params, xb, mc, aux=aux, logit_values=logits)
+    ref = R.moe_forward_reference_ops(params, xb, mc, aux=aux)
     ref.backward(g)
 
     with torch.no_grad():
         top, idx, counts = moe.router(x2, moe.expert_bias)
-        t_top, t_idx, t_counts, _ = R.router_forward_torch(logits, params["expert_bias"], rc)
+        with torch.autocast(device_type=x2.device.type, dtype=torch.float32):
+            ref_logits = torch.nn.functional.linear(x2, params["gate"].detach(),
+                                                    params["gate_bias"].detach() if "gate_bias" in params else None)
+        t_top, t_idx, t_counts, _ = R.router_forward_torch(ref_logits, params["expert_bias"], rc)
     assert torch.equal(idx, t_idx), "selected experts differ from the reference op sequence"
     assert torch.equal(counts, t_counts), "tokens per expert differ"
     assert torch.equal(top, t_top), "top scores differ"

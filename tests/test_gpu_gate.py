@@ -1,8 +1,9 @@
 """Router gate logits in fp32 (torchtitan/models/common/moe.py:230-232) on the GPU.
 
-For bf16 x and W the layer computes the gate on bf16 GEMMs with fp32
-accumulation (moe._GateF32) instead of the fp32 GEMM under autocast. Both are
-checked against the fp64 product of the same values:
+The layer's default gate is the reference's own call (the fp32 GEMM under
+autocast), which the tests below check it is, bit for bit. The opt-in gate
+(``bf16_mfma=True``: bf16 GEMMs with fp32 accumulation, moe._GateF32) and the
+fp32 path are both checked against the fp64 product of the same values:
   * logits: the error of the bf16-GEMM path is at most 2x the fp32 path's
     (plus 1e-6 of the largest logit): both are fp32 sums of the same exact
     products, in different orders;
@@ -13,7 +14,10 @@ checked against the fp64 product of the same values:
     terms both are many ulps off) or one ulp;
   * bias gradient: the fp32 column sum of the logit gradient.
 The upstream gradient spans six decades, so the second and third bf16 terms of
-its split carry weight.
+its split carry weight. The opt-in gate's logits are the fp32 GEMM's to
+summation order only, so a token whose K-th and (K+1)-th biased scores nearly
+tie can get another expert set: test_opt_in_gate_routing_disagreement counts
+how often at the Kimi-Linear layer shapes.
 """
 
 import pytest
@@ -58,7 +62,7 @@ def test_gate_logits_f32_vs_fp64(case):
         xs = x.clone().requires_grad_(True)
         gate.zero_grad(set_to_none=True)
         if fast:
-            y = gate_logits_f32(xs, gate)
+            y = gate_logits_f32(xs, gate, bf16_mfma=True)
         else:
             with torch.autocast(device_type="cuda", dtype=torch.float32):
                 y = gate(xs)
@@ -103,17 +107,61 @@ def test_gate_logits_f32_vs_fp64(case):
 
 
 def test_gate_logits_fallback_paths():
-    """fp32 weights, or an outer autocast, keep the reference's autocast region."""
+    """The default gate is the reference's autocast region for bf16 weights; fp32
+    weights, or an outer autocast, keep it also when the opt-in is asked for."""
     dev = torch.device("cuda:0")
     gate = Linear(Linear.Config(in_features=256, out_features=16)).to(dev)
     x = torch.randn(64, 256, device=dev).bfloat16()
-    y = gate_logits_f32(x, gate)  # fp32 weight
+    gb = Linear(Linear.Config(in_features=256, out_features=16)).to(dev)
+    gb.weight.data = gb.weight.data.bfloat16()
+    with torch.autocast(device_type="cuda", dtype=torch.float32):
+        ref0 = gb(x)
+    assert torch.equal(gate_logits_f32(x, gb), ref0)  # default: the reference's call
+    y = gate_logits_f32(x, gate, bf16_mfma=True)  # fp32 weight
     with torch.autocast(device_type="cuda", dtype=torch.float32):
         ref = gate(x)
     assert torch.equal(y, ref)
     gate.weight.data = gate.weight.data.bfloat16()
     with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
-        y2 = gate_logits_f32(x, gate)
+        y2 = gate_logits_f32(x, gate, bf16_mfma=True)
     with torch.autocast(device_type="cuda", dtype=torch.float32):
         ref2 = F.linear(x, gate.weight)
     assert y2.dtype == torch.float32 and torch.equal(y2, ref2)
+
+
+@pytest.mark.parametrize("n_tokens,zipf", [(16384, False), (32768, True)])
+def test_opt_in_gate_routing_disagreement(n_tokens, zipf):
+    """How often the opt-in bf16-MFMA gate routes a token to another expert set
+    than the reference's fp32 autocast gate, at the Kimi-Linear layer shape (dim
+    2304, 256 experts, top-8 sigmoid + expert bias), over three seeds. The
+    default gate is the reference's call and never disagrees; the rate of the
+    opt-in one is printed and bounded at 1e-3 of the tokens."""
+    from oracle import moe_ref as R
+
+    dev = torch.device("cuda:0")
+    d, e, k = 2304, 256, 8
+    rc = R.RouterCfg(num_experts=e, top_k=k, score_func="sigmoid", route_norm=True, route_scale=2.5)
+    total, differ = 0, 0
+    for seed in (1, 2, 3):
+        banner(f"opt-in gate routing n={n_tokens} zipf={zipf} seed={seed}")
+        g = torch.Generator(device=dev).manual_seed(seed)
+        gate = Linear(Linear.Config(in_features=d, out_features=e)).to(dev)
+        gate.weight.data = (torch.randn(e, d, generator=g, device=dev) * 0.02).bfloat16()
+        bias = (torch.rand(e, generator=g, device=dev) * 2 - 1) * 0.01
+        if zipf:
+            ranks = torch.randperm(e, generator=g, device=dev).float() + 1.0
+            bias = bias + 0.25 * ranks.pow(-1.2) - 1.0 * (ranks > e - 20).float()
+        x = torch.randn(n_tokens, d, generator=g, device=dev).bfloat16()
+        with torch.no_grad():
+            ref = gate_logits_f32(x, gate)
+            fast = gate_logits_f32(x, gate, bf16_mfma=True)
+            _, i_ref, _, _ = R.router_forward_torch(ref, bias, rc)
+            _, i_fast, _, _ = R.router_forward_torch(fast, bias, rc)
+        s_ref = torch.sort(i_ref, dim=1).values
+        s_fast = torch.sort(i_fast, dim=1).values
+        differ += int((s_ref != s_fast).any(dim=1).sum())
+        total += n_tokens
+    rate = differ / total
+    print(f"[case] opt-in gate: {differ} of {total} tokens routed to another expert set ({rate:.2e})",
+          flush=True)
+    assert rate <= 1e-3

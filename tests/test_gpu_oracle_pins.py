@@ -14,7 +14,6 @@ import torch
 
 from oracle import moe_ref as R
 from tests.conftest import banner
-from torchtitan_amd.moe import gate_logits_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -152,20 +151,21 @@ def test_layer_matches_reference_op_sequence_on_device(dev, name):
                      num_limited_groups=groups[1] if groups else None)
     mc = R.MoECfg(router=rc, dim=d, hidden_dim=h, score_before_experts=sb, use_grouped_mm=True,
                   has_shared=bool(hs))
+    # each side runs its own fp32 gate on the same x (the layer: the reference's
+    # autocast call, its default); routing must agree bit for bit
     x2 = x.view(-1, d)
-    with torch.no_grad():
-        logits = gate_logits_f32(x2, moe.router.gate)  # fp32-order-close to the autocast GEMM
     xb = x.clone().requires_grad_(True)
     try:
-        ref = R.moe_forward_reference_ops(params, xb, mc, logit_values=logits)
+        ref = R.moe_forward_reference_ops(params, xb, mc)
     except RuntimeError as err:  # torch._grouped_mm unavailable for this device
         pytest.skip(f"torch._grouped_mm on this device: {err}")
     ref.backward(gout)
 
-    # routing on the same logits: identical selection, counts and permutation
     with torch.no_grad():
         top, idx, counts = moe.router(x2, moe.expert_bias)
-        t_top, t_idx, t_counts, _ = R.router_forward_torch(logits, params["expert_bias"], rc)
+        with torch.autocast(device_type="cuda", dtype=torch.float32):
+            ref_logits = torch.nn.functional.linear(x2, params["gate"].detach())
+        t_top, t_idx, t_counts, _ = R.router_forward_torch(ref_logits, params["expert_bias"], rc)
     assert torch.equal(idx, t_idx)
     assert torch.equal(counts, t_counts)
     assert torch.equal(top, t_top)

@@ -131,33 +131,70 @@ def test_kimi_init():
     assert 0.01 < layer._moe.experts.w1.std().item() < 0.03
 
 
-def test_float8_converter_selects_experts_by_fqn():
-    from torchtitan_amd.quantization import Float8GroupedMMConverter, find_pad_multiple
+def _dims(pp=False, cp=False, ep=False):
+    return SimpleNamespace(pp_enabled=pp, cp_enabled=cp, ep_enabled=ep)
 
+
+def test_float8_converter_selects_experts_by_fqn(monkeypatch):
+    from torchtitan_amd import quantization as Q
+
+    monkeypatch.setattr(Q, "has_gfx950", lambda: True)
+    kw = {"parallel_dims": _dims(), "model_compile_enabled": False}
     model = torch.nn.ModuleDict({"a": _cfg(hs=0).build(), "b": _cfg(hs=0).build()})
-    conv_cfg = Float8GroupedMMConverter.Config(fqns=["a.experts"])
-    names = conv_cfg.build().convert(model)
+    conv_cfg = Q.Float8GroupedMMConverter.Config(fqns=["a.experts"])
+    names = conv_cfg.build(**kw).convert(model)
     assert names == ["a.experts"]
     assert model["a"].experts.float8 and not model["b"].experts.float8
     assert set(model["a"].state_dict()) == set(model["b"].state_dict())
-    assert find_pad_multiple([conv_cfg]) == 16 and find_pad_multiple([]) is None
-    assert Float8GroupedMMConverter.Config(fqns="experts").build().fqns == ["experts"]
+    assert Q.find_pad_multiple([conv_cfg]) == 16 and Q.find_pad_multiple([]) is None
+    assert Q.Float8GroupedMMConverter.Config(fqns="experts").build(**kw).fqns == ["experts"]
 
 
-def test_mxfp8_converter_selects_experts_by_fqn():
-    from torchtitan_amd.quantization import MXFP8Converter, find_pad_multiple
+def test_float8_converter_guards_follow_reference():
+    """float8.py:238-256: hardware check (ValueError), then no PP and no CP
+    (AssertionError with the reference's messages)."""
+    from torchtitan_amd import quantization as Q
 
+    cfg = Q.Float8GroupedMMConverter.Config(fqns=["experts"])
+    if not Q.has_gfx950():
+        with pytest.raises(ValueError, match="only supported on gfx950"):
+            cfg.build(parallel_dims=_dims(), model_compile_enabled=True)
+    with pytest.raises(TypeError):
+        cfg.build()  # parallel_dims and model_compile_enabled are required, as in the reference
+
+
+def test_float8_converter_rejects_pp_and_cp(monkeypatch):
+    from torchtitan_amd import quantization as Q
+
+    monkeypatch.setattr(Q, "has_gfx950", lambda: True)
+    cfg = Q.Float8GroupedMMConverter.Config(fqns=["experts"])
+    with pytest.raises(AssertionError, match="pipeline parallelism"):
+        cfg.build(parallel_dims=_dims(pp=True), model_compile_enabled=True)
+    with pytest.raises(AssertionError, match="context parallelism"):
+        cfg.build(parallel_dims=_dims(cp=True), model_compile_enabled=True)
+
+
+def test_mxfp8_converter_selects_experts_by_fqn(monkeypatch):
+    from torchtitan_amd import quantization as Q
+
+    monkeypatch.setattr(Q, "has_gfx950", lambda: True)
+    kw = {"parallel_dims": _dims(), "model_compile_enabled": True}
     model = torch.nn.ModuleDict({"a": _cfg(hs=0).build(), "b": _cfg(hs=0).build()})
-    conv_cfg = MXFP8Converter.Config(fqns="b.experts")
-    conv = conv_cfg.build()
-    assert conv.recipe_name == "mxfp8_rceil"
+    conv_cfg = Q.MXFP8Converter.Config(fqns="b.experts")
+    conv = conv_cfg.build(**kw)
+    assert conv.recipe_name == "mxfp8_rceil" and conv.pad_token_groups_for_grouped_mm
+    assert not Q.MXFP8Converter.Config(fqns="b.experts").build(
+        parallel_dims=_dims(ep=True), model_compile_enabled=True).pad_token_groups_for_grouped_mm
     assert conv.convert(model) == ["b.experts"]
     assert model["b"].experts.mxfp8 and not model["a"].experts.mxfp8
     assert not model["b"].experts.float8
     assert set(model["a"].state_dict()) == set(model["b"].state_dict())
-    assert find_pad_multiple([conv_cfg]) == 32
+    assert Q.find_pad_multiple([conv_cfg]) == 32
     with pytest.raises(ValueError):
-        MXFP8Converter.Config(recipe_name="mxfp8_floor").build()
+        Q.MXFP8Converter.Config(recipe_name="mxfp8_floor").build(**kw)
+    monkeypatch.setattr(Q, "has_gfx950", lambda: False)
+    with pytest.raises(AssertionError, match="only supported on gfx950"):
+        conv_cfg.build(**kw)
 
 
 def test_load_balancing_hook_registration_follows_reference_rules():

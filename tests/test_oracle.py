@@ -22,7 +22,13 @@ What fixes each function, independently of the formula being checked:
     exponent (biased exponent of amax / 448, +1 for a non-zero mantissa),
     hand-worked blocks, values on the e4m3 grid that must round-trip exactly,
     power-of-two equivariance, the e4m3 rounding bound, and exact GEMMs of
-    grid values whose blocks carry different scales.
+    grid values whose blocks carry different scales;
+  * experts_fp8_forward / experts_fp8_backward: operands on the e4m3 grid with
+    power-of-two scales along the recipe's axes, where every GEMM must equal
+    the fp64 product rounded once (the SwiGLU gradient from torch's autograd),
+    two planted mistakes (weights scaled along the contraction; transposed
+    operands scaled along the other axis) that these pins must catch, and a
+    bound of 0.1 against an fp64 autograd reference.
 The GPU-lowering rules the oracle states (top-k tie order, deterministic
 scatter-add order, index-backward rounding, short-row sum order) are pinned
 against torch on the device in tests/test_gpu_oracle_pins.py.
@@ -759,3 +765,199 @@ def test_quant_fp8_rows_rounding_bound():
     half_spacing = torch.exp2(torch.floor(torch.log2(a)) - 4)
     assert torch.all((back - y).abs() <= half_spacing)
     assert torch.all(y.abs().amax(dim=1) > 224.0) and torch.all(y.abs().amax(dim=1) <= 448.0)
+
+
+# ---------------------------------------------------------------------------
+# fp8 expert emulation (experts_fp8_forward / experts_fp8_backward): each GEMM is
+# pinned by operands on the e4m3 grid carrying power-of-two scales along the
+# axis the recipe scales (per token row, per expert output column, per column
+# over a group's tokens for dW): quantization is then exact and every GEMM must
+# equal the fp64 product rounded once. A scale taken along the contraction
+# breaks that, which the planted-mistake tests check.
+# ---------------------------------------------------------------------------
+
+
+def _grid_rows(rows: int, cols: int, g: torch.Generator, kmin: int = -5, kmax: int = 5) -> torch.Tensor:
+    """[rows, cols] bf16: e4m3 grid values with random signs, one +-448 per row,
+    each row times its own power of two 2^k, k in [kmin, kmax]."""
+    grid = _e4m3_grid()
+    v = grid[torch.randint(0, len(grid), (rows, cols), generator=g)]
+    v = v * torch.where(torch.rand(rows, cols, generator=g) < 0.5, -1.0, 1.0)
+    v[torch.arange(rows), torch.randint(0, cols, (rows,), generator=g)] = 448.0
+    k = torch.randint(kmin, kmax + 1, (rows, 1), generator=g).float()
+    return (v * torch.exp2(k)).bfloat16()
+
+
+def _both_ways_exact(rows: int, cols: int, g: torch.Generator) -> torch.Tensor:
+    """[rows, cols] bf16 grid values with a 448 in every row and every column, so
+    that quantizing along either axis has scale 1 and is exact."""
+    v = _grid_rows(rows, cols, g, 0, 0).float()
+    v[torch.randint(0, rows, (cols,), generator=g), torch.arange(cols)] = -448.0
+    return v.bfloat16()
+
+
+def _bf16_mm64(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a @ b in fp64, rounded to fp32 and then bf16 (the emulation's rounding)."""
+    return (a.double() @ b.double()).float().bfloat16()
+
+
+def _deq(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    return q.double() * s.double()
+
+
+def _fp8_forward_mismatches(e, d, h, counts, seed) -> int:
+    """Runs experts_fp8_forward on grid operands (x scaled per token row, w1 / w3
+    per (expert, hidden row) over D, w2 per (expert, dim row) over H) and counts
+    elements of g, u, y that differ from the fp64 products: g, u of the inputs
+    themselves, y of h dequantized by the pinned row quantizer."""
+    g = torch.Generator().manual_seed(seed)
+    r = sum(counts)
+    x = _grid_rows(r, d, g)
+    w1 = torch.stack([_grid_rows(h, d, g) for _ in range(e)])
+    w3 = torch.stack([_grid_rows(h, d, g) for _ in range(e)])
+    w2 = torch.stack([_grid_rows(d, h, g) for _ in range(e)])
+    y, gg, uu, hh = R.experts_fp8_forward(w1, w2, w3, x, torch.tensor(counts))
+    qh, sh = R.quant_fp8_rows(hh)
+    hd = _deq(qh, sh)
+    bad, s0 = 0, 0
+    for i, c in enumerate(counts):
+        sl = slice(s0, s0 + c)
+        bad += int((gg[sl] != _bf16_mm64(x[sl], w1[i].t())).sum())
+        bad += int((uu[sl] != _bf16_mm64(x[sl], w3[i].t())).sum())
+        bad += int((y[sl] != _bf16_mm64(hd[sl], w2[i].t())).sum())
+        s0 += c
+    assert torch.equal(hh, F.silu(gg) * uu)
+    return bad
+
+
+def _fp8_backward_mismatches(e, d, h, counts, seed) -> dict:
+    """Runs experts_fp8_backward twice on grid operands and counts mismatches
+    against fp64 products, with the SwiGLU gradient from torch's autograd:
+      dx: dy per token row, w2 per (expert, hidden row) over D, w1 / w3 per
+          (expert, dim column) over H; dg, du dequantized per token row;
+      dW: dy exact both ways (scale 1), x and h per column over each expert's
+          tokens; dg, du dequantized per column over the tokens."""
+    g = torch.Generator().manual_seed(seed)
+    r = sum(counts)
+    cnt = torch.tensor(counts)
+    bad = {"dx": 0, "dw1": 0, "dw2": 0, "dw3": 0}
+
+    def swiglu_grads(gs, us, dh):
+        gq, uq = gs.clone().requires_grad_(True), us.clone().requires_grad_(True)
+        (F.silu(gq) * uq).backward(dh)
+        return gq.grad, uq.grad
+
+    # --- dx ---
+    dy = _grid_rows(r, d, g)
+    w2 = torch.stack([_grid_rows(h, d, g).t() for _ in range(e)])  # [E, D, H], rows of w2^T on the grid
+    w1 = torch.stack([_grid_rows(d, h, g).t() for _ in range(e)])  # [E, H, D], rows of w1^T on the grid
+    w3 = torch.stack([_grid_rows(d, h, g).t() for _ in range(e)])
+    gs = torch.randn(r, h, generator=g).bfloat16()
+    us = torch.randn(r, h, generator=g).bfloat16()
+    hs = F.silu(gs) * us
+    x = torch.randn(r, d, generator=g).bfloat16()
+    dx, *_ = R.experts_fp8_backward(w1, w2, w3, x, cnt, gs, us, hs, dy)
+    s0 = 0
+    dgs, dus = [], []
+    for i, c in enumerate(counts):
+        sl = slice(s0, s0 + c)
+        dg, du = swiglu_grads(gs[sl], us[sl], _bf16_mm64(dy[sl], w2[i]))
+        dgs.append(dg)
+        dus.append(du)
+        s0 += c
+    dg, du = torch.cat(dgs), torch.cat(dus)
+    dgd, dud = _deq(*R.quant_fp8_rows(dg)), _deq(*R.quant_fp8_rows(du))
+    s0 = 0
+    for i, c in enumerate(counts):
+        sl = slice(s0, s0 + c)
+        want = _bf16_mm64(dgd[sl], w1[i]) + _bf16_mm64(dud[sl], w3[i])
+        bad["dx"] += int((dx[sl] != want).sum())
+        s0 += c
+
+    # --- dW ---
+    segs = [c for c in counts if c]
+    dy = torch.cat([_both_ways_exact(c, d, g) for c in segs]) if segs else torch.zeros(0, d).bfloat16()
+    x = torch.cat([_grid_rows(d, c, g).t() for c in segs]) if segs else torch.zeros(0, d).bfloat16()
+    hs = torch.cat([_grid_rows(h, c, g).t() for c in segs]) if segs else torch.zeros(0, h).bfloat16()
+    gs = torch.randn(r, h, generator=g).bfloat16()
+    us = torch.randn(r, h, generator=g).bfloat16()
+    w2 = torch.stack([_grid_rows(h, d, g).t() for _ in range(e)])
+    w1 = torch.randn(e, h, d, generator=g).bfloat16()
+    w3 = torch.randn(e, h, d, generator=g).bfloat16()
+    _, dw1, dw2, dw3 = R.experts_fp8_backward(w1, w2, w3, x, cnt, gs, us, hs, dy)
+    s0 = 0
+    for i, c in enumerate(counts):
+        sl = slice(s0, s0 + c)
+        if c == 0:
+            for name, t in (("dw1", dw1), ("dw2", dw2), ("dw3", dw3)):
+                bad[name] += int(torch.count_nonzero(t[i]))
+            continue
+        dg, du = swiglu_grads(gs[sl], us[sl], _bf16_mm64(dy[sl], w2[i]))
+        dgc = _deq(*R.quant_fp8_rows(dg.t()))  # [H, c]: one scale per hidden column over the tokens
+        duc = _deq(*R.quant_fp8_rows(du.t()))
+        bad["dw1"] += int((dw1[i] != _bf16_mm64(dgc, x[sl])).sum())
+        bad["dw3"] += int((dw3[i] != _bf16_mm64(duc, x[sl])).sum())
+        bad["dw2"] += int((dw2[i] != _bf16_mm64(dy[sl].t(), hs[sl])).sum())
+        s0 += c
+    return bad
+
+
+def test_fp8_forward_exact_on_grid_operands():
+    assert _fp8_forward_mismatches(3, 64, 96, [20, 0, 45], seed=11) == 0
+
+
+def test_fp8_backward_exact_on_grid_operands():
+    bad = _fp8_backward_mismatches(3, 64, 96, [20, 0, 45], seed=12)
+    assert bad == {"dx": 0, "dw1": 0, "dw2": 0, "dw3": 0}, bad
+
+
+def test_fp8_pins_catch_weights_scaled_along_the_contraction(monkeypatch):
+    """Planted mistake: the expert weights scaled per (expert, contraction index)
+    instead of per output column. Square shapes let the wrong scales broadcast
+    silently; the grid pin must see the difference."""
+    assert _fp8_forward_mismatches(2, 64, 64, [64, 64], seed=13) == 0
+    orig = R.quant_fp8_rows
+    monkeypatch.setattr(R, "quant_fp8_rows", lambda t, dim=-1: orig(t, dim=-2 if t.dim() == 3 else dim))
+    assert _fp8_forward_mismatches(2, 64, 64, [64, 64], seed=13) > 0
+
+
+def test_fp8_pins_catch_transposed_operand_scales(monkeypatch):
+    """Planted mistake: every transposed operand of the backward (w1^T, w2^T, w3^T
+    and the dW operands) scaled along the other axis, i.e. along the
+    contraction. Both the dx and the dW pins must see it."""
+    assert _fp8_backward_mismatches(2, 64, 64, [64, 64], seed=14) == {"dx": 0, "dw1": 0, "dw2": 0, "dw3": 0}
+    orig = R.quant_fp8_rows
+    monkeypatch.setattr(R, "quant_fp8_rows",
+                        lambda t, dim=-1: orig(t, dim=0 if (t.dim() == 2 and not t.is_contiguous()) else dim))
+    bad = _fp8_backward_mismatches(2, 64, 64, [64, 64], seed=14)
+    assert bad["dx"] > 0 and bad["dw1"] > 0 and bad["dw2"] > 0 and bad["dw3"] > 0, bad
+
+
+def test_fp8_experts_close_to_float64_reference():
+    """Forward and backward of the fp8 emulation within 0.1 (normwise relative,
+    max |ours - ref| / max |ref|) of an fp64 autograd reference of the same
+    bf16 operands; empty experts get zero weight gradients."""
+    g = torch.Generator().manual_seed(15)
+    e, d, h, counts = 3, 64, 96, [20, 0, 45]
+    r = sum(counts)
+    x = torch.randn(r, d, generator=g).bfloat16()
+    w1, w3 = ((torch.randn(e, h, d, generator=g) * 0.1).bfloat16() for _ in range(2))
+    w2 = (torch.randn(e, d, h, generator=g) * 0.1).bfloat16()
+    dy = torch.randn(r, d, generator=g).bfloat16()
+    cnt = torch.tensor(counts)
+    y, g_, u_, h_ = R.experts_fp8_forward(w1, w2, w3, x, cnt)
+    dx, dw1, dw2, dw3 = R.experts_fp8_backward(w1, w2, w3, x, cnt, g_, u_, h_, dy)
+    xr, w1r, w2r, w3r = (t.double().requires_grad_(True) for t in (x, w1, w2, w3))
+    ys, s0 = [], 0
+    for i, c in enumerate(counts):
+        xe = xr[s0:s0 + c]
+        ys.append((F.silu(xe @ w1r[i].t()) * (xe @ w3r[i].t())) @ w2r[i].t())
+        s0 += c
+    yr = torch.cat(ys)
+    yr.backward(dy.double())
+
+    def rel(a, b):
+        return ((a.double() - b).abs().max() / b.abs().max()).item()
+    errs = [rel(y, yr.detach()), rel(dx, xr.grad), rel(dw1, w1r.grad), rel(dw2, w2r.grad), rel(dw3, w3r.grad)]
+    assert max(errs) < 0.1, errs
+    assert torch.count_nonzero(dw1[1]) == 0 and torch.count_nonzero(dw2[1]) == 0

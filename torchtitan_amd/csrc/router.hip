@@ -4,8 +4,8 @@
 // (the same lane/expert layout torch's persistent warp softmax uses on a
 // 64-wide wave), so scores, the group-limited mask, top-k selection, the
 // gather of un-biased scores, route_norm and route_scale all stay in
-// registers and per-wave LDS. The logits themselves come from torch's fp32
-// gate GEMM so that they are the reference's bits.
+// registers and per-wave LDS. The logits come from the caller: by default
+// torch's fp32 gate GEMM under autocast, the reference's own call.
 //
 // Follows torchtitan/models/common/moe.py:
 //   score function            :236-241

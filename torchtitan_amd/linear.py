@@ -1,9 +1,8 @@
 """``Linear``: nn.Linear with the Config protocol (torchtitan/models/common/linear.py:14-35).
 
-Used for the router gate (fp32 logits: moe.gate_logits_f32 runs bf16 weights on
-bf16 GEMMs with fp32 accumulation, which equals the reference's fp32 autocast GEMM
-up to summation order, and anything else through that autocast GEMM) and the
-shared expert's projections.
+Used for the router gate (fp32 logits: moe.gate_logits_f32 calls it under the
+reference's fp32 autocast; an opt-in variant runs bf16 weights on bf16 GEMMs with
+fp32 accumulation) and the shared expert's projections.
 """
 
 from __future__ import annotations

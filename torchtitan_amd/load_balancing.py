@@ -5,8 +5,9 @@ Mirrors register_moe_load_balancing_hook of
 torchtitan/components/optimizer.py:337-444. The per-layer update
 (``expert_bias += d - mean(d)``, ``d = coeff * sign(mean(t) - t)``,
 ``tokens_per_expert = 0``) runs as one HIP launch for every layer
-(``moe_expert_bias_update``). When a process group is given, the counts are
-summed across it first, as the reference does over its loss mesh.
+(``moe_expert_bias_update``). When a process group is given, each rank first
+floors its double-counted tokens (activation checkpointing) and the counts are
+then summed across the group, in the reference's order.
 """
 
 from __future__ import annotations
@@ -61,13 +62,16 @@ def update_expert_bias(model_parts: list[nn.Module], group=None) -> None:
             raise ValueError("every MoE layer needs fp32 tokens_per_expert and expert_bias of one size")
         if not (t.is_contiguous() and b.is_contiguous()):
             raise ValueError("tokens_per_expert and expert_bias must be contiguous")
+    halve = [_is_recomputation_enabled(block) for block, _ in blocks]
     if group is not None:
-        stacked = torch.stack(tpe)
+        # floor each rank's double-counted tokens before the sum, as the
+        # reference does (optimizer.py:389-394 before :400-414)
+        stacked = torch.stack([t // 2 if h else t for t, h in zip(tpe, halve)])
         torch.distributed.all_reduce(stacked, op=torch.distributed.ReduceOp.SUM, group=group)
         for t, row in zip(tpe, stacked):
             t.copy_(row)
-    bias_update(tpe, bias, [float(moe.load_balance_coeff) for _, moe in blocks],
-                [_is_recomputation_enabled(block) for block, _ in blocks])
+        halve = [False] * len(halve)
+    bias_update(tpe, bias, [float(moe.load_balance_coeff) for _, moe in blocks], halve)
 
 
 def bias_update(tokens_per_expert: list[torch.Tensor], expert_bias: list[torch.Tensor], coeffs: list[float],

@@ -19,6 +19,10 @@ from torch import Tensor
 from ._lib import call, lib, ptr, require_gpu, stream_of
 
 SCORE_FUNCS = {"softmax": 0, "sigmoid": 1}
+# Shape limits of the routing kernels taken together: the router takes E <= 512
+# and K <= 64, the histogram and reorder K <= 32 (and E <= 1024).
+MAX_EXPERTS = 512
+MAX_TOP_K = 32
 DTYPE_CODES = {torch.bfloat16: 0, torch.float32: 1}
 
 # Gradient of x[token_idx] accumulates a token's K rows with a rounding to the
