@@ -182,6 +182,39 @@ int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, const int64_
                              int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
                              uint16_t* dw2, moe_stream_t stream);
 
+/* ---- fp32 experts: _run_experts_for_loop in the input dtype --------------
+ * Replace the per-expert fp32 matmuls of torchtitan/models/common/moe.py:24-50
+ * (and their autograd) with one launch per GEMM over all experts: fp32
+ * operands, fp32 accumulation (v_mfma_f32_16x16x4f32), the SwiGLU of :41-43 in
+ * fp32. Same layouts as the bf16 entry points, fp32 elements; D, H multiples of
+ * 64, E <= 1024; rows past sum(counts) are not written. */
+
+/* g = x w1^T, u = x w3^T, h = silu(g) * u per expert segment (moe.py:41-42). */
+int moe_grouped_gemm_f32_gate_up(const float* x, const float* w1, const float* w3, const int64_t* counts,
+                                 int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden, float* g,
+                                 float* u, float* h, moe_stream_t stream);
+
+/* y = h w2^T per expert segment (moe.py:43). */
+int moe_grouped_gemm_f32_down(const float* h, const float* w2, const int64_t* counts, int64_t n_rows,
+                              int32_t n_experts, int32_t dim, int32_t hidden, float* y, moe_stream_t stream);
+
+/* Autograd of moe.py:41-43 through h: dh = dy w2; du = dh * silu(g);
+ * dg = (dh * u) * sigmoid(g) (1 + g (1 - sigmoid(g))). dg, du [R, H]. */
+int moe_grouped_gemm_f32_bwd_dgu(const float* dy, const float* w2, const float* g, const float* u,
+                                 const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                 int32_t hidden, float* dg, float* du, moe_stream_t stream);
+
+/* dx = dg w1 + du w3 per expert segment (autograd of moe.py:41-42). */
+int moe_grouped_gemm_f32_bwd_dx(const float* dg, const float* du, const float* w1, const float* w3,
+                                const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
+                                int32_t hidden, float* dx, moe_stream_t stream);
+
+/* Weight gradient out[e] = a_e^T b_e over expert e's rows: a [R, m], b [R, n]
+ * -> out [E, m, n] (dw1 = dg^T x, dw3 = du^T x, dw2 = dy^T h; zero for empty
+ * experts). m, n multiples of 64. */
+int moe_grouped_gemm_f32_bwd_dw(const float* a, const float* b, const int64_t* counts, int64_t n_rows,
+                                int32_t n_experts, int32_t m, int32_t n, float* out, moe_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * gpt-oss experts (torchtitan/models/gpt_oss/moe.py:43-52, 92-122, the
  * grouped-mm path): mlp1_weight [E, 2H, D] bf16 with the glu row 2j and the

@@ -522,6 +522,19 @@ __global__ __launch_bounds__(256) void mx_quant_tokens_t_kernel(const uint16_t* 
   int n = s_seg[2];
   if ((int64_t)seg0 + n > R) n = (int)(R - seg0 > 0 ? R - seg0 : 0);
   const int n_out = (n + kMxPad - 1) / kMxPad * kMxPad;
+  if (e == E - 1 && (int64_t)pstart + n_out <= Rpad) {
+    // The columns past the last group, up to Rpad, belong to no group: zero them
+    // (and their scale rows) so that every byte of q and s is defined. Both ends
+    // are multiples of 32, so the rows' tails take 16-byte stores.
+    const int64_t end = (int64_t)pstart + n_out;
+    const int64_t tail16 = (Rpad - end) / 16;
+    for (int64_t i = threadIdx.x; i < 64 * tail16; i += 256) {
+      const int64_t c = i / tail16, j = i - c * tail16;
+      *(uint4*)(q + (c0 + c) * Rpad + end + 16 * j) = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (threadIdx.x < 64)
+      for (int64_t br = end / kMxBlock; br < Rpad / kMxBlock; ++br) s[br * C + c0 + threadIdx.x] = 0;
+  }
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
   slab_t_quant<true, ROWS>(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
                            s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C, nullptr, s_tile,

@@ -60,15 +60,18 @@ def _run_experts_for_loop(
     mlp1_weight: torch.Tensor, mlp1_bias: torch.Tensor, mlp2_weight: torch.Tensor, mlp2_bias: torch.Tensor,
     swiglu_limit: float, x: torch.Tensor, num_tokens_per_expert: torch.Tensor, tp_degree: int = 1,
 ) -> torch.Tensor:
-    """moe.py:55-89 (per-expert matmuls on rows [0, sum(counts)), in x's dtype):
-    the same kernels on those rows, cast back to x's dtype."""
+    """moe.py:55-89: per-expert matmuls on rows [0, sum(counts)) in x's dtype,
+    returning those rows. bf16 runs the bf16 grouped kernels, whose rounding
+    points are those of the reference's bf16 matmuls and bias adds. The gpt-oss
+    epilogues have no fp32 kernels, so other dtypes raise instead of running in
+    a narrower one."""
     _check_tp(tp_degree)
+    if x.dtype != torch.bfloat16 or mlp1_weight.dtype != torch.bfloat16 or mlp2_weight.dtype != torch.bfloat16:
+        raise TypeError("the gpt-oss expert for-loop path runs in bfloat16 on MI355X; got "
+                        f"x {x.dtype}, mlp1_weight {mlp1_weight.dtype}, mlp2_weight {mlp2_weight.dtype}")
     total = int(num_tokens_per_expert.sum().item())
-    out = x.new_zeros(x.shape)
-    if total:
-        out[:total] = _run_experts_grouped_mm(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, swiglu_limit,
-                                              x[:total], num_tokens_per_expert).type_as(x)
-    return out
+    return _run_experts_grouped_mm(mlp1_weight, mlp1_bias, mlp2_weight, mlp2_bias, swiglu_limit,
+                                   x[:total], num_tokens_per_expert)
 
 
 class GptOssGroupedExperts(Module):

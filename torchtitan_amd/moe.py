@@ -47,14 +47,27 @@ def _run_experts_for_loop(
     w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor, x: torch.Tensor,
     num_tokens_per_expert: torch.Tensor,
 ) -> torch.Tensor:
-    """Reference readability path (moe.py:24-50): per-expert matmuls in the input
-    dtype with a host sync. On MI355X this runs the same grouped kernel as
-    _run_experts_grouped_mm on rows [0, sum(counts)) in bf16, then casts back."""
+    """Reference readability path (moe.py:24-50): the experts in the input dtype,
+    over the first sum(counts) rows, returning those rows.
+
+    fp32 inputs run the fp32 grouped kernels (fp32 products and sums, the SwiGLU
+    in fp32, as the reference's fp32 per-expert matmuls); bf16 inputs run the
+    bf16 grouped kernels, whose rounding points (each GEMM output, silu and the
+    product rounded to bf16) are those of the reference's bf16 matmuls. As in the
+    reference, reading sum(counts) synchronises with the host."""
     total = int(num_tokens_per_expert.sum().item())
-    out = x.new_zeros(x.shape)
-    if total:
-        out[:total] = _run_experts_grouped_mm(w1, w2, w3, x[:total], num_tokens_per_expert)
-    return out
+    xs = x[:total]
+    if x.dtype == torch.float32:
+        if not (w1.dtype == w2.dtype == w3.dtype == torch.float32):
+            raise TypeError(f"expected float32 expert weights for float32 x, got {w1.dtype}, {w2.dtype}, {w3.dtype}")
+        y, _, _, _ = ops.grouped_swiglu_f32(xs, w1, w2, w3, num_tokens_per_expert)
+        return y
+    if x.dtype == torch.bfloat16:
+        if not (w1.dtype == w2.dtype == w3.dtype == torch.bfloat16):
+            raise TypeError(f"expected bfloat16 expert weights for bfloat16 x, got {w1.dtype}, {w2.dtype}, {w3.dtype}")
+        y, _, _, _ = ops.grouped_swiglu(xs, w1, w2, w3, num_tokens_per_expert)
+        return y
+    raise TypeError(f"the MI355X experts run in float32 or bfloat16, got {x.dtype}")
 
 
 def _run_experts_grouped_mm(

@@ -365,6 +365,85 @@ grouped_swiglu.register_autograd(_gs_bwd, setup_context=_gs_setup)
 
 
 # ---------------------------------------------------------------------------
+# fp32 grouped SwiGLU experts: _run_experts_for_loop in the input dtype
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_f32", mutates_args=())
+def grouped_swiglu_f32(
+    x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """fp32 grouped SwiGLU (every product and sum in fp32, as the reference's
+    fp32 per-expert matmuls, moe.py:24-50). Returns (y [R,D], g, u, h [R,H]);
+    rows past sum(counts) of y are zero."""
+    require_gpu(x, w1, w2, w3, num_tokens_per_expert)
+    for t, name in ((x, "x"), (w1, "w1"), (w2, "w2"), (w3, "w3")):
+        if t.dtype != torch.float32:
+            raise TypeError(f"grouped_swiglu_f32 expects float32 {name}, got {t.dtype}")
+    x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    g = x.new_zeros(r, h_dim)
+    u = x.new_zeros(r, h_dim)
+    h = x.new_zeros(r, h_dim)
+    y = x.new_zeros(r, d)
+    s = stream_of(x)
+    call("moe_grouped_gemm_f32_gate_up", ptr(x), ptr(w1), ptr(w3), ptr(counts), r, e, d, h_dim,
+         ptr(g), ptr(u), ptr(h), s)
+    call("moe_grouped_gemm_f32_down", ptr(h), ptr(w2), ptr(counts), r, e, d, h_dim, ptr(y), s)
+    return y, g, u, h
+
+
+@grouped_swiglu_f32.register_fake
+def _(x, w1, w2, w3, num_tokens_per_expert):
+    r, d = x.shape
+    h_dim = w1.shape[1]
+    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+
+
+@torch.library.custom_op("moe_mi355x::grouped_swiglu_f32_backward", mutates_args=())
+def grouped_swiglu_f32_backward(
+    dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
+    g: Tensor, u: Tensor, h: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
+    dy = dy.to(torch.float32).contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    r, d = x.shape
+    e, h_dim, _ = w1.shape
+    dg = x.new_zeros(r, h_dim)
+    du = x.new_zeros(r, h_dim)
+    dx = x.new_zeros(r, d)
+    dw1 = torch.empty_like(w1)
+    dw2 = torch.empty_like(w2)
+    dw3 = torch.empty_like(w3)
+    s = stream_of(x)
+    call("moe_grouped_gemm_f32_bwd_dgu", ptr(dy), ptr(w2), ptr(g), ptr(u), ptr(counts), r, e, d, h_dim,
+         ptr(dg), ptr(du), s)
+    call("moe_grouped_gemm_f32_bwd_dx", ptr(dg), ptr(du), ptr(w1), ptr(w3), ptr(counts), r, e, d, h_dim,
+         ptr(dx), s)
+    call("moe_grouped_gemm_f32_bwd_dw", ptr(dg), ptr(x), ptr(counts), r, e, h_dim, d, ptr(dw1), s)
+    call("moe_grouped_gemm_f32_bwd_dw", ptr(du), ptr(x), ptr(counts), r, e, h_dim, d, ptr(dw3), s)
+    call("moe_grouped_gemm_f32_bwd_dw", ptr(dy), ptr(h), ptr(counts), r, e, d, h_dim, ptr(dw2), s)
+    return dx, dw1, dw2, dw3
+
+
+@grouped_swiglu_f32_backward.register_fake
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h):
+    return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
+
+
+def _gs32_bwd(ctx, dy, _dg, _du, _dh):
+    x, w1, w2, w3, counts, g, u, h = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None, None
+    dx, dw1, dw2, dw3 = grouped_swiglu_f32_backward(dy, x, w1, w2, w3, counts, g, u, h)
+    return dx, dw1, dw2, dw3, None
+
+
+grouped_swiglu_f32.register_autograd(_gs32_bwd, setup_context=_gs_setup)
+
+
+# ---------------------------------------------------------------------------
 # combine: out = shared + sum of a token's routed rows (deterministic)
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("moe_mi355x::combine", mutates_args=())
