@@ -87,6 +87,20 @@ int moe_reorder(const int64_t* selected_experts, const float* top_scores, int64_
                 float* scores_sorted, int64_t* token_idx, int64_t* counts, int32_t* offsets,
                 int32_t* slot_pos, int32_t* tok_pos, moe_stream_t stream);
 
+/* moe_reorder without a workspace argument. No counterpart in the reference:
+ * for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). It allocates nothing: its workspace
+ * is a fixed device array of MOE_REORDER_NOALLOC_SCRATCH_BYTES that each GPU
+ * holds until the process ends, so 2 * ceil(N / 256) * E * 4 bytes must fit in
+ * it (e.g. N <= 524288 tokens at E = 256), else MOE_ERR_WORKSPACE. All calls on
+ * one GPU share that array: calls that overlap on one GPU (other streams or
+ * threads) race. Outputs and arguments as moe_reorder. */
+#define MOE_REORDER_NOALLOC_SCRATCH_BYTES (4 << 20)
+int moe_reorder_noalloc(const int64_t* selected_experts, const float* top_scores, int64_t n_tokens,
+                        int32_t top_k, int32_t n_experts, float* scores_sorted, int64_t* token_idx,
+                        int64_t* counts, int32_t* offsets, int32_t* slot_pos, int32_t* tok_pos,
+                        moe_stream_t stream);
+
 /* Autograd of top_scores.view(-1)[perm] (moe.py:325): d(scores_sorted) [R] ->
  * d(top_scores) [N,K]. */
 int moe_reorder_bwd(const float* grad_scores_sorted, const int32_t* slot_pos, int64_t n_tokens,

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, list] = {
     "moe_reorder_workspace_bytes": [I64, I32],
     "moe_histogram": [P, I64, I32, I32, P, I64, P, P, P],
     "moe_reorder": [P, P, I64, I32, I32, P, I64, P, P, P, P, P, P, P],
+    "moe_reorder_noalloc": [P, P, I64, I32, I32, P, P, P, P, P, P, P],
     "moe_reorder_bwd": [P, P, I64, I32, P, P],
     "moe_permute": [P, P, P, I64, I32, I32, I32, P, P],
     "moe_permute_bwd": [P, P, P, P, I64, I32, I32, I32, I32, P, P, P],

@@ -443,16 +443,14 @@ MOE_API int moe_histogram(const int64_t* selected_experts, int64_t n_tokens, int
   return launch_status();
 }
 
-MOE_API int moe_reorder(const int64_t* selected_experts, const float* top_scores, int64_t n_tokens,
-                        int32_t top_k, int32_t n_experts, void* workspace, int64_t workspace_bytes,
-                        float* scores_sorted, int64_t* token_idx, int64_t* counts, int32_t* offsets,
-                        int32_t* slot_pos, int32_t* tok_pos, hipStream_t stream) {
-  int st = check_idx_args(n_tokens, top_k, n_experts);
-  if (st) return st;
-  if (workspace_bytes < moe_reorder_workspace_bytes(n_tokens, n_experts)) return kErrWorkspace;
-  if (!slot_pos || !tok_pos || !token_idx || (scores_sorted && !top_scores)) return kErrInvalidArgument;
+// The reorder launches on a caller-chosen workspace (block_hist, then
+// block_base: 2 * ceil(N / 256) * E int32, every word written before it is read).
+static int reorder_launch(const int64_t* selected_experts, const float* top_scores, int64_t n_tokens,
+                          int32_t top_k, int32_t n_experts, int32_t* workspace, float* scores_sorted,
+                          int64_t* token_idx, int64_t* counts, int32_t* offsets, int32_t* slot_pos,
+                          int32_t* tok_pos, hipStream_t stream) {
   const int nb = (int)((n_tokens + kBlockTokens - 1) / kBlockTokens);
-  int32_t* block_hist = (int32_t*)workspace;
+  int32_t* block_hist = workspace;
   int32_t* block_base = block_hist + (int64_t)nb * n_experts;
   if (nb > 0)
     hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
@@ -465,6 +463,18 @@ MOE_API int moe_reorder(const int64_t* selected_experts, const float* top_scores
     hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(256), 0, stream, p);
   }
   return launch_status();
+}
+
+MOE_API int moe_reorder(const int64_t* selected_experts, const float* top_scores, int64_t n_tokens,
+                        int32_t top_k, int32_t n_experts, void* workspace, int64_t workspace_bytes,
+                        float* scores_sorted, int64_t* token_idx, int64_t* counts, int32_t* offsets,
+                        int32_t* slot_pos, int32_t* tok_pos, hipStream_t stream) {
+  int st = check_idx_args(n_tokens, top_k, n_experts);
+  if (st) return st;
+  if (workspace_bytes < moe_reorder_workspace_bytes(n_tokens, n_experts)) return kErrWorkspace;
+  if (!slot_pos || !tok_pos || !token_idx || (scores_sorted && !top_scores)) return kErrInvalidArgument;
+  return reorder_launch(selected_experts, top_scores, n_tokens, top_k, n_experts, (int32_t*)workspace,
+                        scores_sorted, token_idx, counts, offsets, slot_pos, tok_pos, stream);
 }
 
 MOE_API int moe_reorder_bwd(const float* grad_scores_sorted, const int32_t* slot_pos,
@@ -607,4 +617,56 @@ MOE_API int moe_combine_bwd(const void* grad_out, const void* routed_output, con
       launch_expand<float>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, false, stream);
   }
   return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// moe_reorder without a workspace argument, for callers that cannot allocate
+// (code under HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc). The workspace is `scratch`, a fixed device array of
+// kReorderScratchBytes that each GPU holds for the life of the process; its
+// device address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address is ever passed to kernels. Every call
+// on one GPU shares the array: calls that overlap on one GPU (two streams, two
+// threads) race. Nothing needs clearing between calls: the histogram and scan
+// kernels write every workspace word before the scatter reads it.
+// ---------------------------------------------------------------------------
+#include <mutex>
+
+namespace moe {
+constexpr int64_t kReorderScratchBytes = MOE_REORDER_NOALLOC_SCRATCH_BYTES;
+static_assert(kReorderScratchBytes == (4 << 20), "the header states 4 MiB");
+constexpr int kMaxDevices = 64;
+}  // namespace moe
+
+static __device__ __align__(256) uint8_t scratch[moe::kReorderScratchBytes];
+static void* g_scratch_ptr[moe::kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on first use).
+static int scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= moe::kMaxDevices) return kErrLaunch;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return kErrLaunch;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
+MOE_API int moe_reorder_noalloc(const int64_t* selected_experts, const float* top_scores, int64_t n_tokens,
+                                int32_t top_k, int32_t n_experts, float* scores_sorted, int64_t* token_idx,
+                                int64_t* counts, int32_t* offsets, int32_t* slot_pos, int32_t* tok_pos,
+                                hipStream_t stream) {
+  int st = check_idx_args(n_tokens, top_k, n_experts);
+  if (st) return st;
+  if (moe_reorder_workspace_bytes(n_tokens, n_experts) > moe::kReorderScratchBytes) return kErrWorkspace;
+  if (!slot_pos || !tok_pos || !token_idx || (scores_sorted && !top_scores)) return kErrInvalidArgument;
+  void* ws = nullptr;
+  st = scratch_ptr(&ws);
+  if (st) return st;
+  return reorder_launch(selected_experts, top_scores, n_tokens, top_k, n_experts, (int32_t*)ws, scores_sorted,
+                        token_idx, counts, offsets, slot_pos, tok_pos, stream);
 }
