@@ -14,7 +14,12 @@ timings taken inside the timed steps, the roofline of the dominant kernel, and
 the reference's CPU MoE path (the oracle's op-for-op restatement) timed on a
 bounded token sample on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload kimi|dsv3|zipf|kimi_fp8|kimi_mxfp8]
+The timed steps run uninstrumented (that time gives `value`); a second pass of
+the same number of steps brackets every C-ABI launch with HIP events on its
+stream for the per-kernel table and the roofline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--workload kimi|dsv3|zipf|kimi_fp8|kimi_mxfp8|gptoss_20b|c1|c1_grouped]
                        [--no-cpu-baseline] [--cpu-tokens N]
 """
 
@@ -73,6 +78,18 @@ WORKLOADS = {
         score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
         score_before=True, std=0.02, bias=0.01, zipf=None, mxfp8=True,
     ),
+    "c1": dict(
+        desc="tiny fp32 MoE layer, fp32 experts (the for-loop path)",
+        bs=2, slen=2048, dim=256, experts=8, top_k=2, hidden=512, shared_hidden=0,
+        score_func="softmax", route_norm=False, route_scale=1.0, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.0, zipf=None, fp32=True, grouped=False,
+    ),
+    "c1_grouped": dict(
+        desc="tiny fp32 MoE layer, bf16 grouped-mm experts (use_grouped_mm=True)",
+        bs=2, slen=2048, dim=256, experts=8, top_k=2, hidden=512, shared_hidden=0,
+        score_func="softmax", route_norm=False, route_scale=1.0, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.0, zipf=None, fp32=True, grouped=True,
+    ),
     "gptoss_20b": dict(
         desc="gpt-oss-20b-shape MoE layer (biased clamped-SwiGLU experts, biased softmax gate)",
         bs=4, slen=4096, dim=2880, experts=32, top_k=4, hidden=2880, shared_hidden=0,
@@ -81,8 +98,11 @@ WORKLOADS = {
     ),
 }
 
-GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm", "mxfp8_gemm", "grouped_gemm_oss")
-                     for m in ("gate_up", "down", "bwd_dgu", "bwd_dx", "bwd_dw13", "bwd_dw1", "bwd_dw2"))
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+
+GEMM_ENTRIES = tuple(f"moe_{kind}_{m}" for kind in ("grouped_gemm", "fp8_gemm", "mxfp8_gemm", "grouped_gemm_oss",
+                                                   "grouped_gemm_f32")
+                     for m in ("gate_up", "down", "bwd_dgu", "bwd_dx", "bwd_dw13", "bwd_dw1", "bwd_dw2", "bwd_dw"))
 
 
 def kernel_work(name: str, w: dict) -> tuple[str, float]:
@@ -93,8 +113,11 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
     d, e, k, h = w["dim"], w["experts"], w["top_k"], w["hidden"]
     r = n * k
     b = 2  # bf16 rows
-    flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw1": 4, "bwd_dw2": 2}
-    for kind in ("moe_grouped_gemm_oss_", "moe_grouped_gemm_", "moe_fp8_gemm_", "moe_mxfp8_gemm_"):
+    # bwd_dw (fp32 kernels) is one launch per weight: 2 R D H each
+    flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw1": 4, "bwd_dw2": 2,
+             "bwd_dw": 2}
+    for kind in ("moe_grouped_gemm_oss_", "moe_grouped_gemm_f32_", "moe_grouped_gemm_", "moe_fp8_gemm_",
+                 "moe_mxfp8_gemm_"):
         if name.startswith(kind) and name[len(kind):] in flops:
             return "mfma", float(flops[name[len(kind):]] * r * d * h)
     nbytes = {
@@ -159,7 +182,8 @@ def make_layer(w: dict, device: torch.device, seed: int):
     cls = GptOssMoE if w.get("gptoss") else MoE
     cfg = cls.Config(
         num_experts=e,
-        experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e),
+        experts=GroupedExperts.Config(dim=d, hidden_dim=h, num_experts=e,
+                                      use_grouped_mm=w.get("grouped", True)),
         router=TokenChoiceTopKRouter.Config(
             num_experts=e, gate=Linear.Config(in_features=d, out_features=e, bias=bool(w.get("gptoss"))),
             top_k=w["top_k"],
@@ -178,9 +202,15 @@ def make_layer(w: dict, device: torch.device, seed: int):
         moe = cfg.build()
     moe = moe.to_empty(device=device)
     gen = torch.Generator(device=device).manual_seed(seed)
+    pdtype = torch.float32 if w.get("fp32") else torch.bfloat16
     with torch.no_grad():
         for name, p in moe.named_parameters():
-            p.data = torch.empty(p.shape, dtype=torch.bfloat16, device=device).normal_(0.0, w["std"], generator=gen)
+            t = torch.empty(p.shape, dtype=torch.float32, device=device)
+            if w.get("fp32"):  # the tiny layer's init: trunc_normal_(std) with the default bounds +-2
+                torch.nn.init.trunc_normal_(t, mean=0.0, std=w["std"], generator=gen)
+            else:
+                t.normal_(0.0, w["std"], generator=gen)
+            p.data = t.to(pdtype)
         bias = (torch.rand(e, generator=gen, device=device) * 2 - 1) * w["bias"]
         if w["zipf"]:
             # Zipf(s)-shaped per-expert boost over a random expert order, plus a
@@ -203,16 +233,59 @@ def make_layer(w: dict, device: torch.device, seed: int):
     return moe
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (as lscpu prints it), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _time_reference_ops(params: dict, cfg, xs: torch.Tensor, gs: torch.Tensor, label: str) -> float:
+    """Median of 3 forward + backward passes of the reference op sequence on the
+    CPU after 1 warmup, in seconds."""
+    from oracle import moe_ref as R
+
+    times = []
+    for it in range(4):
+        for p in params.values():
+            p.grad = None
+        xi = xs.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        out = R.moe_forward_reference_ops(params, xi, cfg)
+        out.backward(gs)
+        times.append(time.perf_counter() - t0)
+        print(f"[bench] cpu baseline {label} iteration {it}: {times[-1]:.3f} s", file=sys.stderr, flush=True)
+    return statistics.median(times[1:])
+
+
+def _router_cfg(w: dict):
+    from oracle import moe_ref as R
+
+    return R.RouterCfg(num_experts=w["experts"], top_k=w["top_k"], score_func=w["score_func"],
+                       num_expert_groups=w["groups"], num_limited_groups=w["limited"],
+                       route_norm=w["route_norm"], route_scale=w["route_scale"])
+
+
 def cpu_baseline(moe, w: dict, x: torch.Tensor, g: torch.Tensor, n_tokens: int) -> dict:
     """The reference's CPU MoE path (oracle restatement of moe.py:380-477 with the
     same torch calls; histc -> bincount on the CPU) on the first n_tokens tokens,
     forward + backward, 1 warmup + median of 3, on this host's cores."""
     from oracle import moe_ref as R
 
-    threads = len(os.sched_getaffinity(0))
-    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
-        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
-    torch.set_num_threads(threads)
+    threads = _cpu_threads()
     sd = {k: v.detach().cpu() for k, v in moe.state_dict().items()}
     params = {"gate": sd["router.gate.weight"], "expert_bias": sd["expert_bias"]}
     if w.get("gptoss"):
@@ -226,35 +299,65 @@ def cpu_baseline(moe, w: dict, x: torch.Tensor, g: torch.Tensor, n_tokens: int) 
     for k, p in params.items():
         if k != "expert_bias":
             p.requires_grad_(True)
-    rc = R.RouterCfg(num_experts=w["experts"], top_k=w["top_k"], score_func=w["score_func"],
-                     num_expert_groups=w["groups"], num_limited_groups=w["limited"],
-                     route_norm=w["route_norm"], route_scale=w["route_scale"])
-    cfg = R.MoECfg(router=rc, dim=w["dim"], hidden_dim=w["hidden"], score_before_experts=w["score_before"],
-                   use_grouped_mm=True, has_shared=bool(w["shared_hidden"]),
-                   expert_kind="gptoss" if w.get("gptoss") else "swiglu")
+    grouped = w.get("grouped", True)
+    cfg = R.MoECfg(router=_router_cfg(w), dim=w["dim"], hidden_dim=w["hidden"],
+                   score_before_experts=w["score_before"], use_grouped_mm=grouped,
+                   has_shared=bool(w["shared_hidden"]), expert_kind="gptoss" if w.get("gptoss") else "swiglu")
     xs = x.reshape(-1, w["dim"])[:n_tokens].detach().cpu().reshape(1, n_tokens, w["dim"])
     gs = g.reshape(-1, w["dim"])[:n_tokens].detach().cpu().reshape(1, n_tokens, w["dim"])
-    times = []
-    for it in range(4):
-        for p in params.values():
-            p.grad = None
-        xi = xs.clone().requires_grad_(True)
-        t0 = time.perf_counter()
-        out = R.moe_forward_reference_ops(params, xi, cfg)
-        out.backward(gs)
-        times.append(time.perf_counter() - t0)
-        print(f"[bench] cpu baseline iteration {it}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
-    t = statistics.median(times[1:])
+    t = _time_reference_ops(params, cfg, xs, gs, w["desc"])
     print(f"[bench] cpu baseline: {n_tokens} tokens, {threads} threads, {t:.2f} s/iter", file=sys.stderr, flush=True)
+    experts = "bf16 torch._grouped_mm experts" if grouped else f"{x.dtype} for-loop experts"
     return {
         "value": n_tokens * w["top_k"] / t,
         "unit": "routed tokens/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": (f"reference op sequence (torch ops, CPU, bf16 grouped_mm) fwd+bwd on the first "
-                   f"{n_tokens} of {w['bs'] * w['slen']} tokens of the same layer; median of 3 after 1 warmup; "
-                   f"{t:.2f} s/iter"),
+        "sample": (f"reference op sequence (torch ops on the CPU, {experts}) fwd+bwd on "
+                   f"{'all' if n_tokens == w['bs'] * w['slen'] else 'the first'} {n_tokens} of "
+                   f"{w['bs'] * w['slen']} tokens of the same layer; median of 3 after 1 warmup; {t:.2f} s/iter"),
     }
+
+
+def cpu_baseline_tiny(seed: int = 0) -> dict:
+    """The tiny fp32 layer (dim 256, 8 experts, top-2 softmax, hidden 512, no
+    shared expert, 4096 tokens) on the CPU through the reference op sequence in
+    both expert modes: bf16 torch._grouped_mm (use_grouped_mm=True, the default)
+    and the fp32 per-expert for-loop (moe.py:24-50). Inputs are drawn on the CPU
+    from one seeded generator in the order gate, w1, w2, w3, bias, x, g."""
+    from oracle import moe_ref as R
+
+    w = WORKLOADS["c1"]
+    threads = _cpu_threads()
+    n, d, e, h = w["bs"] * w["slen"], w["dim"], w["experts"], w["hidden"]
+    gen = torch.Generator().manual_seed(seed)
+
+    def tn(*shape):
+        return torch.nn.init.trunc_normal_(torch.empty(shape), mean=0.0, std=w["std"], generator=gen)
+
+    params = {"gate": tn(e, d), "w1": tn(e, h, d), "w2": tn(e, d, h), "w3": tn(e, h, d), "expert_bias": torch.zeros(e)}
+    x = torch.randn(1, n, d, generator=gen)
+    g = torch.randn(1, n, d, generator=gen)
+    for k, p in params.items():
+        if k != "expert_bias":
+            p.requires_grad_(True)
+    out = {"cores": threads, "cpu_model": cpu_model(), "kind": "port", "unit": "routed tokens/s",
+           "sample": f"all {n} tokens, fp32 parameters and activations; median of 3 after 1 warmup"}
+    for grouped, key in ((True, "grouped_mm_bf16"), (False, "for_loop_fp32")):
+        cfg = R.MoECfg(router=_router_cfg(w), dim=d, hidden_dim=h, score_before_experts=w["score_before"],
+                       use_grouped_mm=grouped, has_shared=False)
+        t = _time_reference_ops(params, cfg, x, g, f"tiny fp32 layer ({key})")
+        out[key] = round(n * w["top_k"] / t, 1)
+    return out
+
+
+def _gemm_peak(name: str) -> float:
+    if name.startswith(("moe_fp8_", "moe_mxfp8_")):
+        return PEAK_FP8_TFLOPS
+    if name.startswith("moe_grouped_gemm_f32_"):
+        return PEAK_FP32_TFLOPS
+    return PEAK_BF16_TFLOPS
 
 
 TRAFFIC_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
@@ -284,7 +387,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=None,
-                    help="tokens in the CPU baseline sample (default: 8192, or 1024 for dsv3)")
+                    help="tokens in the CPU baseline sample (default: all for kimi, 1024 for dsv3, else 8192)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE layer runs with all experts resident on a single "
@@ -305,8 +408,9 @@ def main() -> int:
     k = w["top_k"]
     moe = make_layer(w, dev, args.seed)
     gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
-    x = torch.randn(w["bs"], w["slen"], w["dim"], generator=gen, device=dev).bfloat16()
-    g = torch.randn(w["bs"], w["slen"], w["dim"], generator=gen, device=dev).bfloat16()
+    adtype = torch.float32 if w.get("fp32") else torch.bfloat16
+    x = torch.randn(w["bs"], w["slen"], w["dim"], generator=gen, device=dev).to(adtype)
+    g = torch.randn(w["bs"], w["slen"], w["dim"], generator=gen, device=dev).to(adtype)
     x.requires_grad_(True)
     params = list(moe.parameters())
 
@@ -324,8 +428,6 @@ def main() -> int:
     with torch.no_grad():
         counts = moe.router(x.detach().view(-1, w["dim"]), moe.expert_bias)[2].cpu()
 
-    timer = _lib.KernelTimer()
-    _lib.set_timer(timer)
     print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -333,8 +435,17 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    _lib.set_timer(None)
     ms = (t1 - t0) * 1e3 / args.steps
+
+    # per-kernel table: the same number of steps again, every C-ABI launch
+    # bracketed by HIP events on its stream
+    timer = _lib.KernelTimer()
+    _lib.set_timer(timer)
+    print(f"[bench] per-kernel timing over {args.steps} steps", file=sys.stderr, flush=True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    _lib.set_timer(None)
 
     durations = timer.durations_ms()
     launch_args = timer.launch_args()
@@ -348,7 +459,7 @@ def main() -> int:
             if all(v is not None for v in lb):
                 work = sum(lb) / len(lb)  # bytes of the average launch, over the average launch time
         if bound == "mfma":
-            peak = PEAK_FP8_TFLOPS if name.startswith(("moe_fp8_", "moe_mxfp8_")) else PEAK_BF16_TFLOPS
+            peak = _gemm_peak(name)
             achieved, unit = work / (avg * 1e-3) / 1e12, "TFLOP/s"
         elif work is not None:
             achieved, peak, unit = work / (avg * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
@@ -364,27 +475,30 @@ def main() -> int:
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
     dom = max(kernels, key=lambda nm: kernels[nm]["avg_ms"] * kernels[nm]["launches_per_step"])
     dk = kernels[dom]
-    gemm_peak = PEAK_FP8_TFLOPS if (w.get("fp8") or w.get("mxfp8")) else PEAK_BF16_TFLOPS
+    gemm_peak = (PEAK_FP8_TFLOPS if (w.get("fp8") or w.get("mxfp8")) else
+                 PEAK_FP32_TFLOPS if (w.get("fp32") and not w.get("grouped", True)) else PEAK_BF16_TFLOPS)
     roofline = {
         "kernel": dom,
         "bound": dk["bound"],
         "achieved": dk["achieved"],
-        "peak": (PEAK_FP8_TFLOPS if dom.startswith(("moe_fp8_", "moe_mxfp8_")) else PEAK_BF16_TFLOPS)
-        if dk["bound"] == "mfma"
-        else PEAK_HBM_GBS,
+        "peak": _gemm_peak(dom) if dk["bound"] == "mfma" else PEAK_HBM_GBS,
         "unit": dk["unit"],
         "frac": dk["frac"],
-        "traffic": None,
+        "traffic": measured_traffic(args.workload, dom),
+        "traffic_source": (f"profiles/hbm_traffic_{args.workload}.txt: rocprofv3 FETCH_SIZE and WRITE_SIZE per "
+                           f"dispatch of the committed build, scaled by a copy-kernel calibration; not measured "
+                           f"in this run"),
     }
-    roofline["traffic"] = measured_traffic(args.workload, dom)
     mover = ("moe_permute", "moe_combine", "moe_combine_bwd", "moe_permute_bwd")
     mover_ms = sum(kernels[m]["avg_ms"] for m in mover if m in kernels)
     mover_bytes = sum(kernel_work(m, w)[1] for m in mover if m in kernels)
 
-    cpu = None
+    cpu = cpu_tiny = None
     if not args.no_cpu_baseline:
-        cpu_tokens = args.cpu_tokens or (1024 if args.workload == "dsv3" else 8192)
+        cpu_tokens = args.cpu_tokens or {"dsv3": 1024, "kimi": n}.get(args.workload, 8192)
         cpu = cpu_baseline(moe, w, x, g, min(cpu_tokens, n))
+        if args.workload == "kimi":
+            cpu_tiny = cpu_baseline_tiny()
 
     line = {
         "metric": "MoE layer fwd+bwd routed tokens/s; grouped-GEMM TFLOPS as % of MFMA peak",
@@ -398,6 +512,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": ("fp8 e4m3 (grouped GEMMs), bf16 elsewhere" if w.get("fp8") else
+                  "fp32" if (w.get("fp32") and not w.get("grouped", True)) else
+                  "fp32 (bf16 grouped GEMMs)" if w.get("fp32") else
                   "MXFP8 e4m3 + e8m0 block-32 scales (grouped GEMMs), bf16 elsewhere" if w.get("mxfp8") else "bf16"),
         "data": "synthetic (random-init weights, x ~ N(0,1), g ~ N(0,1))",
         "config": {
@@ -425,6 +541,7 @@ def main() -> int:
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_tiny_fp32_layer": cpu_tiny,
     }
     print(json.dumps(line), flush=True)
     return 0

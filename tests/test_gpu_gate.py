@@ -1,9 +1,11 @@
 """Router gate logits in fp32 (torchtitan/models/common/moe.py:230-232) on the GPU.
 
-The layer's default gate is the reference's own call (the fp32 GEMM under
-autocast), which the tests below check it is, bit for bit. The opt-in gate
-(``bf16_mfma=True``: bf16 GEMMs with fp32 accumulation, moe._GateF32) and the
-fp32 path are both checked against the fp64 product of the same values:
+The layer's default gate computes its logits with the reference's own call (the
+fp32 GEMM under autocast), which the tests below check bit for bit, and its
+backward on bf16 GEMMs over an exact three-term split of the fp32 logit
+gradient (moe._GateRef). That backward, the opt-in gate (``bf16_mfma=True``:
+forward too on bf16 GEMMs with fp32 accumulation, moe._GateF32) and the fp32
+autocast path are checked against the fp64 product of the same values:
   * logits: the error of the bf16-GEMM path is at most 2x the fp32 path's
     (plus 1e-6 of the largest logit): both are fp32 sums of the same exact
     products, in different orders;
@@ -43,10 +45,11 @@ def _ulp_bf16(t: torch.Tensor) -> torch.Tensor:
     return torch.exp2(e - 7)
 
 
+@pytest.mark.parametrize("mode", ["default", "bf16_mfma"])
 @pytest.mark.parametrize("case", list(CASES))
-def test_gate_logits_f32_vs_fp64(case):
+def test_gate_logits_f32_vs_fp64(case, mode):
     n, d, e, bias = CASES[case]
-    banner(f"gate {case}: n={n} dim={d} experts={e} bias={bias}")
+    banner(f"gate {case} {mode}: n={n} dim={d} experts={e} bias={bias}")
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(7)
     gate = Linear(Linear.Config(in_features=d, out_features=e, bias=bias)).to(dev)
@@ -62,7 +65,7 @@ def test_gate_logits_f32_vs_fp64(case):
         xs = x.clone().requires_grad_(True)
         gate.zero_grad(set_to_none=True)
         if fast:
-            y = gate_logits_f32(xs, gate, bf16_mfma=True)
+            y = gate_logits_f32(xs, gate, bf16_mfma=(mode == "bf16_mfma"))
         else:
             with torch.autocast(device_type="cuda", dtype=torch.float32):
                 y = gate(xs)
@@ -83,6 +86,8 @@ def test_gate_logits_f32_vs_fp64(case):
     print(f"[case] {case}: logits max err fast {err_f:.3e} fp32-autocast {err_r:.3e} (max |logit| {scale:.3e})",
           flush=True)
     assert err_f <= 2 * err_r + 1e-6 * scale
+    if mode == "default":
+        assert torch.equal(y_f, y_r), "the default gate's logits are not the autocast GEMM's bits"
 
     for name, got, ref, truth in (
         ("dx", dx_f, dx_r, upd @ wd),

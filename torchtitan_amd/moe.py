@@ -151,16 +151,54 @@ def _bf16_terms(d: torch.Tensor) -> torch.Tensor:
     return torch.cat([hi, mid, lo], dim=1)
 
 
+def _gate_backward_bf16(ctx, grad: torch.Tensor):
+    """dx, dW (and the bias gradient) of fp32 logits = x W^T (+ b) for bf16 x and
+    W: the fp32 logit gradient is split exactly into three bf16 terms
+    (_bf16_terms), and dx, dW are bf16 GEMMs over the 3x longer sum -- exact
+    products accumulated in fp32, as the fp32 GEMMs of the autocast backward,
+    in another summation order -- rounded to x's and W's dtype once, as
+    autocast's casts do."""
+    x, w = ctx.saved_tensors
+    d3 = _bf16_terms(grad.float().contiguous())
+    dx = dw = db = None
+    if ctx.needs_input_grad[0]:
+        dx = torch.mm(d3, torch.cat([w, w, w], dim=0))  # fp32 accumulation, one rounding to bf16
+    if ctx.needs_input_grad[1]:
+        e = w.shape[0]
+        dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
+        dw = ((dw3[:e] + dw3[e:2 * e]) + dw3[2 * e:]).to(w.dtype)
+    if ctx.has_bias and ctx.needs_input_grad[2]:
+        db = grad.float().sum(0).to(ctx.b_dtype)
+    return dx, dw, db
+
+
+class _GateRef(torch.autograd.Function):
+    """The reference's gate (moe.py:230-232) with a bf16-MFMA backward.
+
+    Forward: F.linear on the fp32 casts of x, W (and b), which is what the
+    reference's ``gate(x)`` under ``torch.autocast(dtype=float32)`` runs -- the
+    same fp32 GEMM, so the logits, and the routing, are the reference's bits.
+    Backward: _gate_backward_bf16, the same exact products as the fp32 backward
+    GEMMs, summed in another order, without the fp32 copies of x and W."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
+        logits = torch.nn.functional.linear(x.float(), w.float(), b.float() if b is not None else None)
+        ctx.save_for_backward(x, w)
+        ctx.has_bias = b is not None
+        ctx.b_dtype = b.dtype if b is not None else None
+        return logits
+
+    backward = staticmethod(_gate_backward_bf16)
+
+
 class _GateF32(torch.autograd.Function):
     """fp32(x) @ fp32(W)^T (+ fp32(b)) for bf16 x and W, on bf16 GEMMs with fp32
     accumulation and fp32 output.
 
     A product of two bf16 values is exact in fp32, so the forward equals the fp32
     GEMM of the reference's autocast region (moe.py:230-232) up to summation
-    order. In the backward the fp32 logit gradient is split exactly into three
-    bf16 terms (_bf16_terms), and dx, dW are bf16 GEMMs over the 3x longer sum,
-    again exact products accumulated in fp32; they are rounded to x's and W's
-    dtype once, as autocast's casts do."""
+    order. The backward is _gate_backward_bf16."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
@@ -172,39 +210,30 @@ class _GateF32(torch.autograd.Function):
         ctx.b_dtype = b.dtype if b is not None else None
         return logits
 
-    @staticmethod
-    def backward(ctx, grad: torch.Tensor):
-        x, w = ctx.saved_tensors
-        d3 = _bf16_terms(grad.float().contiguous())
-        dx = dw = db = None
-        if ctx.needs_input_grad[0]:
-            dx = torch.mm(d3, torch.cat([w, w, w], dim=0))  # fp32 accumulation, one rounding to bf16
-        if ctx.needs_input_grad[1]:
-            e = w.shape[0]
-            dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
-            dw = ((dw3[:e] + dw3[e:2 * e]) + dw3[2 * e:]).to(w.dtype)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = grad.float().sum(0).to(ctx.b_dtype)
-        return dx, dw, db
+    backward = staticmethod(_gate_backward_bf16)
 
 
 def gate_logits_f32(x: torch.Tensor, gate: nn.Linear, bf16_mfma: bool = False) -> torch.Tensor:
     """The router's gate in fp32 (moe.py:230-232).
 
-    By default this is the reference's own call, ``gate(x)`` under
-    ``torch.autocast(dtype=float32)``: an fp32 GEMM whose logits are the
-    reference's bits, so that top-k selection matches it exactly.
+    The logits are by default those of the reference's own call, ``gate(x)``
+    under ``torch.autocast(dtype=float32)``: the same fp32 GEMM, so that top-k
+    selection matches it exactly. For bf16 x and W on the GPU (outside an outer
+    autocast) that forward runs in _GateRef, whose backward takes bf16 GEMMs
+    over an exact three-term split of the logit gradient instead of fp32 GEMMs;
+    anything else runs the autocast region as is.
 
-    ``bf16_mfma=True`` (opt-in, bf16 x and W on the GPU only) takes _GateF32:
-    the same exact products summed in another order, about 0.25 ms faster at
-    16K tokens x 2304 x 256 experts. A few-ulp logit difference can change a
-    token's expert set where its K-th and (K+1)-th biased scores nearly tie."""
+    ``bf16_mfma=True`` (opt-in) takes _GateF32 for bf16 x and W: the forward
+    too on bf16 GEMMs with fp32 accumulation, the same exact products summed in
+    another order. A few-ulp logit difference can change a token's expert set
+    where its K-th and (K+1)-th biased scores nearly tie."""
     w, b = _local(gate.weight), gate.bias
     b = _local(b) if b is not None else None
-    if (bf16_mfma and x.is_cuda and x.dim() == 2 and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+    if (x.is_cuda and x.dim() == 2 and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
             and (b is None or b.dtype in (torch.bfloat16, torch.float32))
             and not torch.is_autocast_enabled(x.device.type)):
-        return _GateF32.apply(x.contiguous(), w.contiguous(), b)
+        fn = _GateF32 if bf16_mfma else _GateRef
+        return fn.apply(x.contiguous(), w.contiguous(), b)
     with torch.autocast(device_type=x.device.type, dtype=torch.float32):
         return gate(x)
 
