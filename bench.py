@@ -20,7 +20,7 @@ stream for the per-kernel table and the roofline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
                        [--workload kimi|dsv3|zipf|kimi_fp8|kimi_mxfp8|gptoss_20b|c1|c1_grouped]
-                       [--no-cpu-baseline] [--cpu-tokens N]
+                       [--no-cpu-baseline] [--cpu-tokens N] [--gemm-ceiling]
 """
 
 from __future__ import annotations
@@ -378,6 +378,45 @@ def measured_traffic(workload: str, entry: str) -> int | None:
     return None
 
 
+def gemm_ceiling(w: dict, dev: torch.device, reps: int = 10) -> dict:
+    """hipBLASLt (through torch.bmm / torch.mm, contiguous bf16 operands) on the
+    uniform-batch equivalents of the six expert GEMMs of workload w: E batches of
+    M = N*K/E rows each (every expert with the mean load, no ragged tail, no
+    fused epilogue), and the same work as one dense GEMM. A reference for what
+    the vendor library reaches on these shapes on this GPU; not part of the step."""
+    n, d, e, k, h = w["bs"] * w["slen"], w["dim"], w["experts"], w["top_k"], w["hidden"]
+    m = n * k // e
+    shapes = {  # name: (batch, rows, contraction, columns)
+        "gate_up": (e, m, d, 2 * h), "down": (e, m, h, d), "bwd_dgu": (e, m, d, h),
+        "bwd_dx": (e, m, 2 * h, d), "bwd_dw13": (e, 2 * h, m, d), "bwd_dw2": (e, d, m, h),
+        "dense_gate_up": (1, n * k, d, 2 * h),
+    }
+    gen = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+    for name, (b, mm, kk, nn) in shapes.items():
+        a = torch.randn(b, mm, kk, generator=gen, device=dev).bfloat16()
+        bm = torch.randn(b, kk, nn, generator=gen, device=dev).bfloat16()
+        fn = (lambda: torch.mm(a[0], bm[0])) if b == 1 else (lambda: torch.bmm(a, bm))
+        for _ in range(3):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ts = []
+        for _ in range(reps):
+            ev[0].record()
+            fn()
+            ev[1].record()
+            ev[1].synchronize()
+            ts.append(ev[0].elapsed_time(ev[1]))
+        ms = statistics.median(ts)
+        tf = 2.0 * b * mm * kk * nn / (ms * 1e-3) / 1e12
+        out[name] = {"shape": [b, mm, kk, nn], "ms": round(ms, 4), "tflops": round(tf, 1),
+                     "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+        print(f"[bench] library GEMM {name} {b}x[{mm}x{kk}]x[{kk}x{nn}]: {ms:.4f} ms {tf:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
+        del a, bm
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -386,6 +425,8 @@ def main() -> int:
     ap.add_argument("--workload", default="kimi", choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="also time the vendor library on uniform-batch equivalents of the six expert GEMMs")
     ap.add_argument("--cpu-tokens", type=int, default=None,
                     help="tokens in the CPU baseline sample (default: all for kimi, 1024 for dsv3, else 8192)")
     args = ap.parse_args()
@@ -543,6 +584,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "cpu_baseline_tiny_fp32_layer": cpu_tiny,
     }
+    if args.gemm_ceiling:
+        line["library_gemm_uniform_batch"] = gemm_ceiling(w, dev)
     print(json.dumps(line), flush=True)
     return 0
 
