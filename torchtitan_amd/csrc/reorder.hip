@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void expand_rows_kernel(const T* __restrict__ 
 // sorted index_put with accumulate); r_k = routed[pos_k], or
 // round(routed[pos_k] * score) when the score is applied after the experts
 // (moe.py:465-469). Without a shared expert the sum starts from zero.
-template <typename T>
+template <typename T, int MAXK>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shared_out,
                                                       const T* __restrict__ routed,
                                                       const int32_t* __restrict__ tok_pos,
@@ -275,6 +275,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shar
        c += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = c / cpr;
     const int ch = (int)(c - t * cpr);
+    // the K positions, then all K row chunks in flight before the first add
+    int32_t pos[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) pos[k] = k < K ? tok_pos[t * K + k] : 0;
     float a[n];
     if (shared_out) {
       Chunk<T>::unpack(*(const uint4*)(shared_out + t * D + ch * n), a);
@@ -282,14 +286,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ shar
 #pragma unroll
       for (int i = 0; i < n; ++i) a[i] = 0.f;
     }
-    for (int k = 0; k < K; ++k) {
-      const int64_t pos = tok_pos[t * K + k];
-      uint4 v = *(const uint4*)(routed + pos * D + ch * n);
-      if (scores_sorted) v = scale_chunk<T>(v, scores_sorted[pos]);
-      float f[n];
-      Chunk<T>::unpack(v, f);
+    uint4 v[MAXK];
 #pragma unroll
-      for (int i = 0; i < n; ++i) a[i] = Chunk<T>::round(a[i] + f[i]);
+    for (int k = 0; k < MAXK; ++k)
+      v[k] = k < K ? *(const uint4*)(routed + (int64_t)pos[k] * D + ch * n) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+      if (k < K) {
+        uint4 w = v[k];
+        if (scores_sorted) w = scale_chunk<T>(w, scores_sorted[pos[k]]);
+        float f[n];
+        Chunk<T>::unpack(w, f);
+#pragma unroll
+        for (int i = 0; i < n; ++i) a[i] = Chunk<T>::round(a[i] + f[i]);
+      }
     }
     *(uint4*)(out + t * D + ch * n) = Chunk<T>::pack(a);
   }
@@ -355,13 +365,14 @@ __global__ __launch_bounds__(256) void permute_bwd_kernel(
   for (int64_t t = (int64_t)blockIdx.x * 4 + wv; t < n_tokens; t += (int64_t)gridDim.x * 4) {
     float part[MAXK];
     float sc[MAXK];
-    int64_t pos[MAXK];
+    int32_t pos[MAXK];
 #pragma unroll
     for (int k = 0; k < MAXK; ++k) {
       part[k] = 0.f;
-      pos[k] = (k < K) ? (int64_t)tok_pos[t * K + k] : 0;
+      pos[k] = (k < K) ? tok_pos[t * K + k] : 0;
       sc[k] = (k < K && scores_sorted) ? scores_sorted[pos[k]] : 1.0f;
     }
+    constexpr int HK = MAXK / 2;  // row chunks loaded in two batches of HK
     for (int ch = lane; ch < cpr; ch += kWave) {
       uint4 xv = make_uint4(0, 0, 0, 0);
       if (scores_sorted) xv = *(const uint4*)(x + t * D + ch * n);
@@ -369,17 +380,27 @@ __global__ __launch_bounds__(256) void permute_bwd_kernel(
 #pragma unroll
       for (int i = 0; i < n; ++i) a[i] = 0.f;
 #pragma unroll
-      for (int k = 0; k < MAXK; ++k) {
-        if (k < K) {
-          uint4 g = *(const uint4*)(grad_routed + pos[k] * D + ch * n);
-          if (scores_sorted) {
-            part[k] += dot_chunk<T>(g, xv);
-            g = scale_chunk<T>(g, sc[k]);
-          }
-          float f[n];
-          Chunk<T>::unpack(g, f);
+      for (int h = 0; h < 2; ++h) {
+        uint4 gk[HK];
 #pragma unroll
-          for (int i = 0; i < n; ++i) a[i] = round_each ? Chunk<T>::round(a[i] + f[i]) : (a[i] + f[i]);
+        for (int kk = 0; kk < HK; ++kk) {
+          const int k = h * HK + kk;
+          gk[kk] = (k < K) ? *(const uint4*)(grad_routed + (int64_t)pos[k] * D + ch * n) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int kk = 0; kk < HK; ++kk) {
+          const int k = h * HK + kk;
+          if (k < K) {
+            uint4 g = gk[kk];
+            if (scores_sorted) {
+              part[k] += dot_chunk<T>(g, xv);
+              g = scale_chunk<T>(g, sc[k]);
+            }
+            float f[n];
+            Chunk<T>::unpack(g, f);
+#pragma unroll
+            for (int i = 0; i < n; ++i) a[i] = round_each ? Chunk<T>::round(a[i] + f[i]) : (a[i] + f[i]);
+          }
         }
       }
       *(uint4*)(grad_x + t * D + ch * n) = Chunk<T>::pack(a);
@@ -511,6 +532,22 @@ static void launch_expand(const void* src, int64_t n_tokens, int dim, int top_k,
                        top_k, slot_pos, scores, (T*)out);
 }
 
+// the K row chunks of a token are held in registers at once: a kernel per bound on K
+template <typename T>
+static void launch_combine(const void* shared_out, const void* routed, const int32_t* tok_pos, const float* scores,
+                           int64_t n_tokens, int dim, int top_k, void* out, hipStream_t stream) {
+  const dim3 grid(stream_grid(n_tokens * (dim / Chunk<T>::kN), 256, 32768));
+  if (top_k <= 8)
+    hipLaunchKernelGGL((combine_kernel<T, 8>), grid, dim3(256), 0, stream, (const T*)shared_out, (const T*)routed,
+                       tok_pos, scores, n_tokens, dim, top_k, (T*)out);
+  else if (top_k <= 16)
+    hipLaunchKernelGGL((combine_kernel<T, 16>), grid, dim3(256), 0, stream, (const T*)shared_out, (const T*)routed,
+                       tok_pos, scores, n_tokens, dim, top_k, (T*)out);
+  else
+    hipLaunchKernelGGL((combine_kernel<T, kMaxTopK>), grid, dim3(256), 0, stream, (const T*)shared_out,
+                       (const T*)routed, tok_pos, scores, n_tokens, dim, top_k, (T*)out);
+}
+
 template <typename T>
 static void launch_permute_bwd(const void* grad_routed, const void* x, const int32_t* tok_pos,
                                const float* scores, int64_t n_tokens, int dim, int top_k, int round_each,
@@ -582,14 +619,10 @@ MOE_API int moe_combine(const void* shared_out, const void* routed_output, const
   if (st) return st;
   if (n_tokens == 0) return kOk;
   if (!routed_output || !tok_pos || !out) return kErrInvalidArgument;
-  const dim3 grid(stream_grid(n_tokens * (dim / (dtype == MOE_DTYPE_BF16 ? 8 : 4))));
   if (dtype == MOE_DTYPE_BF16)
-    hipLaunchKernelGGL(combine_kernel<uint16_t>, grid, dim3(256), 0, stream, (const uint16_t*)shared_out,
-                       (const uint16_t*)routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k,
-                       (uint16_t*)out);
+    launch_combine<uint16_t>(shared_out, routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k, out, stream);
   else
-    hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, stream, (const float*)shared_out,
-                       (const float*)routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k, (float*)out);
+    launch_combine<float>(shared_out, routed_output, tok_pos, scores_sorted, n_tokens, dim, top_k, out, stream);
   return launch_status();
 }
 
