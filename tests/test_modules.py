@@ -101,6 +101,55 @@ def test_feed_forward_is_swiglu():
     torch.testing.assert_close(ff(x), ref.t())
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_feed_forward_fused_backward_matches_module_autograd(dtype):
+    """The shared expert's own backward (dg, du side by side, one GEMM for dW1 and
+    dW3) against autograd through the three projections: output, dx and dW2 are
+    the same calls and equal bit for bit; dW1 and dW3 are each one fp32-accumulated
+    product rounded once, within the bound of such a sum. Tokens are 2-D here: the
+    CPU's matmul of a 3-D input is not the folded 2-D product (the GPU's is, and
+    the GPU test runs 3-D inputs)."""
+    torch.manual_seed(0)
+    d, hs, n = 40, 24, 96
+    ff = FeedForward.Config(w1=Linear.Config(in_features=d, out_features=hs),
+                            w2=Linear.Config(in_features=hs, out_features=d),
+                            w3=Linear.Config(in_features=d, out_features=hs)).build().to(dtype)
+    x = torch.randn(n, d).to(dtype)
+    gy = torch.randn(n, d).to(dtype)
+    assert ff._fused_backward_applies(x.clone().requires_grad_(True))
+    xa = x.clone().requires_grad_(True)
+    out = ff(xa)
+    out.backward(gy)
+    xb = x.clone().requires_grad_(True)
+    w = [lin.weight.detach().clone().requires_grad_(True) for lin in (ff.w1, ff.w2, ff.w3)]
+    a1 = torch.nn.functional.linear(xb, w[0])
+    a3 = torch.nn.functional.linear(xb, w[2])
+    a1.retain_grad()
+    a3.retain_grad()
+    ref = torch.nn.functional.linear(torch.nn.functional.silu(a1) * a3, w[1])
+    ref.backward(gy)
+    assert torch.equal(out, ref)
+    assert torch.equal(xa.grad, xb.grad)
+    assert torch.equal(ff.w2.weight.grad, w[1].grad)
+    x2 = x.reshape(n, d).double()
+    for lin, a in ((ff.w1, a1), (ff.w3, a3)):
+        ga = a.grad.reshape(n, hs).double()
+        truth = ga.t() @ x2
+        bound = n * 2.0 ** -24 * (ga.abs().t() @ x2.abs())
+        ulp = 2.0 ** (torch.floor(torch.log2(truth.abs().clamp_min(2.0 ** -126))) - (23 if dtype == torch.float32 else 7))
+        assert ((lin.weight.grad.double() - truth).abs() <= bound + ulp).all()
+
+
+def test_feed_forward_with_bias_keeps_module_autograd():
+    ff = FeedForward.Config(w1=Linear.Config(in_features=8, out_features=6, bias=True),
+                            w2=Linear.Config(in_features=6, out_features=8),
+                            w3=Linear.Config(in_features=8, out_features=6)).build()
+    x = torch.randn(5, 8, requires_grad=True)
+    assert not ff._fused_backward_applies(x)
+    ff(x).sum().backward()
+    assert ff.w1.bias.grad is not None and x.grad is not None
+
+
 KIMI_48B = SimpleNamespace(
     hidden_size=2304, num_experts=256, num_experts_per_token=8, moe_intermediate_size=1024,
     moe_renormalize=True, moe_router_activation_func="sigmoid", num_shared_experts=1,

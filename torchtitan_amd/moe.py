@@ -165,7 +165,15 @@ def _gate_backward_bf16(ctx, grad: torch.Tensor):
         dx = torch.mm(d3, torch.cat([w, w, w], dim=0))  # fp32 accumulation, one rounding to bf16
     if ctx.needs_input_grad[1]:
         e = w.shape[0]
-        dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
+        n = x.shape[0]
+        if n >= 8192 and n % 2 == 0:
+            # two token halves as a batch of two: the [3E, D] output alone is too few
+            # tiles for the chip; the fp32 halves are added before the one rounding
+            dw3 = torch.bmm(d3.view(2, n // 2, 3 * e).transpose(1, 2), x.view(2, n // 2, -1),
+                            out_dtype=torch.float32)
+            dw3 = dw3[0] + dw3[1]
+        else:
+            dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
         dw = ((dw3[:e] + dw3[e:2 * e]) + dw3[2 * e:]).to(w.dtype)
     if ctx.has_bias and ctx.needs_input_grad[2]:
         db = grad.float().sum(0).to(ctx.b_dtype)
