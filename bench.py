@@ -66,6 +66,12 @@ WORKLOADS = {
         score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
         score_before=True, std=0.02, bias=0.01, zipf=1.2,
     ),
+    "kimi_32k": dict(
+        desc="Kimi-shape MoE layer at 32768 tokens, bf16 (the fp8 workloads' token count)",
+        bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,
+        score_func="sigmoid", route_norm=True, route_scale=2.5, groups=None, limited=None,
+        score_before=True, std=0.02, bias=0.01, zipf=None,
+    ),
     "kimi_fp8": dict(
         desc="Kimi-shape MoE layer with fp8 e4m3 grouped GEMMs",
         bs=8, slen=4096, dim=2304, experts=256, top_k=8, hidden=1024, shared_hidden=1024,

@@ -20,12 +20,14 @@
 //    SwiGLU backward), dx (dg . w1 + du . w3, two scaled products added in
 //    bf16), dw13 and dw2 (k = the expert's token group).
 //
-// Tiles: 256 threads, 2 x 2 waves, BM x BN output tile, 128 k per stage.
+// Tiles: 256 x 256 outputs of eight 64 x 128 wave tiles (MXFP8: 128 x 128 of
+// four 64 x 64 wave tiles), 128 k per stage, persistent workgroups.
 // Operands reach LDS by direct-to-LDS copies (global_load_lds_dwordx4, one
 // wave instruction = 8 rows x 128 bytes, coalesced) into row-major 128-byte
 // rows with 16-byte chunk c of row r at c ^ ((r >> 1) & 7), which is
 // conflict-free for the fragment reads; two stages, one barrier per k-step,
-// copies waited for with explicit vmcnt. Each lane's 32-byte MFMA fragment is
+// copies waited for with explicit vmcnt. The copy stream runs through a
+// workgroup's tiles one stage ahead of the MFMAs, across tile boundaries. Each lane's 32-byte MFMA fragment is
 // chunks (lane >> 4) and 4 + (lane >> 4) of its row (any k order is valid as
 // long as both operands share it). Rows past a segment and k past a padded
 // token group are copied from a zero row.
@@ -56,7 +58,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr float kFp8Max = 448.0f;
 constexpr int kPad = 16;
 constexpr int kMaxE = 1024;
-constexpr int kThreads = 256;
 
 // float -> float8_e4m3fn, round to nearest even, saturating at +-448.
 __device__ __forceinline__ uint32_t e4m3(float x) {
@@ -590,29 +591,39 @@ __device__ const uint4 kUnitScales[1] = {{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu,
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// NW waves as WGM x (NW / WGM) wave tiles of (16 TM) x (16 TN), NS LDS stages of
+// 128 k, OCC workgroups per CU. One stream of copy stages runs through this
+// workgroup's tiles NS - 1 stages ahead of the MFMAs, across tile boundaries,
+// so the next tile's first stages are in flight during this tile's epilogue.
 // MX: e8m0 block scales (p.ep / p.eq / p.eq2) applied by the MFMA instead of
-// the fp32 row scales of the epilogues; token groups aligned to 32.
-template <int MODE, int BM, int BN, int OCC, bool MX>
-__global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
+// the fp32 row scales of the epilogues; token groups aligned to 32; 128 x 128
+// tiles of four waves and two stages (the scale copies assume them).
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, int OCC, bool MX>
+__global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
   constexpr bool kRowGrouped = MODE <= kDx;
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
-  constexpr int CPW_P = BM / 8 / 4, CPW_Q = BN / 8 / 4;  // 1 KB copies (8 rows x 128 B) per wave and stage
+  constexpr int WGN = NW / WGM;
+  constexpr int WM = TM * 16, WN = TN * 16, BM = WGM * WM, BN = WGN * WN;
+  constexpr int CPW_P = BM / 8 / NW, CPW_Q = BN / 8 / NW;  // 1 KB copies (8 rows x 128 B) per wave and stage
+  constexpr int CPW = CPW_P + CPW_Q;
   constexpr int PAD = MX ? kMxPad : kPad;
-  static_assert(!MX || (BM == 128 && BN == 128), "the MX scale copies assume 128 x 128 tiles");
+  static_assert(CPW_P * 8 * NW == BM && CPW_Q * 8 * NW == BN && CPW <= 30, "copies per wave");
+  static_assert(NS == 2 || NS == 3, "stages");
+  static_assert(!MX || (NW == 4 && WGM == 2 && BM == 128 && BN == 128 && NS == 2),
+                "the MX scale copies assume 128 x 128 tiles of four waves and two stages");
   static_assert(TN % 2 == 0 && (MODE != kGateUp || TN % 4 == 0), "epilogue block pairs");
-  __shared__ __attribute__((aligned(1024))) uint8_t sP[2][BM * 128];
-  __shared__ __attribute__((aligned(1024))) uint8_t sQ[2][BN * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t sP[NS][BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ[NS][BN * 128];
   // MX scales of a stage: row-grouped, P row m's 4 k-blocks at 4 m and Q row n's
   // at 512 + 4 n; token-transposed, k-block j of P row m at 128 j + m, of Q
   // row n at 512 + 128 j + n
-  __shared__ __attribute__((aligned(16))) uint8_t sS[2][MX ? 1024 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sS[NS][MX ? 1024 : 16];
   __shared__ int s_seg[kMaxE + 1];
   __shared__ int s_pst[kMaxE + 1];
   __shared__ int s_tile[kMaxE + 1];
   __shared__ int s_tmp[8];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv / WGN, wn = wv % WGN;
   const int E = p.E, D = p.D, H = p.H;
   int Ntot = 0, Kfix = 0, Mfix = 0;
   if (MODE == kGateUp) { Ntot = 2 * H; Kfix = D; }
@@ -663,83 +674,90 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
   const int G = gridDim.x;
   const int lb = (G % 8 == 0) ? ((int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
 
-  for (int t = lb; t < total_tiles; t += G) {
+  struct TileRef { int e, seg0, seg1, pst0, mt, nt, klen, nk; };
+  auto decode = [&](int t) {
+    TileRef r;
     int lo = 0, hi = E - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_tile[mid] <= t) lo = mid; else hi = mid - 1;
     }
-    const int e = lo;
-    const int64_t e64 = e;
-    const int local = t - s_tile[e];
-    const int seg0 = s_seg[e], seg1 = s_seg[e + 1];
-    int mt, nt;
+    r.e = lo;
+    const int local = t - s_tile[lo];
+    r.seg0 = s_seg[lo];
+    r.seg1 = s_seg[lo + 1];
+    r.pst0 = s_pst[lo];
     if (kRowGrouped) {
-      const int mtiles = (seg1 - seg0 + BM - 1) / BM;
-      nt = local / mtiles;
-      mt = local - nt * mtiles;
+      const int mtiles = (r.seg1 - r.seg0 + BM - 1) / BM;
+      r.nt = local / mtiles;
+      r.mt = local - r.nt * mtiles;
     } else {
-      nt = local / MT;
-      mt = local - nt * MT;
+      r.nt = local / MT;
+      r.mt = local - r.nt * MT;
     }
-    const int pst0 = s_pst[e];
-    const int Klen = kRowGrouped ? Kfix : (s_pst[e + 1] - pst0);  // bytes of k
-    const int nk = (Klen + 127) / 128;
-    const int row0 = seg0 + mt * BM;
+    r.klen = kRowGrouped ? Kfix : (s_pst[lo + 1] - r.pst0);  // bytes of k
+    r.nk = (r.klen + 127) / 128;
+    return r;
+  };
 
-    // copy sources: lane i of copy c fills row 8 c + i / 8, 16-byte chunk (i % 8),
-    // loading global chunk (i % 8) ^ ((row >> 1) & 7) of that row
-    const int cr = lane >> 3;
-    const uint8_t* srcP[CPW_P];
-    const uint8_t* srcQ[CPW_Q];
-    bool okP[CPW_P];
-    int chP[CPW_P], chQ[CPW_Q];
+  // ---- copy sources of the tile being copied: lane i of copy c fills row 8 c + i / 8,
+  // 16-byte chunk (i % 8), loading global chunk (i % 8) ^ ((row >> 1) & 7) of that row ----
+  const int crow = lane >> 3;
+  const uint8_t* srcP[CPW_P];
+  const uint8_t* srcQ[CPW_Q];
+  bool okP[CPW_P];
+  int chP[CPW_P], chQ[CPW_Q];
+#pragma unroll
+  for (int b = 0; b < CPW_P; ++b) chP[b] = ((lane & 7) ^ ((((wv * CPW_P + b) * 8 + crow) >> 1) & 7)) * 16;
+#pragma unroll
+  for (int b = 0; b < CPW_Q; ++b) chQ[b] = ((lane & 7) ^ ((((wv * CPW_Q + b) * 8 + crow) >> 1) & 7)) * 16;
+  // MX scale copy source of this lane (row-grouped: one dword copy per wave,
+  // waves 0-1 P rows, 2-3 Q rows; token-transposed: one 16-byte copy by wave 0,
+  // lanes 0-31 P, 32-63 Q, each 16 rows of k-block 4 kt + (lane & 31) / 8)
+  const uint8_t* srcS = nullptr;
+  bool okS = false;
+  int64_t kstrideS = 0;
+  auto setup = [&](const TileRef& r) {
+    const int64_t e64 = r.e;
+    const int row0 = r.seg0 + r.mt * BM;
 #pragma unroll
     for (int b = 0; b < CPW_P; ++b) {
-      const int m = (wv * CPW_P + b) * 8 + cr;
-      chP[b] = ((lane & 7) ^ ((m >> 1) & 7)) * 16;
+      const int m = (wv * CPW_P + b) * 8 + crow;
       if (kRowGrouped) {
-        const int r = row0 + m;
-        okP[b] = r < seg1;
-        srcP[b] = p.qp + (int64_t)r * Kfix + chP[b];
+        const int rr = row0 + m;
+        okP[b] = rr < r.seg1;
+        srcP[b] = p.qp + (int64_t)rr * Kfix + chP[b];
       } else {
         okP[b] = true;
-        srcP[b] = p.qp + (int64_t)(mt * BM + m) * p.Rpad + pst0 + chP[b];
+        srcP[b] = p.qp + (int64_t)(r.mt * BM + m) * p.Rpad + r.pst0 + chP[b];
       }
     }
 #pragma unroll
     for (int b = 0; b < CPW_Q; ++b) {
-      const int n = (wv * CPW_Q + b) * 8 + cr;
-      chQ[b] = ((lane & 7) ^ ((n >> 1) & 7)) * 16;
+      const int n = (wv * CPW_Q + b) * 8 + crow;
       const uint8_t* rowp;
       if (MODE == kGateUp) {
         const int blk = n >> 4;
-        const int hc = nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
+        const int hc = r.nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
         rowp = ((blk & 1) ? p.qq2 : p.qq) + (e64 * H + hc) * (int64_t)D;
       } else if (MODE == kDown) {
-        rowp = p.qq + (e64 * D + nt * BN + n) * (int64_t)H;
+        rowp = p.qq + (e64 * D + r.nt * BN + n) * (int64_t)H;
       } else if (MODE == kDgu) {
-        rowp = p.qq + (e64 * H + nt * BN + n) * (int64_t)D;
+        rowp = p.qq + (e64 * H + r.nt * BN + n) * (int64_t)D;
       } else if (MODE == kDx) {
-        rowp = p.qq + (e64 * D + nt * BN + n) * (int64_t)(2 * H);
+        rowp = p.qq + (e64 * D + r.nt * BN + n) * (int64_t)(2 * H);
       } else {
-        rowp = p.qq + (int64_t)(nt * BN + n) * p.Rpad + pst0;
+        rowp = p.qq + (int64_t)(r.nt * BN + n) * p.Rpad + r.pst0;
       }
       srcQ[b] = rowp + chQ[b];
     }
-    // MX scale copy source of this lane (row-grouped: one dword copy per wave,
-    // waves 0-1 P rows, 2-3 Q rows; token-transposed: one 16-byte copy by wave 0,
-    // lanes 0-31 P, 32-63 Q, each 16 rows of k-block 4 kt + (lane & 31) / 8)
-    const uint8_t* srcS = nullptr;
-    bool okS = false;
-    int64_t kstrideS = 0;
     if (MX) {
       if (kRowGrouped) {
         const int kb_row = Kfix / kMxBlock;  // scale bytes per row
         if (wv < 2) {
-          const int r = row0 + wv * 64 + lane;
-          okS = r < seg1;
-          srcS = p.ep + (int64_t)r * kb_row;
+          const int rr = row0 + wv * 64 + lane;
+          okS = rr < r.seg1;
+          srcS = p.ep + (int64_t)rr * kb_row;
         } else {
           const int n = (wv - 2) * 64 + lane;
           okS = true;
@@ -747,46 +765,77 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
           const uint8_t* base = p.eq;
           if (MODE == kGateUp) {
             const int blk = n >> 4;
-            qrow = e64 * H + nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
+            qrow = e64 * H + r.nt * (BN / 2) + (blk >> 1) * 16 + (n & 15);
             if (blk & 1) base = p.eq2;
           } else if (MODE == kDown) {
-            qrow = e64 * D + nt * BN + n;
+            qrow = e64 * D + r.nt * BN + n;
           } else if (MODE == kDgu) {
-            qrow = e64 * H + nt * BN + n;
+            qrow = e64 * H + r.nt * BN + n;
           } else {
-            qrow = e64 * D + nt * BN + n;
+            qrow = e64 * D + r.nt * BN + n;
           }
           srcS = base + qrow * kb_row;
         }
       } else {
         const int sub = lane & 31;
-        const int64_t kb0 = pst0 / kMxBlock + (sub >> 3);
+        const int64_t kb0 = r.pst0 / kMxBlock + (sub >> 3);
         kstrideS = lane < 32 ? Mfix : Ntot;
-        srcS = (lane < 32 ? p.ep + kb0 * Mfix + mt * BM : p.eq + kb0 * Ntot + nt * BN) + (sub & 7) * 16;
+        srcS = (lane < 32 ? p.ep + kb0 * Mfix + r.mt * BM : p.eq + kb0 * Ntot + r.nt * BN) + (sub & 7) * 16;
       }
     }
-    auto issue = [&](int kt) {
-      const int s = kt & 1;
-      const int k0 = kt * 128;
+  };
+  // stage kt of tile r into LDS buffer s
+  auto issue = [&](const TileRef& r, int kt, int s) {
+    const int k0 = kt * 128;
 #pragma unroll
-      for (int b = 0; b < CPW_P; ++b) {
-        const bool ok = okP[b] && k0 + chP[b] < Klen;
-        dma16(ok ? (const void*)(srcP[b] + k0) : (const void*)kZeroRow, lds_addr(&sP[s][(wv * CPW_P + b) * 1024]));
-      }
+    for (int b = 0; b < CPW_P; ++b) {
+      const bool ok = okP[b] && k0 + chP[b] < r.klen;
+      dma16(ok ? (const void*)(srcP[b] + k0) : (const void*)kZeroRow, lds_addr(&sP[s][(wv * CPW_P + b) * 1024]));
+    }
 #pragma unroll
-      for (int b = 0; b < CPW_Q; ++b) {
-        const bool ok = k0 + chQ[b] < Klen;
-        dma16(ok ? (const void*)(srcQ[b] + k0) : (const void*)kZeroRow, lds_addr(&sQ[s][(wv * CPW_Q + b) * 1024]));
+    for (int b = 0; b < CPW_Q; ++b) {
+      const bool ok = k0 + chQ[b] < r.klen;
+      dma16(ok ? (const void*)(srcQ[b] + k0) : (const void*)kZeroRow, lds_addr(&sQ[s][(wv * CPW_Q + b) * 1024]));
+    }
+    if (MX) {
+      if (kRowGrouped) {
+        dma4(okS ? (const void*)(srcS + kt * 4) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 256]));
+      } else if (wv == 0) {
+        const bool ok = (4 * kt + ((lane & 31) >> 3)) * kMxBlock < r.klen;
+        dma16(ok ? (const void*)(srcS + 4 * kt * kstrideS) : (const void*)kUnitScales, lds_addr(&sS[s][0]));
       }
-      if (MX) {
-        if (kRowGrouped) {
-          dma4(okS ? (const void*)(srcS + kt * 4) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 256]));
-        } else if (wv == 0) {
-          const bool ok = (4 * kt + ((lane & 31) >> 3)) * kMxBlock < Klen;
-          dma16(ok ? (const void*)(srcS + 4 * kt * kstrideS) : (const void*)kUnitScales, lds_addr(&sS[s][0]));
-        }
+    }
+  };
+  // the copy cursor: tile ct_i, its stage ik; stage g goes to LDS buffer g % NS.
+  // Tiles without k-steps (dW of an expert without tokens) have no stages.
+  int ct_i = lb, ik = 0, gi = 0, gc = 0;
+  TileRef ir{};
+  auto seek = [&](int t0) {
+    for (ct_i = t0; ct_i < total_tiles; ct_i += G) {
+      ir = decode(ct_i);
+      if (ir.nk > 0) {
+        setup(ir);
+        break;
       }
-    };
+    }
+    ik = 0;
+  };
+  auto issue_next = [&]() {
+    issue(ir, ik, gi % NS);
+    ++gi;
+    if (++ik == ir.nk) seek(ct_i + G);
+  };
+  seek(lb);
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (ct_i < total_tiles) issue_next();
+
+  for (int t = lb; t < total_tiles; t += G) {
+    const TileRef cur = decode(t);
+    const int e = cur.e;
+    const int64_t e64 = e;
+    const int seg1 = cur.seg1, mt = cur.mt, nt = cur.nt, nk = cur.nk;
+    const int row0 = cur.seg0 + mt * BM;
 
     f32x4_t acc[TM][TN];
 #pragma unroll
@@ -857,17 +906,17 @@ __global__ __launch_bounds__(kThreads, OCC) void fp8_gemm_kernel(Params p) {
     };
     const int kt_half = (MODE == kDx) ? H / 128 : -1;
 
-    // the previous tile's LDS reads are done in every wave
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (nk > 0) issue(0);
     for (int kt = 0; kt < nk; ++kt) {
-      // stage kt has landed in every wave; the reads of the other buffer are retired
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (kt + 1 < nk) issue(kt + 1);
+      // stage gc has landed in every wave once at most the one stage issued after it
+      // is outstanding (stores of an epilogue or of the dx park only add to the
+      // count); the barrier also retires every wave's reads of the buffer refilled next
+      if (NS == 3 && gi - gc >= 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(CPW) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (ct_i < total_tiles) issue_next();
       if (MODE == kDx && kt == kt_half) park_dx_half();
-      compute(kt & 1);
+      compute(gc % NS);
+      ++gc;
     }
-
     // ---- epilogues: lane holds C[m = .. + ml][n = .. + nql + 0..3]; pairs of
     // 16-column blocks are stored as 64-byte row pieces (span64) at column
     // 32 jp + 8 (lane / 16) of the wave's span ----
@@ -1022,21 +1071,30 @@ static int cu_count() {
   return g_cus[dev];
 }
 
-constexpr int kBM = 128, kBN = 128, kOcc = 2;
-
-template <int MODE, bool MX = false>
-static void launch(const Params& p, hipStream_t stream) {
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, int OCC, bool MX>
+static void launch_cfg(const Params& p, hipStream_t stream) {
+  constexpr int BM = WGM * TM * 16, BN = (NW / WGM) * TN * 16;
   int64_t max_tiles;
-  if (MODE == kGateUp) max_tiles = (p.R / kBM + p.E) * (2 * p.H / kBN);
-  else if (MODE == kDown || MODE == kDx) max_tiles = (p.R / kBM + p.E) * (p.D / kBN);
-  else if (MODE == kDgu) max_tiles = (p.R / kBM + p.E) * (p.H / kBN);
-  else if (MODE == kDw13) max_tiles = (int64_t)p.E * (2 * p.H / kBM) * (p.D / kBN);
-  else max_tiles = (int64_t)p.E * (p.D / kBM) * (p.H / kBN);
-  int64_t g = (int64_t)cu_count() * kOcc;
+  if (MODE == kGateUp) max_tiles = (p.R / BM + p.E) * (2 * p.H / BN);
+  else if (MODE == kDown || MODE == kDx) max_tiles = (p.R / BM + p.E) * (p.D / BN);
+  else if (MODE == kDgu) max_tiles = (p.R / BM + p.E) * (p.H / BN);
+  else if (MODE == kDw13) max_tiles = (int64_t)p.E * (2 * p.H / BM) * (p.D / BN);
+  else max_tiles = (int64_t)p.E * (p.D / BM) * (p.H / BN);
+  int64_t g = (int64_t)cu_count() * OCC;
   if (g > max_tiles) g = max_tiles;
   if (g >= 8) g -= g % 8;
   if (g < 1) g = 1;
-  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, kBM, kBN, kOcc, MX>), dim3((int)g), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((fp8_gemm_kernel<MODE, NW, WGM, TM, TN, NS, OCC, MX>), dim3((int)g), dim3(NW * 64), 0, stream, p);
+}
+
+// Tiles (measured at the Kimi shape, 32768 tokens): 256 x 256 outputs of eight
+// 64 x 128 wave tiles, two 64 KB stages, one workgroup per CU -- half the copy
+// bytes per MFMA of 128 x 128 tiles (the six GEMMs 11.5 -> 9.8 ms); MXFP8 keeps
+// 128 x 128 tiles of four waves, two per CU.
+template <int MODE, bool MX = false>
+static void launch(const Params& p, hipStream_t stream) {
+  if constexpr (MX) launch_cfg<MODE, 4, 2, 4, 4, 2, 2, true>(p, stream);
+  else launch_cfg<MODE, 8, 4, 4, 8, 2, 1, false>(p, stream);
 }
 
 static int check_shape(int64_t R, int E, int D, int H) {
