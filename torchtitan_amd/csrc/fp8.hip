@@ -20,8 +20,8 @@
 //    SwiGLU backward), dx (dg . w1 + du . w3, two scaled products added in
 //    bf16), dw13 and dw2 (k = the expert's token group).
 //
-// Tiles: 256 x 256 outputs of eight 64 x 128 wave tiles (MXFP8: 128 x 128 of
-// four 64 x 64 wave tiles), 128 k per stage, persistent workgroups.
+// Tiles: 256 x 256 outputs of eight 64 x 128 wave tiles, 128 k per stage,
+// persistent workgroups.
 // Operands reach LDS by direct-to-LDS copies (global_load_lds_dwordx4, one
 // wave instruction = 8 rows x 128 bytes, coalesced) into row-major 128-byte
 // rows with 16-byte chunk c of row r at c ^ ((r >> 1) & 7), which is
@@ -596,8 +596,8 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 // workgroup's tiles NS - 1 stages ahead of the MFMAs, across tile boundaries,
 // so the next tile's first stages are in flight during this tile's epilogue.
 // MX: e8m0 block scales (p.ep / p.eq / p.eq2) applied by the MFMA instead of
-// the fp32 row scales of the epilogues; token groups aligned to 32; 128 x 128
-// tiles of four waves and two stages (the scale copies assume them).
+// the fp32 row scales of the epilogues; token groups aligned to 32; BM = BN =
+// 32 NW and two stages (the scale copies assume them).
 template <int MODE, int NW, int WGM, int TM, int TN, int NS, int OCC, bool MX>
 __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
   constexpr bool kRowGrouped = MODE <= kDx;
@@ -608,15 +608,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
   constexpr int PAD = MX ? kMxPad : kPad;
   static_assert(CPW_P * 8 * NW == BM && CPW_Q * 8 * NW == BN && CPW <= 30, "copies per wave");
   static_assert(NS == 2 || NS == 3, "stages");
-  static_assert(!MX || (NW == 4 && WGM == 2 && BM == 128 && BN == 128 && NS == 2),
-                "the MX scale copies assume 128 x 128 tiles of four waves and two stages");
+  static_assert(!MX || (BM == 32 * NW && BN == 32 * NW && NS == 2),
+                "the MX scale copies assume BM = BN = 32 NW (one dword per row and wave lane) and two stages");
   static_assert(TN % 2 == 0 && (MODE != kGateUp || TN % 4 == 0), "epilogue block pairs");
   __shared__ __attribute__((aligned(1024))) uint8_t sP[NS][BM * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ[NS][BN * 128];
   // MX scales of a stage: row-grouped, P row m's 4 k-blocks at 4 m and Q row n's
-  // at 512 + 4 n; token-transposed, k-block j of P row m at 128 j + m, of Q
-  // row n at 512 + 128 j + n
-  __shared__ __attribute__((aligned(16))) uint8_t sS[NS][MX ? 1024 : 16];
+  // at 4 BM + 4 n; token-transposed, k-block j of P row m at BM j + m, of Q
+  // row n at 4 BM + BN j + n
+  __shared__ __attribute__((aligned(16))) uint8_t sS[NS][MX ? 4 * (BM + BN) : 16];
   __shared__ int s_seg[kMaxE + 1];
   __shared__ int s_pst[kMaxE + 1];
   __shared__ int s_tile[kMaxE + 1];
@@ -711,12 +711,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
   for (int b = 0; b < CPW_P; ++b) chP[b] = ((lane & 7) ^ ((((wv * CPW_P + b) * 8 + crow) >> 1) & 7)) * 16;
 #pragma unroll
   for (int b = 0; b < CPW_Q; ++b) chQ[b] = ((lane & 7) ^ ((((wv * CPW_Q + b) * 8 + crow) >> 1) & 7)) * 16;
-  // MX scale copy source of this lane (row-grouped: one dword copy per wave,
-  // waves 0-1 P rows, 2-3 Q rows; token-transposed: one 16-byte copy by wave 0,
-  // lanes 0-31 P, 32-63 Q, each 16 rows of k-block 4 kt + (lane & 31) / 8)
+  // MX scale copy source of this lane. Row-grouped: one dword copy per wave, the
+  // first NW / 2 waves P rows 64 wv + lane, the others Q rows. Token-transposed:
+  // one 16-byte copy by each lane gl = 64 wv + lane < (BM + BN) / 4 (the first NW / 4
+  // waves), gl < BM / 4 P, the rest Q, each 16 rows of one k-block kbS of the stage.
   const uint8_t* srcS = nullptr;
   bool okS = false;
   int64_t kstrideS = 0;
+  int kbS = 0;
   auto setup = [&](const TileRef& r) {
     const int64_t e64 = r.e;
     const int row0 = r.seg0 + r.mt * BM;
@@ -754,12 +756,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
     if (MX) {
       if (kRowGrouped) {
         const int kb_row = Kfix / kMxBlock;  // scale bytes per row
-        if (wv < 2) {
+        if (wv < NW / 2) {
           const int rr = row0 + wv * 64 + lane;
           okS = rr < r.seg1;
           srcS = p.ep + (int64_t)rr * kb_row;
         } else {
-          const int n = (wv - 2) * 64 + lane;
+          const int n = (wv - NW / 2) * 64 + lane;
           okS = true;
           int64_t qrow;
           const uint8_t* base = p.eq;
@@ -777,10 +779,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
           srcS = base + qrow * kb_row;
         }
       } else {
-        const int sub = lane & 31;
-        const int64_t kb0 = r.pst0 / kMxBlock + (sub >> 3);
-        kstrideS = lane < 32 ? Mfix : Ntot;
-        srcS = (lane < 32 ? p.ep + kb0 * Mfix + r.mt * BM : p.eq + kb0 * Ntot + r.nt * BN) + (sub & 7) * 16;
+        const int gl = wv * 64 + lane;
+        const bool isP = gl < BM / 4;
+        const int sub = isP ? gl : gl - BM / 4;
+        const int cpk = isP ? BM / 16 : BN / 16;  // 16-byte chunks per k-block
+        kbS = sub / cpk;
+        const int64_t kb0 = r.pst0 / kMxBlock + kbS;
+        kstrideS = isP ? Mfix : Ntot;
+        srcS = (isP ? p.ep + kb0 * Mfix + r.mt * BM : p.eq + kb0 * Ntot + r.nt * BN) + (sub % cpk) * 16;
       }
     }
   };
@@ -800,9 +806,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
     if (MX) {
       if (kRowGrouped) {
         dma4(okS ? (const void*)(srcS + kt * 4) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 256]));
-      } else if (wv == 0) {
-        const bool ok = (4 * kt + ((lane & 31) >> 3)) * kMxBlock < r.klen;
-        dma16(ok ? (const void*)(srcS + 4 * kt * kstrideS) : (const void*)kUnitScales, lds_addr(&sS[s][0]));
+      } else if (wv < NW / 4) {
+        const bool ok = (4 * kt + kbS) * kMxBlock < r.klen;
+        dma16(ok ? (const void*)(srcS + 4 * kt * kstrideS) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 1024]));
       }
     }
   };
@@ -850,12 +856,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
           const int m = wm * WM + i * 16 + ml;
-          scp[i] = sS[s][kRowGrouped ? m * 4 + g4 : g4 * 128 + m];
+          scp[i] = sS[s][kRowGrouped ? m * 4 + g4 : g4 * BM + m];
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int n = wn * WN + j * 16 + ml;
-          scq[j] = sS[s][kRowGrouped ? 512 + n * 4 + g4 : 512 + g4 * 128 + n];
+          scq[j] = sS[s][kRowGrouped ? 4 * BM + n * 4 + g4 : 4 * BM + g4 * BN + n];
         }
       }
       v8i_t af[TM];
@@ -1089,12 +1095,12 @@ static void launch_cfg(const Params& p, hipStream_t stream) {
 
 // Tiles (measured at the Kimi shape, 32768 tokens): 256 x 256 outputs of eight
 // 64 x 128 wave tiles, two 64 KB stages, one workgroup per CU -- half the copy
-// bytes per MFMA of 128 x 128 tiles (the six GEMMs 11.5 -> 9.8 ms); MXFP8 keeps
-// 128 x 128 tiles of four waves, two per CU.
+// bytes per MFMA of 128 x 128 tiles of four waves (six GEMMs: fp8 11.4 -> 9.6 ms,
+// MXFP8 10.9 -> 9.0 ms). D and H are multiples of 256 (check_shape), so every
+// n-tile and dW m-tile is whole.
 template <int MODE, bool MX = false>
 static void launch(const Params& p, hipStream_t stream) {
-  if constexpr (MX) launch_cfg<MODE, 4, 2, 4, 4, 2, 2, true>(p, stream);
-  else launch_cfg<MODE, 8, 4, 4, 8, 2, 1, false>(p, stream);
+  launch_cfg<MODE, 8, 4, 4, 8, 2, 1, MX>(p, stream);
 }
 
 static int check_shape(int64_t R, int E, int D, int H) {
