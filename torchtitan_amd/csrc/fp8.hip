@@ -252,13 +252,14 @@ constexpr int kTRows = 128;  // slab rows transposed per pass
 //  * ROWS (MX): the same read also quantizes the slab along its columns (the
 //    row-wise MX layout, blocks of 32 columns): row r's 64 values go to
 //    qr + r * ldr and its two block scales to sr + r * ldsr.
-// A pass moves 128 rows (four 16-byte loads per thread) through s_tile
+// A pass moves 128 rows (four 16-byte loads per thread, double-buffered in
+// registers so that two passes' loads are in flight) through s_tile
 // (128 row-major rows of 128 bytes, written with 16-byte stores, the 16-byte
 // chunk c of row r at c ^ ((r / 16) % 8)). Each thread then quantizes two units
 // of 16 rows of one column (2-byte reads; the swizzle keeps the eight row
 // groups a wave reads at once in distinct banks) and stores their 16 bytes, so
 // that 8 consecutive lanes write 128 contiguous bytes of one output row. The
-// next pass's loads are issued as soon as the tile is in LDS.
+// loads two passes ahead are issued as soon as the tile is in LDS.
 template <bool MX, bool ROWS>
 __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows, int n_out,
                                              uint8_t* __restrict__ out, int64_t ldo, uint8_t* __restrict__ sc,
@@ -266,8 +267,8 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
                                              uint8_t* __restrict__ qr = nullptr, int64_t ldr = 0,
                                              uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0) {
   const int t = threadIdx.x;
-  uint4 v[4];
-  auto load = [&](int a0) {
+  uint4 va[4], vb[4];
+  auto load = [&](uint4 (&v)[4], int a0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * 256;
@@ -275,8 +276,9 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
     }
   };
-  if (n_out > 0) load(0);
-  for (int a0 = 0; a0 < n_out; a0 += kTRows) {
+  // one pass of 128 rows held in v; v is reloaded with the pass two ahead as soon
+  // as it is in LDS, so two passes' loads are in flight while one is transposed
+  auto pass = [&](uint4 (&v)[4], int a0) {
     const uint32_t nan = has_nan8(v[0]) | has_nan8(v[1]) | has_nan8(v[2]) | has_nan8(v[3]);
     if constexpr (ROWS) {
       const bool rows_fast = wave_nan_free(nan);
@@ -303,7 +305,7 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       *(uint4*)(s_tile + r * 32 + (((c & 7) ^ ((r >> 4) & 7)) * 4)) = v[i];
     }
     const bool fast = !__syncthreads_or(nan != 0u);  // block-uniform: the tile holds no NaN
-    if (a0 + kTRows < n_out) load(a0 + kTRows);
+    if (a0 + 2 * kTRows < n_out) load(v, a0 + 2 * kTRows);
     // unit (column cc, rows 16 kq .. 16 kq + 15 of the pass): 8 consecutive lanes cover one
     // output row's 128 bytes, so every store instruction writes 8 rows x 128 contiguous bytes
 #pragma unroll
@@ -347,6 +349,12 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
           if ((kq & 1) == 0) sc[(int64_t)cc * sc_b + (int64_t)(rb / kMxBlock) * sc_k] = (uint8_t)e;
       }
     }
+  };
+  if (n_out > 0) load(va, 0);
+  if (n_out > kTRows) load(vb, kTRows);
+  for (int a0 = 0; a0 < n_out; a0 += 2 * kTRows) {
+    pass(va, a0);
+    if (a0 + kTRows < n_out) pass(vb, a0 + kTRows);
   }
 }
 
