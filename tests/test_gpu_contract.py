@@ -25,6 +25,7 @@ import torch
 import torchtitan_amd.moe as moe_module
 from tests.conftest import banner
 from torchtitan_amd import FeedForward, GroupedExperts, Linear, MoE, TokenChoiceTopKRouter, ops
+from torchtitan_amd.feed_forward import swiglu_ffn_backward
 
 pytestmark = pytest.mark.gpu
 
@@ -138,6 +139,15 @@ def _opcheck_cases(dev):
     cases["grouped_swiglu_oss_backward"] = (ops.grouped_swiglu_oss_backward,
                                             (bf(r, d), x, m1.detach(), b1.detach(), m2.detach(), b2.detach(), counts,
                                              og, ou, oh, 7.0))
+    # the shared expert's backward (feed_forward.swiglu_ffn_backward) on its forward's intermediates
+    hs = 128
+    xs, sw1, sw2, sw3 = bf(n, d), bf(hs, d, scale=0.05), bf(d, hs, scale=0.05), bf(hs, d, scale=0.05)
+    a1, a3 = torch.nn.functional.linear(xs, sw1), torch.nn.functional.linear(xs, sw3)
+    sl = torch.nn.functional.silu(a1)
+    cases["swiglu_ffn_backward"] = (swiglu_ffn_backward, (bf(n, d), xs, sw1, sw2, sw3, a1, a3, sl, sl * a3,
+                                                          True, True, True))
+    cases["swiglu_ffn_backward_dw_only"] = (swiglu_ffn_backward, (bf(n, d), xs, sw1, sw2, sw3, a1, a3, sl, sl * a3,
+                                                                  False, True, True))
     return cases
 
 
@@ -146,13 +156,13 @@ OPCHECK_NAMES = ["router", "router_backward", "reorder", "reorder_backward", "pe
                  "grouped_swiglu_f32", "grouped_swiglu_f32_backward",
                  "grouped_swiglu_fp8", "grouped_swiglu_fp8_backward", "grouped_swiglu_mxfp8",
                  "grouped_swiglu_mxfp8_backward", "grouped_swiglu_oss", "grouped_swiglu_oss_backward",
-                 "gather_rows", "scatter_rows"]
+                 "gather_rows", "scatter_rows", "swiglu_ffn_backward", "swiglu_ffn_backward_dw_only"]
 
 
 def test_opcheck_covers_every_op():
     ns = torch.ops.moe_mi355x
     registered = {n for n in dir(ns) if isinstance(getattr(ns, n, None), torch._ops.OpOverloadPacket)}
-    checked = {n.replace("_no_shared", "") for n in OPCHECK_NAMES}
+    checked = {n.replace("_no_shared", "").replace("_dw_only", "") for n in OPCHECK_NAMES}
     assert registered <= checked, registered - checked
 
 

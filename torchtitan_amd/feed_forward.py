@@ -22,6 +22,48 @@ def compute_ffn_hidden_dim(dim: int, *, multiple_of: int = 1, ffn_dim_multiplier
     return multiple_of * ((hidden + multiple_of - 1) // multiple_of)
 
 
+@torch.library.custom_op("moe_mi355x::swiglu_ffn_backward", mutates_args=())
+def swiglu_ffn_backward(
+    dy: torch.Tensor, x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor,
+    a1: torch.Tensor, a3: torch.Tensor, s: torch.Tensor, h: torch.Tensor,
+    need_dx: bool, need_dw13: bool, need_dw2: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dx, [dW1; dW3], dW2) of w2(silu(w1 x) * w3 x) from the forward's a1 = w1 x,
+    a3 = w3 x, s = silu(a1) and h = s * a3; unrequested results are empty.
+
+    dh = dy w2, dW2 = dy^T h, du = dh * s and dg = silu_backward(dh * a3, a1) are
+    autograd's own calls and roundings, dx = (dg w1) + (du w3) its sum. dg and du
+    are written side by side into one [tokens, 2 Hs] buffer, so [dW1; dW3] is a
+    single dgu^T x GEMM (fp32 accumulation, one rounding per element). A custom op,
+    so that a compiled graph calls it whole: the side-by-side writes are out=
+    views that graph capture does not trace."""
+    d, hs = x.shape[-1], w1.shape[0]
+    x2, dy2 = x.reshape(-1, d), dy.reshape(-1, d)
+    empty = x.new_empty(0)
+    dh = dy2.mm(w2)
+    dw2 = dy2.t().mm(h.reshape(-1, hs)) if need_dw2 else empty
+    dgu = torch.empty(x2.shape[0], 2 * hs, dtype=dh.dtype, device=dh.device)
+    dg, du = dgu[:, :hs], dgu[:, hs:]
+    torch.mul(dh, s.reshape(-1, hs), out=du)
+    dsilu = dh * a3.reshape(-1, hs)
+    if dg.device.type == "cpu":
+        # the CPU's vectorised kernel (contiguous output) and its strided one
+        # evaluate exp differently; the GPU's elementwise kernels do not
+        dg.copy_(torch.ops.aten.silu_backward(dsilu, a1.reshape(-1, hs)))
+    else:
+        torch.ops.aten.silu_backward.grad_input(dsilu, a1.reshape(-1, hs), grad_input=dg)
+    dx = (dg.mm(w1) + du.mm(w3)).view(x.shape) if need_dx else empty.clone()
+    dw13 = dgu.t().mm(x2) if need_dw13 else empty.clone()
+    return dx, dw13, dw2
+
+
+@swiglu_ffn_backward.register_fake
+def _(dy, x, w1, w2, w3, a1, a3, s, h, need_dx, need_dw13, need_dw2):
+    hs, d = w1.shape
+    return (x.new_empty(x.shape if need_dx else (0,)), x.new_empty((2 * hs, d) if need_dw13 else (0,)),
+            x.new_empty((d, hs) if need_dw2 else (0,)))
+
+
 class _SwiGLUFFN(torch.autograd.Function):
     """w2(silu(w1 x) * w3 x) for bias-free projections, with one GEMM for the
     weight gradients of w1 and w3.
@@ -30,11 +72,11 @@ class _SwiGLUFFN(torch.autograd.Function):
     modules (feed_forward.py:53-54), so the output is theirs bit for bit.
     Backward: dh = dy w2, dW2 = dy^T h, dx = (dg w1) + (du w3) and the SwiGLU
     derivative (dg = silu_backward(dh * u, g), du = dh * silu(g)) are autograd's
-    own calls and roundings. dg and du are written side by side into one
-    [tokens, 2 Hs] buffer, so dW1 and dW3 come out of a single dgu^T x GEMM
-    (fp32 accumulation, one rounding per element, as each of autograd's two):
-    a 2 Hs-row output fills the chip where two Hs-row outputs leave most
-    compute units idle (1024 x 2304 is 144 library tiles on 256 CUs)."""
+    own calls and roundings (swiglu_ffn_backward). dg and du are written side by
+    side into one [tokens, 2 Hs] buffer, so dW1 and dW3 come out of a single
+    dgu^T x GEMM (fp32 accumulation, one rounding per element, as each of
+    autograd's two): a 2 Hs-row output fills the chip where two Hs-row outputs
+    leave most compute units idle (1024 x 2304 is 144 library tiles on 256 CUs)."""
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> torch.Tensor:
@@ -48,26 +90,11 @@ class _SwiGLUFFN(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy: torch.Tensor):
         x, w1, w2, w3, a1, a3, s, h = ctx.saved_tensors
-        d, hs = x.shape[-1], w1.shape[0]
-        x2, dy2 = x.reshape(-1, d), dy.reshape(-1, d)
-        dh = dy2.mm(w2)
-        dw2 = dy2.t().mm(h.reshape(-1, hs)) if ctx.needs_input_grad[2] else None
-        dgu = torch.empty(x2.shape[0], 2 * hs, dtype=dh.dtype, device=dh.device)
-        dg, du = dgu[:, :hs], dgu[:, hs:]
-        torch.mul(dh, s.reshape(-1, hs), out=du)
-        dsilu = dh * a3.reshape(-1, hs)
-        if dg.device.type == "cpu":
-            # the CPU's vectorised kernel (contiguous output) and its strided one
-            # evaluate exp differently; the GPU's elementwise kernels do not
-            dg.copy_(torch.ops.aten.silu_backward(dsilu, a1.reshape(-1, hs)))
-        else:
-            torch.ops.aten.silu_backward.grad_input(dsilu, a1.reshape(-1, hs), grad_input=dg)
-        dx = (dg.mm(w1) + du.mm(w3)).view(x.shape) if ctx.needs_input_grad[0] else None
-        dw1 = dw3 = None
-        if ctx.needs_input_grad[1] or ctx.needs_input_grad[3]:
-            dw13 = dgu.t().mm(x2)
-            dw1, dw3 = dw13[:hs], dw13[hs:]
-        return dx, dw1, dw2, dw3
+        need = ctx.needs_input_grad
+        dx, dw13, dw2 = swiglu_ffn_backward(dy, x, w1, w2, w3, a1, a3, s, h, need[0], need[1] or need[3], need[2])
+        hs = w1.shape[0]
+        return (dx if need[0] else None, dw13[:hs] if need[1] else None, dw2 if need[2] else None,
+                dw13[hs:] if need[3] else None)
 
 
 class FeedForward(Module):
