@@ -208,13 +208,15 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
   }
 }
 
-// Column amax over `n_rows` rows of a 64-column slab (row stride ld elements)
-// -> s_amax[64]; every thread of the block calls it. Four independent 16-byte
+// Column amax over `n_rows` rows of a COLS-column slab (row stride ld elements)
+// -> s_amax[COLS]; every thread of the 4 COLS-thread block calls it. Four independent 16-byte
 // loads per thread are in flight per iteration.
+template <int COLS>
 __device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int64_t ld, int n_rows, float* s_red,
                                           float* s_amax) {
   const int t = threadIdx.x;
-  const int ch = t & 7, r0 = t >> 3;  // 8 chunks of 8 columns, 32 rows per sweep
+  constexpr int CPR = COLS / 8;
+  const int ch = t % CPR, r0 = t / CPR;  // CPR chunks of 8 columns, 32 rows per sweep
   float m[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) m[i] = 0.f;
@@ -234,7 +236,7 @@ __device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int
 #pragma unroll
   for (int i = 0; i < 8; ++i) s_red[(ch * 8 + i) * 33 + r0] = m[i];
   __syncthreads();
-  if (t < 64) {
+  if (t < COLS) {
     float a = 0.f;
     for (int j = 0; j < 32; ++j) a = fmaxf(a, s_red[t * 33 + j]);
     s_amax[t] = a;
@@ -244,35 +246,39 @@ __device__ __forceinline__ void slab_amax(const uint16_t* __restrict__ base, int
 
 constexpr int kTRows = 128;  // slab rows transposed per pass
 
-// Quantizes a [n_rows x 64] bf16 slab (row stride ld) transposed: output row b
+// Quantizes a [n_rows x COLS] bf16 slab (row stride ld; COLS 64 or 128, a block of
+// 4 COLS threads) transposed: output row b
 // (slab column b) holds n_out values at out + b * ldo, rows >= n_rows zero
 // (n_out a multiple of 16, and of 32 for MX).
 //  * fp8 (MX false): column b scaled by s_col[b];
 //  * MX: one e8m0 scale per (column b, 32-row block k) at sc + b * sc_b + k * sc_k;
 //  * ROWS (MX): the same read also quantizes the slab along its columns (the
-//    row-wise MX layout, blocks of 32 columns): row r's 64 values go to
-//    qr + r * ldr and its two block scales to sr + r * ldsr.
+//    row-wise MX layout, blocks of 32 columns): row r's COLS values go to
+//    qr + r * ldr and its COLS / 32 block scales to sr + r * ldsr.
 // A pass moves 128 rows (four 16-byte loads per thread, double-buffered in
 // registers so that two passes' loads are in flight) through s_tile
-// (128 row-major rows of 128 bytes, written with 16-byte stores, the 16-byte
+// (128 row-major rows of 2 COLS bytes, written with 16-byte stores, the 16-byte
 // chunk c of row r at c ^ ((r / 16) % 8)). Each thread then quantizes two units
 // of 16 rows of one column (2-byte reads; the swizzle keeps the eight row
 // groups a wave reads at once in distinct banks) and stores their 16 bytes, so
 // that 8 consecutive lanes write 128 contiguous bytes of one output row. The
-// loads two passes ahead are issued as soon as the tile is in LDS.
-template <bool MX, bool ROWS>
+// loads two passes ahead are issued as soon as the tile is in LDS. 128-column
+// slabs (launched whenever the width allows) write the row-wise layout in whole
+// 128-byte lines: 2-12 % faster than 64-column ones at the Kimi shapes.
+template <bool MX, bool ROWS, int COLS>
 __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows, int n_out,
                                              uint8_t* __restrict__ out, int64_t ldo, uint8_t* __restrict__ sc,
                                              int64_t sc_b, int64_t sc_k, const float* s_col, uint32_t* s_tile,
                                              uint8_t* __restrict__ qr = nullptr, int64_t ldr = 0,
                                              uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0) {
+  constexpr int T = 4 * COLS, CPR = COLS / 8;
   const int t = threadIdx.x;
   uint4 va[4], vb[4];
   auto load = [&](uint4 (&v)[4], int a0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = t + i * 256;
-      const int r = c >> 3, ch = c & 7;
+      const int c = t + i * T;
+      const int r = c / CPR, ch = c % CPR;
       v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
     }
   };
@@ -285,8 +291,8 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       // lanes t, t ^ 1, t ^ 2, t ^ 3 hold the four 8-column chunks of one 32-column block
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int c = t + i * 256;
-        const int r = c >> 3, ch = c & 7;
+        const int c = t + i * T;
+        const int r = c / CPR, ch = c % CPR;
         float a = amax8(v[i]);
         a = fmaxf(a, __shfl_xor(a, 1));
         a = fmaxf(a, __shfl_xor(a, 2));
@@ -300,9 +306,9 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
     __syncthreads();  // every thread's reads of the previous pass are done
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = t + i * 256;
-      const int r = c >> 3;
-      *(uint4*)(s_tile + r * 32 + (((c & 7) ^ ((r >> 4) & 7)) * 4)) = v[i];
+      const int c = t + i * T;
+      const int r = c / CPR;
+      *(uint4*)(s_tile + r * (COLS / 2) + (((c % CPR) ^ ((r >> 4) & 7)) * 4)) = v[i];
     }
     const bool fast = !__syncthreads_or(nan != 0u);  // block-uniform: the tile holds no NaN
     if (a0 + 2 * kTRows < n_out) load(v, a0 + 2 * kTRows);
@@ -310,14 +316,14 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
     // output row's 128 bytes, so every store instruction writes 8 rows x 128 contiguous bytes
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int u = t + 256 * h;
+      const int u = t + T * h;
       const int cc = u >> 3, kq = u & 7;
       const int rb = a0 + 16 * kq;
       // column cc of pass rows 16 kq + s sits in chunk (cc / 8) ^ kq of its row
-      const uint16_t* xs = (const uint16_t*)s_tile + (16 * kq) * 64 + (((cc >> 3) ^ kq) * 8) + (cc & 7);
+      const uint16_t* xs = (const uint16_t*)s_tile + (16 * kq) * COLS + (((cc >> 3) ^ kq) * 8) + (cc & 7);
       float xv[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) xv[k] = bf2f(xs[64 * k]);
+      for (int k = 0; k < 16; ++k) xv[k] = bf2f(xs[COLS * k]);
       float f;
       uint32_t e = 0;
       if constexpr (MX) {
@@ -359,41 +365,43 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
 }
 
 // x [E][A][B] -> q rows (e, b) of A values at q + e * q_estride + b * q_ld, and
-// scale[e * s_estride + b] = amax over A. Block per (e, 64 columns).
-__global__ __launch_bounds__(256) void quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
+// scale[e * s_estride + b] = amax over A. Block per (e, COLS columns).
+template <int COLS>
+__global__ __launch_bounds__(4 * COLS) void quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
                                                            uint8_t* __restrict__ q, int64_t q_estride, int64_t q_ld,
                                                            float* __restrict__ scale, int64_t s_estride) {
-  __shared__ float s_red[64 * 33];
-  __shared__ float s_amax[64];
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
-  const int nb = B / 64;
+  __shared__ float s_red[COLS * 33];
+  __shared__ float s_amax[COLS];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
+  const int nb = B / COLS;
   const int64_t e = blockIdx.x / nb;
-  const int b0 = (blockIdx.x % nb) * 64;
+  const int b0 = (blockIdx.x % nb) * COLS;
   const uint16_t* base = x + e * A * (int64_t)B + b0;
-  slab_amax(base, B, A, s_red, s_amax);
-  if (threadIdx.x < 64) {
+  slab_amax<COLS>(base, B, A, s_red, s_amax);
+  if (threadIdx.x < COLS) {
     const float s = scale_of(s_amax[threadIdx.x]);
     s_amax[threadIdx.x] = s;
     scale[e * s_estride + b0 + threadIdx.x] = s;
   }
   __syncthreads();
-  slab_t_quant<false, false>(base, B, A, A, q + e * q_estride + b0 * q_ld, q_ld, nullptr, 0, 0, s_amax, s_tile);
+  slab_t_quant<false, false, COLS>(base, B, A, A, q + e * q_estride + b0 * q_ld, q_ld, nullptr, 0, 0, s_amax, s_tile);
 }
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
 // 16-aligned offset pstart_e, zero padded to ceil16(count_e)), scale [E][C].
-// Block per (e, 64 columns); empty groups exit.
-__global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ counts,
+// Block per (e, COLS columns); empty groups exit.
+template <int COLS>
+__global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ counts,
                                                              int64_t R, int E, int C, int64_t Rpad,
                                                              uint8_t* __restrict__ q, float* __restrict__ scale) {
-  __shared__ float s_red[64 * 33];
-  __shared__ float s_amax[64];
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
+  __shared__ float s_red[COLS * 33];
+  __shared__ float s_amax[COLS];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
   __shared__ int s_tmp[8];
   __shared__ int s_seg[2];
-  const int nc = C / 64;
+  const int nc = C / COLS;
   const int e = blockIdx.x / nc;
-  const int c0 = (blockIdx.x % nc) * 64;
+  const int c0 = (blockIdx.x % nc) * COLS;
   {
     int cnt[4], pc[4], st[4], pst[4];
 #pragma unroll
@@ -417,14 +425,14 @@ __global__ __launch_bounds__(256) void quant_tokens_t_kernel(const uint16_t* __r
   const int n_out = (n + kPad - 1) / kPad * kPad;
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
   const uint16_t* base = x + (int64_t)seg0 * C + c0;
-  slab_amax(base, C, n, s_red, s_amax);
-  if (threadIdx.x < 64) {
+  slab_amax<COLS>(base, C, n, s_red, s_amax);
+  if (threadIdx.x < COLS) {
     const float s = scale_of(s_amax[threadIdx.x]);
     s_amax[threadIdx.x] = s;
     scale[(int64_t)e * C + c0 + threadIdx.x] = s;
   }
   __syncthreads();
-  slab_t_quant<false, false>(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, nullptr, 0, 0, s_amax,
+  slab_t_quant<false, false, COLS>(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, nullptr, 0, 0, s_amax,
                              s_tile);
 }
 
@@ -464,53 +472,55 @@ __global__ __launch_bounds__(256) void mx_quant_rows_kernel(const uint4* __restr
 }
 
 // x [E][A][B] -> q rows (e, b) of A values at q + e * q_estride + b * q_ld, and
-// their A/32 scales at s + e * s_estride + b * s_ld. Block per (e, 64 columns).
-__global__ __launch_bounds__(256) void mx_quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
+// their A/32 scales at s + e * s_estride + b * s_ld. Block per (e, COLS columns).
+template <int COLS>
+__global__ __launch_bounds__(4 * COLS) void mx_quant_cols_t_kernel(const uint16_t* __restrict__ x, int A, int B,
                                                               uint8_t* __restrict__ q, int64_t q_estride,
                                                               int64_t q_ld, uint8_t* __restrict__ s,
                                                               int64_t s_estride, int64_t s_ld) {
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
-  const int nb = B / 64;
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
+  const int nb = B / COLS;
   const int64_t e = blockIdx.x / nb;
-  const int b0 = (blockIdx.x % nb) * 64;
-  slab_t_quant<true, false>(x + e * A * (int64_t)B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
+  const int b0 = (blockIdx.x % nb) * COLS;
+  slab_t_quant<true, false, COLS>(x + e * A * (int64_t)B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
                             s + e * s_estride + b0 * s_ld, s_ld, 1, nullptr, s_tile);
 }
 
 // Both MX layouts of x [E][A][B] from one read: the row-wise one (q_r [E][A][B],
 // s_r [E][A][B / 32], as mx_quant_rows on [E A, B]) and the transposed one of
-// mx_quant_cols_t. Block per (e, 64 columns).
-__global__ __launch_bounds__(256) void mx_dual_cols_kernel(const uint16_t* __restrict__ x, int A, int B,
+// mx_quant_cols_t. Block per (e, COLS columns).
+template <int COLS>
+__global__ __launch_bounds__(4 * COLS) void mx_dual_cols_kernel(const uint16_t* __restrict__ x, int A, int B,
                                                            uint8_t* __restrict__ q, int64_t q_estride, int64_t q_ld,
                                                            uint8_t* __restrict__ s, int64_t s_estride, int64_t s_ld,
                                                            uint8_t* __restrict__ qr, uint8_t* __restrict__ sr) {
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
-  const int nb = B / 64;
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
+  const int nb = B / COLS;
   const int64_t e = blockIdx.x / nb;
-  const int b0 = (blockIdx.x % nb) * 64;
+  const int b0 = (blockIdx.x % nb) * COLS;
   const int64_t row0 = e * A;  // first row of expert e in the [E A, B] view
-  slab_t_quant<true, true>(x + row0 * B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
+  slab_t_quant<true, true, COLS>(x + row0 * B + b0, B, A, A, q + e * q_estride + b0 * q_ld, q_ld,
                            s + e * s_estride + b0 * s_ld, s_ld, 1, nullptr, s_tile, qr + row0 * B + b0, B,
                            sr + row0 * (B / kMxBlock) + b0 / kMxBlock, B / kMxBlock);
 }
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
 // 32-aligned offset pstart_e, zero padded to ceil32(count_e)) and the scales
-// k-block major, s [Rpad / 32][C]. Block per (e, 64 columns); empty groups exit.
+// k-block major, s [Rpad / 32][C]. Block per (e, COLS columns); empty groups exit.
 // With ROWS, the same read also writes the row-wise layout of the group's rows
 // (qr [R][C], sr [R][C / 32]).
-template <bool ROWS>
-__global__ __launch_bounds__(256) void mx_quant_tokens_t_kernel(const uint16_t* __restrict__ x,
+template <bool ROWS, int COLS>
+__global__ __launch_bounds__(4 * COLS) void mx_quant_tokens_t_kernel(const uint16_t* __restrict__ x,
                                                                 const int64_t* __restrict__ counts, int64_t R, int E,
                                                                 int C, int64_t Rpad, uint8_t* __restrict__ q,
                                                                 uint8_t* __restrict__ s, uint8_t* __restrict__ qr,
                                                                 uint8_t* __restrict__ sr) {
-  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * 32];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
   __shared__ int s_tmp[8];
   __shared__ int s_seg[3];
-  const int nc = C / 64;
+  const int nc = C / COLS;
   const int e = blockIdx.x / nc;
-  const int c0 = (blockIdx.x % nc) * 64;
+  const int c0 = (blockIdx.x % nc) * COLS;
   {
     int cnt[4], pc[4], st[4], pst[4];
 #pragma unroll
@@ -537,15 +547,15 @@ __global__ __launch_bounds__(256) void mx_quant_tokens_t_kernel(const uint16_t* 
     // are multiples of 32, so the rows' tails take 16-byte stores.
     const int64_t end = (int64_t)pstart + n_out;
     const int64_t tail16 = (Rpad - end) / 16;
-    for (int64_t i = threadIdx.x; i < 64 * tail16; i += 256) {
+    for (int64_t i = threadIdx.x; i < COLS * tail16; i += 4 * COLS) {
       const int64_t c = i / tail16, j = i - c * tail16;
       *(uint4*)(q + (c0 + c) * Rpad + end + 16 * j) = make_uint4(0u, 0u, 0u, 0u);
     }
-    if (threadIdx.x < 64)
+    if (threadIdx.x < COLS)
       for (int64_t br = end / kMxBlock; br < Rpad / kMxBlock; ++br) s[br * C + c0 + threadIdx.x] = 0;
   }
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
-  slab_t_quant<true, ROWS>(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
+  slab_t_quant<true, ROWS, COLS>(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
                            s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C, nullptr, s_tile,
                                 ROWS ? qr + (int64_t)seg0 * C + c0 : nullptr, C,
                                 ROWS ? sr + (int64_t)seg0 * (C / kMxBlock) + c0 / kMxBlock : nullptr, C / kMxBlock);
@@ -1157,8 +1167,12 @@ MOE_API int moe_fp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a
       scale_expert_stride < b)
     return kErrInvalidArgument;
   if (!x || !q || !scale) return kErrInvalidArgument;
-  hipLaunchKernelGGL(quant_cols_t_kernel, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
-                     q_expert_stride, q_row_stride, scale, scale_expert_stride);
+  if (b % 128 == 0)
+    hipLaunchKernelGGL(quant_cols_t_kernel<128>, dim3(n_experts * (b / 128)), dim3(512), 0, stream, x, a, b, q,
+                       q_expert_stride, q_row_stride, scale, scale_expert_stride);
+  else
+    hipLaunchKernelGGL(quant_cols_t_kernel<64>, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
+                       q_expert_stride, q_row_stride, scale, scale_expert_stride);
   return launch_status();
 }
 
@@ -1168,8 +1182,12 @@ MOE_API int moe_fp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
   if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
   if (!x || !counts || !q || !scale) return kErrInvalidArgument;
-  hipLaunchKernelGGL(quant_tokens_t_kernel, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts, n_rows,
-                     n_experts, cols, padded_rows, q, scale);
+  if (cols % 128 == 0)
+    hipLaunchKernelGGL(quant_tokens_t_kernel<128>, dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x, counts,
+                       n_rows, n_experts, cols, padded_rows, q, scale);
+  else
+    hipLaunchKernelGGL(quant_tokens_t_kernel<64>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
+                       n_rows, n_experts, cols, padded_rows, q, scale);
   return launch_status();
 }
 
@@ -1294,8 +1312,12 @@ MOE_API int moe_mxfp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t
   if (scale_row_stride < a / kMxBlock || scale_expert_stride < (int64_t)(b - 1) * scale_row_stride + a / kMxBlock)
     return kErrInvalidArgument;
   if (!x || !q || !scale) return kErrInvalidArgument;
-  hipLaunchKernelGGL(mx_quant_cols_t_kernel, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
-                     q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride);
+  if (b % 128 == 0)
+    hipLaunchKernelGGL(mx_quant_cols_t_kernel<128>, dim3(n_experts * (b / 128)), dim3(512), 0, stream, x, a, b, q,
+                       q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride);
+  else
+    hipLaunchKernelGGL(mx_quant_cols_t_kernel<64>, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
+                       q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride);
   return launch_status();
 }
 
@@ -1305,8 +1327,12 @@ MOE_API int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, i
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
   if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
   if (!x || !counts || !q || !scale) return kErrInvalidArgument;
-  hipLaunchKernelGGL(mx_quant_tokens_t_kernel<false>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
-                     n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr);
+  if (cols % 128 == 0)
+    hipLaunchKernelGGL((mx_quant_tokens_t_kernel<false, 128>), dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x,
+                       counts, n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr);
+  else
+    hipLaunchKernelGGL((mx_quant_tokens_t_kernel<false, 64>), dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x,
+                       counts, n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr);
   return launch_status();
 }
 
@@ -1320,8 +1346,12 @@ MOE_API int moe_mxfp8_quant_dual_cols(const uint16_t* x, int32_t n_experts, int3
   if (scale_row_stride < a / kMxBlock || scale_expert_stride < (int64_t)(b - 1) * scale_row_stride + a / kMxBlock)
     return kErrInvalidArgument;
   if (!x || !q || !scale || !q_rows || !scale_rows) return kErrInvalidArgument;
-  hipLaunchKernelGGL(mx_dual_cols_kernel, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
-                     q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride, q_rows, scale_rows);
+  if (b % 128 == 0)
+    hipLaunchKernelGGL(mx_dual_cols_kernel<128>, dim3(n_experts * (b / 128)), dim3(512), 0, stream, x, a, b, q,
+                       q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride, q_rows, scale_rows);
+  else
+    hipLaunchKernelGGL(mx_dual_cols_kernel<64>, dim3(n_experts * (b / 64)), dim3(256), 0, stream, x, a, b, q,
+                       q_expert_stride, q_row_stride, scale, scale_expert_stride, scale_row_stride, q_rows, scale_rows);
   return launch_status();
 }
 
@@ -1331,8 +1361,12 @@ MOE_API int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
   if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
   if (!x || !counts || !q || !scale || !q_rows || !scale_rows) return kErrInvalidArgument;
-  hipLaunchKernelGGL(mx_quant_tokens_t_kernel<true>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
-                     n_rows, n_experts, cols, padded_rows, q, scale, q_rows, scale_rows);
+  if (cols % 128 == 0)
+    hipLaunchKernelGGL((mx_quant_tokens_t_kernel<true, 128>), dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x,
+                       counts, n_rows, n_experts, cols, padded_rows, q, scale, q_rows, scale_rows);
+  else
+    hipLaunchKernelGGL((mx_quant_tokens_t_kernel<true, 64>), dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x,
+                       counts, n_rows, n_experts, cols, padded_rows, q, scale, q_rows, scale_rows);
   return launch_status();
 }
 
