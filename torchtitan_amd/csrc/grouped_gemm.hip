@@ -148,8 +148,14 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
 template <typename T>
 __device__ __forceinline__ uint32_t lds_addr(T* ptr) { return (uint32_t)(size_t)((LDSP T*)ptr); }
 
-// Row-major LDS tile with 64-byte rows (32 bf16 of k): element offset of chunk kc of row r.
-__device__ __forceinline__ int rm_off(int r, int kc) { return (r * 4 + (kc ^ ((r >> 1) & 3))) * 8; }
+// Row-major LDS tile with rows of BK bf16 of k (64 or 128 bytes): element offset of
+// 16-byte chunk kc of row r. 64-byte rows: chunk kc ^ ((r >> 1) & 3); 128-byte rows
+// (whole cache lines per row): chunk kc ^ (r & 7).
+template <int BK>
+__device__ __forceinline__ int rm_off(int r, int kc) {
+  if constexpr (BK == 32) return (r * 4 + (kc ^ ((r >> 1) & 3))) * 8;
+  else return (r * 8 + (kc ^ (r & 7))) * 8;
+}
 
 // 16-byte chunk swizzle of a k-major tile row k (rows of 16 or more chunks):
 // conflict-free for transposed fragment reads (32 lanes per LDS pass read 8 k-rows).
@@ -159,8 +165,9 @@ __device__ __forceinline__ int km_off(int k, int n) { return k * ROWE + ((((n >>
 
 // MFMA fragment (16 rows x 32 k, lane l: row l % 16, k 8 (l / 16) .. + 7) from a
 // K-contiguous tile (row-major 64-byte rows).
-__device__ __forceinline__ bf16x8_t frag_rm(const uint16_t* tile, int row, int lane) {
-  return *(const bf16x8_t*)(tile + rm_off(row, lane >> 4));
+template <int BK>
+__device__ __forceinline__ bf16x8_t frag_rm(const uint16_t* tile, int row, int lane, int kh) {
+  return *(const bf16x8_t*)(tile + rm_off<BK>(row, kh * 4 + (lane >> 4)));
 }
 // the same fragment from a k-major tile of ROWE elements per k-row, with two
 // transposing reads (each lane supplies 4 consecutive rows of one k)
@@ -178,14 +185,17 @@ __device__ const uint4 kZeroRow[64] = {};  // source of the zero rows past a seg
 
 // TAIL: the n extent (and, for dW, the m extent) is not a multiple of the tile;
 // compiled only for such shapes so that whole-tile shapes keep the tighter code.
-template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT, bool TAIL>
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT, bool TAIL, int BKT>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p) {
   using T = ModeTraits<MODE>;
   constexpr int WGN = NW / WGM;
   constexpr int WM = TM * 16, WN = TN * 16;
-  constexpr int BM = WGM * WM, BN = WGN * WN, BK = 32;
-  constexpr int CPW_P = BM / 16 / NW, CPW_Q = BN / 16 / NW;  // 1 KB copies per wave and stage
-  static_assert(CPW_P * 16 * NW == BM && CPW_Q * 16 * NW == BN, "copies per wave");
+  constexpr int BM = WGM * WM, BN = WGN * WN, BK = BKT;
+  static_assert(BK == 32 || (BK == 64 && !T::kPT && !T::kQT), "k-steps of 64 for k-contiguous operands only");
+  constexpr int RPC = 512 / BK;  // tile rows per 1 KB copy (k-contiguous tiles)
+  constexpr int KH = BK / 32;    // MFMA k-steps per stage
+  constexpr int CPW_P = BM * BK / 512 / NW, CPW_Q = BN * BK / 512 / NW;  // 1 KB copies per wave and stage
+  static_assert(CPW_P * 512 * NW == BM * BK && CPW_Q * 512 * NW == BN * BK, "copies per wave");
   constexpr int CPW = CPW_P + CPW_Q;
   constexpr int CHP = BM / 8, CHQ = BN / 8;          // 16-byte chunks per k-row (k-major tiles)
   static_assert(BM % 64 == 0 && BN % 64 == 0 && CPW <= 30, "tile");
@@ -253,8 +263,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
   // copy-lane maps. K-contiguous tile: one copy = 16 rows x 64 B, lane i -> row i >> 2,
   // chunk (i & 3) ^ ((row >> 1) & 3). k-major tile: one copy = 1 KB of k-rows, lane i ->
   // k-row i / (ROWB / 16), chunk (i % (ROWB / 16)) ^ kswz(k).
-  const int dr = lane >> 2;
-  const int dc = (lane & 3) ^ ((dr >> 1) & 3);
+  const int dr = BK == 32 ? lane >> 2 : lane >> 3;
+  const int dc = BK == 32 ? (lane & 3) ^ ((dr >> 1) & 3) : (lane & 7) ^ (dr & 7);
 
   // ---- tiles ----
   struct TileRef { int e, seg0, seg1, mt, nt, nk; };
@@ -307,7 +317,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       else { pb = p.dgu; ldp = 2 * H; }
 #pragma unroll
       for (int b = 0; b < CPW_P; ++b) {
-        const int rr = row0 + (wv * CPW_P + b) * 16 + dr;
+        const int rr = row0 + (wv * CPW_P + b) * RPC + dr;
         srcP[b] = pb + (int64_t)rr * ldp + dc * 8;
         klP[b] = rr;  // rows past the segment copy the zero row
         inP[b] = true;
@@ -328,7 +338,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     if constexpr (!T::kQT) {
 #pragma unroll
       for (int b = 0; b < CPW_Q; ++b) {
-        const int n = (wv * CPW_Q + b) * 16 + dr;
+        const int n = (wv * CPW_Q + b) * RPC + dr;
         inQ[b] = (MODE == kFwdGateUp) ? gate_up_col(r.nt, n, BN) < H : r.nt * BN + n < D;
         const uint16_t* rowp = (MODE == kFwdGateUp) ? gate_up_row(p, e64, r.nt, n, BN)
                                                      : p.w2 + (e64 * D + r.nt * BN + n) * (int64_t)H;
@@ -463,22 +473,25 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       auto compute = [&](int s) {
         const uint16_t* cP = sP[s];
         const uint16_t* cQ = sQ[s];
-        bf16x8_t af[TM];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if (!decltype(full)::value && i >= tmv) continue;
-          if constexpr (T::kPT) af[i] = frag_km<BM>(cP, wm * WM + i * 16, lane);
-          else af[i] = frag_rm(cP, wm * WM + i * 16 + ml, lane);
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          bf16x8_t bq;
-          if constexpr (T::kQT) bq = frag_km<BN>(cQ, wn * WN + j * 16, lane);
-          else bq = frag_rm(cQ, wn * WN + j * 16 + ml, lane);
+        for (int kh = 0; kh < KH; ++kh) {
+          bf16x8_t af[TM];
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
             if (!decltype(full)::value && i >= tmv) continue;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq, af[i], acc[i][j], 0, 0, 0);
+            if constexpr (T::kPT) af[i] = frag_km<BM>(cP, wm * WM + i * 16, lane);
+            else af[i] = frag_rm<BK>(cP, wm * WM + i * 16 + ml, lane, kh);
+          }
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            bf16x8_t bq;
+            if constexpr (T::kQT) bq = frag_km<BN>(cQ, wn * WN + j * 16, lane);
+            else bq = frag_rm<BK>(cQ, wn * WN + j * 16 + ml, lane, kh);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+              if (!decltype(full)::value && i >= tmv) continue;
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq, af[i], acc[i][j], 0, 0, 0);
+            }
           }
         }
       };
@@ -713,7 +726,7 @@ static int persistent_grid(int64_t max_tiles, int per_cu) {
 
 // One launch of grouped_gemm_kernel with NW waves in WGM x (NW / WGM), wave
 // tiles (16 TM) x (16 TN), NS LDS stages and OCC workgroups per CU.
-template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT>
+template <int MODE, int NW, int WGM, int TM, int TN, int NS, bool SKIP, int OCC, int ACT, int BKT = 32>
 static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
   constexpr int BM = WGM * TM * 16, BN = (NW / WGM) * TN * 16;
   auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
@@ -731,13 +744,16 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
   else tail = p.D % BM != 0 || p.H % BN != 0;
   const dim3 grid(persistent_grid(max_tiles, OCC)), block(NW * 64);
   if (tail)
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC, ACT, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC, ACT, true, BKT>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC, ACT, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NW, WGM, TM, TN, NS, SKIP, OCC, ACT, false, BKT>), grid, block, 0, stream, p);
 }
 
 // Tile per mode (measured at the Kimi and DSv3 shapes). The forward modes run
-// 128 x 256 tiles, four waves, two workgroups per CU. The backward modes run
+// 128 x 256 tiles, four waves, two workgroups per CU; gate_up over a long
+// contraction (D >= 4096) runs the same tile as eight 64 x 64 waves with 64-wide
+// k-steps (whole 128-byte rows per copy) and three stages at one workgroup per CU
+// (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower). The backward modes run
 // one eight-wave workgroup per CU with three LDS stages and wider tiles, which
 // halves the copy traffic per flop of the dW operands: 128 x 512 (dgu, and dx
 // when D is a multiple of 512), 128 x 384 (dx, D a multiple of 384), 256 x 256
@@ -747,6 +763,12 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 template <int MODE, int ACT = kSwiGLU>
 static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
   if constexpr (MODE == kFwdGateUp || MODE == kFwdDown) {
+    if constexpr (MODE == kFwdGateUp && ACT == kSwiGLU) {
+      if (p.D >= 4096) {  // long contractions: 128-byte rows per stage, eight 64 x 64 waves
+        launch_cfg<MODE, 8, 2, 4, 4, 3, true, 1, ACT, 64>(p, R, stream);
+        return;
+      }
+    }
     launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2, ACT>(p, R, stream);
   } else if constexpr (MODE == kBwdDgu) {
     if (p.H % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, true, 1, ACT>(p, R, stream);
