@@ -189,6 +189,39 @@ def test_fp8_quantizers_bit_exact(dev):
         pstart += (n + 15) // 16 * 16
 
 
+
+@pytest.mark.parametrize("width", [192, 320, 384])
+def test_fp8_transposing_quantizers_slab_widths(dev, width):
+    """The transposing quantizers at widths that take 64-column slabs (192, 320)
+    and 128-column ones (384): bit-exact against the oracle as at width 128."""
+    banner(f"fp8 transposing quantizers width={width}")
+    g = torch.Generator().manual_seed(width)
+    from torchtitan_amd import _lib, ops
+    e, a = 3, 256
+    w = torch.randn(e, a, width, generator=g).bfloat16()
+    qt = torch.empty(e, width, a, dtype=torch.uint8, device=dev)
+    st = torch.empty(e, width, dtype=torch.float32, device=dev)
+    _lib.call("moe_fp8_quant_cols_t", w.to(dev).data_ptr(), e, a, width, qt.data_ptr(), width * a, a, st.data_ptr(),
+              width, torch.cuda.current_stream().cuda_stream)
+    for i in range(e):
+        rq, rs = R.quant_fp8_rows(w[i].t())
+        assert torch.equal(qt[i].cpu(), rq.view(torch.uint8))
+        assert torch.equal(st[i].cpu(), rs.view(-1))
+    counts = torch.tensor([5, 0, 300, 16, 1], dtype=torch.int64)
+    r = int(counts.sum())
+    xt = torch.randn(r, width, generator=g).bfloat16()
+    rpad = ops._padded_rows(r, len(counts))
+    q2, s2 = ops._quant_tokens_t(xt.to(dev), counts.to(dev), len(counts), rpad)
+    q2, s2 = q2.cpu(), s2.cpu()
+    start = pstart = 0
+    for i, n in enumerate(counts.tolist()):
+        if n:
+            rq, rs = R.quant_fp8_rows(xt[start:start + n].t())
+            assert torch.equal(q2[:, pstart:pstart + n], rq.view(torch.uint8))
+            assert torch.equal(s2[i], rs.view(-1))
+        start += n
+        pstart += (n + 15) // 16 * 16
+
 CASES = {
     "ragged_e8": (8, 256, 512, [37, 0, 130, 16, 255, 1, 64, 100]),
     "e16_d512_h256": (16, 512, 256, [96, 81, 0, 0, 200, 17, 33, 64, 128, 5, 70, 90, 300, 2, 0, 40]),

@@ -124,6 +124,42 @@ def test_mxfp8_quantizers_bit_exact(dev):
             assert torch.equal(sw13t[i][:, half * hh_ // 32:(half + 1) * hh_ // 32], rs)
 
 
+
+@pytest.mark.parametrize("width", [192, 320, 384])
+def test_mxfp8_transposing_quantizers_slab_widths(dev, width):
+    """The MXFP8 transposing and dual quantizers at widths that take 64-column
+    slabs (192, 320) and 128-column ones (384): bit-exact against the oracle."""
+    banner(f"mxfp8 transposing quantizers width={width}")
+    from torchtitan_amd import _lib, ops
+    g = torch.Generator().manual_seed(width)
+    st = torch.cuda.current_stream().cuda_stream
+    e, a = 3, 256
+    w = torch.randn(e, a, width, generator=g).bfloat16()
+    qr = torch.empty(e * a, width, dtype=torch.uint8, device=dev)
+    sr = torch.empty(e * a, width // 32, dtype=torch.uint8, device=dev)
+    qt = torch.empty(e, width, a, dtype=torch.uint8, device=dev)
+    stt = torch.empty(e, width, a // 32, dtype=torch.uint8, device=dev)
+    _lib.call("moe_mxfp8_quant_dual_cols", w.to(dev).data_ptr(), e, a, width, qr.data_ptr(), sr.data_ptr(),
+              qt.data_ptr(), width * a, a, stt.data_ptr(), width * (a // 32), a // 32, st)
+    rq, rs = R.quant_mxfp8(w.reshape(-1, width))
+    assert torch.equal(qr.cpu(), rq.view(torch.uint8)) and torch.equal(sr.cpu(), rs)
+    for i in range(e):
+        rq, rs = R.quant_mxfp8(w[i].t())
+        assert torch.equal(qt[i].cpu(), rq.view(torch.uint8)) and torch.equal(stt[i].cpu(), rs)
+    counts = torch.tensor([5, 0, 300, 32, 1], dtype=torch.int64)
+    r = int(counts.sum())
+    xt = torch.randn(r, width, generator=g).bfloat16()
+    rpad = ops._mx_padded_rows(r, len(counts))
+    segs = [(int(counts[:i].sum()), int(n)) for i, n in enumerate(counts)]
+    rq2, rs2, _ = _tokens_t(xt, segs, rpad)
+    used = sum((n + 31) // 32 * 32 for _, n in segs)
+    q2, s2 = ops._mx_quant_tokens_t(xt.to(dev), counts.to(dev), len(counts), rpad)
+    assert torch.equal(q2.cpu()[:, :used], rq2[:, :used]) and torch.equal(s2.cpu()[:used // 32], rs2[:used // 32])
+    dqr, dsr, dqt, dst = ops._mx_dual_tokens(xt.to(dev), counts.to(dev), len(counts), rpad)
+    rqr, rsr = R.quant_mxfp8(xt)
+    assert torch.equal(dqr.cpu(), rqr.view(torch.uint8)) and torch.equal(dsr.cpu(), rsr)
+    assert torch.equal(dqt.cpu()[:, :used], rq2[:, :used]) and torch.equal(dst.cpu()[:used // 32], rs2[:used // 32])
+
 def test_mxfp8_gemm_entry_points_match_emulation(dev):
     """Every MXFP8 GEMM kernel against R._mx_mm on identical quantized operands."""
     banner("mxfp8 GEMM entry points")
