@@ -18,9 +18,9 @@
 // Design (gfx950, 64-wide waves):
 //  * Wave tiles of 64 x 128 (or 64 x 96) of v_mfma_f32_16x16x32_bf16 (fp32
 //    accumulate), two waves per SIMD so each hides the other's LDS latency:
-//    forward modes 4 waves / 128 x 256 block / two workgroups per CU, backward
-//    modes 8 waves / 128 x 512, 128 x 384 or 256 x 256 block / one workgroup
-//    per CU (wider blocks copy fewer bytes per flop). k-step 32.
+//    forward modes and dgu 4 waves / 128 x 256 block / two workgroups per CU,
+//    dx and dW 8 waves / 128 x 512, 128 x 384 or 256 x 256 block / one
+//    workgroup per CU (wider blocks copy fewer bytes per flop). k-step 32.
 //  * Operands go HBM/L2 -> LDS with direct-to-LDS copies
 //    (global_load_lds_dwordx4: each wave instruction fills 1 KB of LDS), so no
 //    VGPRs stage the tiles and no ds_write is issued. Two or three LDS stages:
@@ -620,9 +620,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       }
     } else if (MODE == kBwdDgu) {
       // dh = bf16(dy . w2) is gathered into the 64-byte span layout first, so g and u
-      // are read, and dg and du written, as 16-byte pieces of 64 contiguous bytes per row
+      // are read, and dg and du written, as 16-byte pieces of 64 contiguous bytes per row.
+      // The g and u pieces of a 16-row block are loaded together, and the next block's
+      // are in flight while this block computes and stores: one memory round trip per
+      // tile is exposed instead of one per piece (the loads would otherwise wait behind
+      // each piece's stores, which may alias them).
+      uint4 gbuf[1][TN / 2], ubuf[1][TN / 2];
+      auto load_gu = [&](int i, int b) {
+        const int r = row0 + wm * WM + i * 16 + ml;
+#pragma unroll
+        for (int jp = 0; jp < TN / 2; ++jp) {
+          const int hh = nt * BN + wn * WN + jp * 32 + g8;
+          if (r < seg1 && (!TAIL || hh < H)) {
+            const int64_t off = (int64_t)r * H + hh;
+            gbuf[b][jp] = *(const uint4*)(p.g + off);
+            ubuf[b][jp] = *(const uint4*)(p.u + off);
+          }
+        }
+      };
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
+        load_gu(i, 0);
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
 #pragma unroll
@@ -633,9 +651,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
             const uint4 sdh = span64(pack4(lo), pack4(hi), lane);
             const int hh = nt * BN + wn * WN + jp * 32 + g8;
             if (TAIL && hh >= H) continue;
-            const int64_t off = (int64_t)r * H + hh;
-            const uint4 gw = *(const uint4*)(p.g + off);
-            const uint4 uw = *(const uint4*)(p.u + off);
+            const uint4 gw = gbuf[0][jp];
+            const uint4 uw = ubuf[0][jp];
             const uint32_t dhw[4] = {sdh.x, sdh.y, sdh.z, sdh.w};
             const uint32_t gww[4] = {gw.x, gw.y, gw.z, gw.w};
             const uint32_t uww[4] = {uw.x, uw.y, uw.z, uw.w};
@@ -753,13 +770,16 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 // 128 x 256 tiles, four waves, two workgroups per CU; gate_up over a long
 // contraction (D >= 4096) runs the same tile as eight 64 x 64 waves with 64-wide
 // k-steps (whole 128-byte rows per copy) and three stages at one workgroup per CU
-// (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower). The backward modes run
+// (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower). dgu runs the
+// forward tile too: its epilogue reads g and u and writes dg and du, and with two
+// workgroups per CU one's epilogue overlaps the other's MFMAs (against one
+// eight-wave 128 x 512 workgroup: DSv3 3.15 -> 2.81 ms, Kimi -1.5 %). dx and dW run
 // one eight-wave workgroup per CU with three LDS stages and wider tiles, which
-// halves the copy traffic per flop of the dW operands: 128 x 512 (dgu, and dx
-// when D is a multiple of 512), 128 x 384 (dx, D a multiple of 384), 256 x 256
-// (dW). D and H are multiples of 64 (check_gemm_shape). The tail skip is
-// compiled into the row-grouped modes except dx, whose second copy of the K
-// loop costs more registers than the skip saves.
+// halves the copy traffic per flop of the dW operands: 128 x 384 (dx, D a multiple
+// of 384), 128 x 512 (dx, D a multiple of 512), 256 x 256 (dW). D and H are
+// multiples of 64 (check_gemm_shape). The tail skip is compiled into the
+// row-grouped modes except dx, whose second copy of the K loop costs more
+// registers than the skip saves.
 template <int MODE, int ACT = kSwiGLU>
 static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
   if constexpr (MODE == kFwdGateUp || MODE == kFwdDown) {
@@ -771,8 +791,7 @@ static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
     }
     launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2, ACT>(p, R, stream);
   } else if constexpr (MODE == kBwdDgu) {
-    if (p.H % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, true, 1, ACT>(p, R, stream);
-    else launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2, ACT>(p, R, stream);
+    launch_cfg<MODE, 4, 2, 4, 8, 2, true, 2, ACT>(p, R, stream);
   } else if constexpr (MODE == kBwdDx) {
     if (p.D % 384 == 0) launch_cfg<MODE, 8, 2, 4, 6, 3, false, 1, ACT>(p, R, stream);
     else if (p.D % 512 == 0) launch_cfg<MODE, 8, 2, 4, 8, 3, false, 1, ACT>(p, R, stream);
