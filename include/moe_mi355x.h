@@ -65,6 +65,35 @@ int moe_router_bwd(const float* grad_top_scores, const float* scores,
                    int32_t top_k, int32_t score_func, int32_t route_norm, float route_scale,
                    float* grad_logits, moe_stream_t stream);
 
+/* The gate's backward (autograd of the fp32 gate under autocast, moe.py:229-232)
+ * on bf16 GEMMs: grad_logits [N,C] fp32 -> terms [N,3C] bf16 (hi | mid | lo),
+ * hi = bf16(d), mid = bf16(d - hi), lo = bf16(d - hi - mid), so that
+ * hi + mid + lo == d exactly and dx = terms.[W;W;W], dW = terms^T.x carry the
+ * fp32 GEMMs' exact products. C % 4 == 0; both pointers 16-byte aligned. */
+int moe_gate_grad_split3(const float* grad_logits, int64_t n_rows, int32_t n_cols, uint16_t* terms,
+                         moe_stream_t stream);
+
+/* grad_weight [E,D] bf16 from the fp32 partials [P,3E,D] of terms^T.x (P = 1, or
+ * 2 token halves): t_b = p0_b (+ p1_b) for the hi, mid, lo row blocks b, then
+ * bf16((t_hi + t_mid) + t_lo). D % 4 == 0; both pointers 16-byte aligned. */
+int moe_gate_dw_reduce(const float* partials, int32_t n_parts, int32_t n_experts, int32_t dim,
+                       uint16_t* grad_weight, moe_stream_t stream);
+
+/* Shared expert SwiGLU between its GEMMs (feed_forward.py:53-54,
+ * silu(w1 x) * w3 x): a1 = x.w1^T, a3 = x.w3^T [N,Hs] -> h = silu(a1) * a3,
+ * silu's output rounded to the dtype before the product, as torch's two ops.
+ * dtype MOE_DTYPE_BF16 or MOE_DTYPE_FP32 (16-byte chunks per thread when Hs is
+ * a multiple of 8 resp. 4 elements and the pointers are 16-byte aligned, one
+ * element per thread otherwise). */
+int moe_swiglu_fwd(const void* a1, const void* a3, int64_t n_rows, int32_t hidden, int32_t dtype, void* h,
+                   moe_stream_t stream);
+
+/* Autograd of moe_swiglu_fwd: dh = dy.w2 [N,Hs] -> dgu [N,2Hs], dg =
+ * silu_backward(dh * a3, a1) in columns [0,Hs) and du = dh * silu(a1) in [Hs,2Hs),
+ * every op rounded as torch's; side by side so that [dW1; dW3] is one GEMM. */
+int moe_swiglu_bwd(const void* dh, const void* a1, const void* a3, int64_t n_rows, int32_t hidden,
+                   int32_t dtype, void* dgu, moe_stream_t stream);
+
 /* Bytes of int32 workspace needed by moe_histogram / moe_reorder. */
 int64_t moe_reorder_workspace_bytes(int64_t n_tokens, int32_t n_experts);
 

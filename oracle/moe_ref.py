@@ -391,6 +391,33 @@ def feed_forward(x, w1, w2, w3):
 
 
 # ---------------------------------------------------------------------------
+# the gate's backward on bf16 GEMMs (a re-expression of the fp32 autocast
+# backward of moe.py:229-232; exact products, fp32 accumulation)
+# ---------------------------------------------------------------------------
+
+
+def gate_grad_split3(d: torch.Tensor) -> torch.Tensor:
+    """[N, C] fp32 -> [N, 3C] bf16 (hi | mid | lo) with hi + mid + lo == d: each
+    term takes the next 8 significand bits of what the previous ones left, so
+    three cover fp32's 24 (torch casts, round to nearest even)."""
+    hi = d.bfloat16()
+    r = d - hi.float()
+    mid = r.bfloat16()
+    lo = (r - mid.float()).bfloat16()
+    return torch.cat([hi, mid, lo], dim=1)
+
+
+def gate_dw_reduce(partials: torch.Tensor, num_experts: int) -> torch.Tensor:
+    """fp32 partials of terms^T x, [3E, D] or [2, 3E, D] (two token halves) ->
+    dW [E, D] bf16: the halves added, then (hi + mid) + lo, rounded once."""
+    p = partials.float()
+    if p.dim() == 3:
+        p = p[0] + p[1]
+    e = num_experts
+    return ((p[:e] + p[e:2 * e]) + p[2 * e:]).bfloat16()
+
+
+# ---------------------------------------------------------------------------
 # MoE.forward (moe.py:380-477)
 # ---------------------------------------------------------------------------
 

@@ -143,11 +143,16 @@ def _opcheck_cases(dev):
     hs = 128
     xs, sw1, sw2, sw3 = bf(n, d), bf(hs, d, scale=0.05), bf(d, hs, scale=0.05), bf(hs, d, scale=0.05)
     a1, a3 = torch.nn.functional.linear(xs, sw1), torch.nn.functional.linear(xs, sw3)
-    sl = torch.nn.functional.silu(a1)
-    cases["swiglu_ffn_backward"] = (swiglu_ffn_backward, (bf(n, d), xs, sw1, sw2, sw3, a1, a3, sl, sl * a3,
+    hsw = torch.nn.functional.silu(a1) * a3
+    cases["swiglu_ffn_backward"] = (swiglu_ffn_backward, (bf(n, d), xs, sw1, sw2, sw3, a1, a3, hsw,
                                                           True, True, True))
-    cases["swiglu_ffn_backward_dw_only"] = (swiglu_ffn_backward, (bf(n, d), xs, sw1, sw2, sw3, a1, a3, sl, sl * a3,
+    cases["swiglu_ffn_backward_dw_only"] = (swiglu_ffn_backward, (bf(n, d), xs, sw1, sw2, sw3, a1, a3, hsw,
                                                                   False, True, True))
+    cases["swiglu_forward"] = (ops.swiglu_forward, (a1, a3))
+    cases["swiglu_backward"] = (ops.swiglu_backward, (bf(n, hs), a1, a3))
+    # the gate's backward pieces
+    cases["gate_grad_split3"] = (ops.gate_grad_split3, (f32(n, e),))
+    cases["gate_dw_reduce"] = (ops.gate_dw_reduce, (f32(2, 3 * e, d), e))
     return cases
 
 
@@ -156,7 +161,8 @@ OPCHECK_NAMES = ["router", "router_backward", "reorder", "reorder_backward", "pe
                  "grouped_swiglu_f32", "grouped_swiglu_f32_backward",
                  "grouped_swiglu_fp8", "grouped_swiglu_fp8_backward", "grouped_swiglu_mxfp8",
                  "grouped_swiglu_mxfp8_backward", "grouped_swiglu_oss", "grouped_swiglu_oss_backward",
-                 "gather_rows", "scatter_rows", "swiglu_ffn_backward", "swiglu_ffn_backward_dw_only"]
+                 "gather_rows", "scatter_rows", "swiglu_ffn_backward", "swiglu_ffn_backward_dw_only",
+                 "swiglu_forward", "swiglu_backward", "gate_grad_split3", "gate_dw_reduce"]
 
 
 def test_opcheck_covers_every_op():

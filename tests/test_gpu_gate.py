@@ -170,3 +170,44 @@ def test_opt_in_gate_routing_disagreement(n_tokens, zipf):
     print(f"[case] opt-in gate: {differ} of {total} tokens routed to another expert set ({rate:.2e})",
           flush=True)
     assert rate <= 1e-3
+
+
+@pytest.mark.parametrize("shape", [(16384, 256), (1000, 64), (3, 8)])
+def test_gate_grad_split3_kernel_matches_torch_casts(shape):
+    """ops.gate_grad_split3 equals the three torch casts and subtractions of the
+    oracle run on the device, bit for bit, over twelve decades of magnitude,
+    signed zeros, infinities and NaN; the terms add back to the gradient."""
+    from oracle.moe_ref import gate_grad_split3
+    from torchtitan_amd import ops
+
+    n, e = shape
+    banner(f"gate split3 {n}x{e}")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    d = torch.randn(n, e, generator=g, device=dev) * torch.exp(
+        torch.empty(n, e, device=dev).uniform_(-14.0, 14.0, generator=g))
+    d[0, :4] = torch.tensor([0.0, -0.0, float("inf"), float("nan")], device=dev)
+    got = ops.gate_grad_split3(d)
+    want = gate_grad_split3(d)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    fin = torch.isfinite(d)
+    hi, mid, lo = (got[:, i * e:(i + 1) * e].float() for i in range(3))
+    assert torch.equal(((hi + mid) + lo)[fin], d[fin])
+
+
+@pytest.mark.parametrize("parts", [1, 2])
+@pytest.mark.parametrize("e_d", [(256, 2304), (8, 256)])
+def test_gate_dw_reduce_kernel_matches_torch_adds(parts, e_d):
+    """ops.gate_dw_reduce equals the oracle's fp32 adds ((halves), then
+    (hi + mid) + lo) and bf16 cast run on the device, bit for bit."""
+    from oracle.moe_ref import gate_dw_reduce
+    from torchtitan_amd import ops
+
+    e, d = e_d
+    banner(f"gate dw reduce parts={parts} e={e} d={d}")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(9)
+    shape = (parts, 3 * e, d) if parts == 2 else (3 * e, d)
+    p = torch.randn(*shape, generator=g, device=dev) * torch.exp(
+        torch.empty(*shape, device=dev).uniform_(-8.0, 8.0, generator=g))
+    assert torch.equal(ops.gate_dw_reduce(p, e).view(torch.int16), gate_dw_reduce(p, e).view(torch.int16))

@@ -85,3 +85,42 @@ def test_shared_expert_matches_reference_module(dev, case):
               f"elements != bf16(fp64) ours {frac_o:.2e} ref {frac_r:.2e}", flush=True)
         assert ratio_o <= 1.0
         assert frac_o <= frac_r + 1e-3
+
+
+SWIGLU_CASES = {
+    # rows, Hs, dtype, element offset of the views (0: 16-byte aligned)
+    "bf16_kimi": (16384, 1024, torch.bfloat16, 0),
+    "bf16_width_1000": (257, 1000, torch.bfloat16, 0),
+    "bf16_width_97_scalar": (300, 97, torch.bfloat16, 0),
+    "bf16_misaligned": (64, 256, torch.bfloat16, 3),
+    "fp32_512": (333, 512, torch.float32, 0),
+    "fp32_width_30_scalar": (100, 30, torch.float32, 0),
+}
+
+
+@pytest.mark.parametrize("case", list(SWIGLU_CASES))
+def test_swiglu_kernels_match_torch_ops_and_autograd(dev, case):
+    """ops.swiglu_forward is torch's silu(a1) * a3 and ops.swiglu_backward its
+    autograd (silu_backward(dh * a3, a1) | dh * silu(a1)) bit for bit, run by torch
+    on the same device; widths off the 16-byte chunk and misaligned views take the
+    one-element-per-thread kernels."""
+    from torchtitan_amd import ops
+
+    rows, hs, dt, off = SWIGLU_CASES[case]
+    banner(f"swiglu kernels {case}")
+    g = torch.Generator(device=dev).manual_seed(11)
+
+    def t(scale):
+        base = (torch.randn(rows * hs + off, generator=g, device=dev) * scale).to(dt)
+        return base[off:].view(rows, hs)
+
+    a1, a3, dh = t(3.0), t(1.0), t(0.5)
+    a1[0, : min(hs, 4)] = torch.tensor([0.0, -0.0, 30.0, -30.0][: min(hs, 4)], device=dev).to(dt)
+    h = ops.swiglu_forward(a1, a3)
+    assert torch.equal(h, F.silu(a1) * a3)
+    ra1, ra3 = a1.clone().requires_grad_(True), a3.clone().requires_grad_(True)
+    (F.silu(ra1) * ra3).backward(dh)
+    dgu = ops.swiglu_backward(dh, a1, a3)
+    assert dgu.shape == (rows, 2 * hs)
+    assert torch.equal(dgu[:, :hs], ra1.grad)
+    assert torch.equal(dgu[:, hs:], ra3.grad)

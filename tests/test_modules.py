@@ -282,13 +282,40 @@ def test_gate_gradient_split_is_exact():
     """The gate backward's three bf16 terms add back to the fp32 gradient exactly
     (8 + 8 + 8 significand bits), over twelve decades and both signs; two terms
     would not."""
-    from torchtitan_amd.moe import _bf16_terms
+    from oracle.moe_ref import gate_grad_split3
 
     g = torch.Generator().manual_seed(3)
     d = torch.randn(512, 64, generator=g) * torch.exp(torch.empty(512, 64).uniform_(-14.0, 14.0, generator=g))
     d[0, :4] = torch.tensor([0.0, -0.0, 1.0 + 2.0 ** -23, -(2.0 - 2.0 ** -23)])
-    t = _bf16_terms(d)
+    t = gate_grad_split3(d)
     assert t.dtype == torch.bfloat16 and t.shape == (512, 192)
     hi, mid, lo = (t[:, i * 64:(i + 1) * 64].float() for i in range(3))
     assert torch.equal((hi + mid) + lo, d)
     assert not torch.equal(hi + mid, d)
+
+
+@pytest.mark.parametrize("halves", [False, True])
+def test_gate_dw_reduce_reassembles_the_gradient(halves):
+    """dW from the three-term partials: with one-hot token rows every partial sum
+    is one exact product, so (hi + mid) + lo of the (half-added) partials is the
+    fp32 gradient itself and dW = bf16(d^T x) exactly; dropping a term, or one
+    token half, changes the result."""
+    from oracle.moe_ref import gate_dw_reduce, gate_grad_split3
+
+    g = torch.Generator().manual_seed(5)
+    n, e, dim = 64, 8, 96
+    d = torch.randn(n, e, generator=g) * torch.exp(torch.empty(n, e).uniform_(-6.0, 6.0, generator=g))
+    x = torch.zeros(n, dim)
+    x[torch.arange(n), torch.randperm(dim, generator=g)[:n]] = 1.0  # each token hits its own column
+    t = gate_grad_split3(d).float()
+    if halves:
+        parts = torch.stack([t[: n // 2].t() @ x[: n // 2], t[n // 2:].t() @ x[n // 2:]])
+    else:
+        parts = t.t() @ x
+    want = (d.t() @ x).bfloat16()
+    assert torch.equal(gate_dw_reduce(parts, e), want)
+    p = parts.clone()
+    p[..., 2 * e:, :] = 0.0  # drop lo
+    assert not torch.equal(gate_dw_reduce(p, e), want)
+    if halves:
+        assert not torch.equal(gate_dw_reduce(parts[0], e), want)

@@ -26,6 +26,10 @@ F32 = ctypes.c_float
 SIGNATURES: dict[str, list] = {
     "moe_router_fwd": [P, P, I64, I32, I32, I32, I32, I32, I32, F32, I32, P, P, P, P],
     "moe_router_bwd": [P, P, P, I64, I32, I32, I32, I32, F32, P, P],
+    "moe_gate_grad_split3": [P, I64, I32, P, P],
+    "moe_gate_dw_reduce": [P, I32, I32, I32, P, P],
+    "moe_swiglu_fwd": [P, P, I64, I32, I32, P, P],
+    "moe_swiglu_bwd": [P, P, P, I64, I32, I32, P, P],
     "moe_reorder_workspace_bytes": [I64, I32],
     "moe_histogram": [P, I64, I32, I32, P, I64, P, P, P],
     "moe_reorder": [P, P, I64, I32, I32, P, I64, P, P, P, P, P, P, P],

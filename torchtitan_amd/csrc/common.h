@@ -75,6 +75,32 @@ __device__ __forceinline__ uint2 pack4(const float (&v)[4]) {
 }
 
 
+// 16-byte chunks of a bf16 (uint16_t) or fp32 row: 8 or 4 elements widened to
+// fp32, and packed back with the row type's rounding.
+template <typename T> struct Chunk;
+template <> struct Chunk<uint16_t> {
+  static constexpr int kN = 8;
+  static __device__ __forceinline__ void unpack(uint4 v, float (&f)[8]) {
+    f[0] = bf_lo(v.x); f[1] = bf_hi(v.x); f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+    f[4] = bf_lo(v.z); f[5] = bf_hi(v.z); f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+  }
+  static __device__ __forceinline__ uint4 pack(const float (&f)[8]) {
+    return make_uint4(pack_bf2(f[0], f[1]), pack_bf2(f[2], f[3]), pack_bf2(f[4], f[5]), pack_bf2(f[6], f[7]));
+  }
+  static __device__ __forceinline__ float round(float f) { return round_bf(f); }
+};
+template <> struct Chunk<float> {
+  static constexpr int kN = 4;
+  static __device__ __forceinline__ void unpack(uint4 v, float (&f)[4]) {
+    f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+  }
+  static __device__ __forceinline__ uint4 pack(const float (&f)[4]) {
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+  }
+  static __device__ __forceinline__ float round(float f) { return f; }
+};
+
 // ---------------------------------------------------------------------------
 // Order-preserving map of fp32 onto uint32 used for top-k selection: larger
 // key == larger value, -0.0 sorts below +0.0 and every NaN is the largest key.

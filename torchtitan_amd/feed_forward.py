@@ -8,6 +8,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import ops
 from .configurable import Module
 from .linear import Linear
 
@@ -25,40 +26,41 @@ def compute_ffn_hidden_dim(dim: int, *, multiple_of: int = 1, ffn_dim_multiplier
 @torch.library.custom_op("moe_mi355x::swiglu_ffn_backward", mutates_args=())
 def swiglu_ffn_backward(
     dy: torch.Tensor, x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor,
-    a1: torch.Tensor, a3: torch.Tensor, s: torch.Tensor, h: torch.Tensor,
+    a1: torch.Tensor, a3: torch.Tensor, h: torch.Tensor,
     need_dx: bool, need_dw13: bool, need_dw2: bool,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dx, [dW1; dW3], dW2) of w2(silu(w1 x) * w3 x) from the forward's a1 = w1 x,
-    a3 = w3 x, s = silu(a1) and h = s * a3; unrequested results are empty.
+    a3 = w3 x and h = silu(a1) * a3; unrequested results are empty.
 
-    dh = dy w2, dW2 = dy^T h, du = dh * s and dg = silu_backward(dh * a3, a1) are
-    autograd's own calls and roundings, dx = (dg w1) + (du w3) its sum. dg and du
-    are written side by side into one [tokens, 2 Hs] buffer, so [dW1; dW3] is a
-    single dgu^T x GEMM (fp32 accumulation, one rounding per element). A custom op,
-    so that a compiled graph calls it whole: the side-by-side writes are out=
-    views that graph capture does not trace."""
+    dh = dy w2, dW2 = dy^T h, du = dh * silu(a1) and dg = silu_backward(dh * a3, a1)
+    are autograd's own calls and roundings, dx = (dg w1) + (du w3) its sum. dg and du
+    are written side by side into one [tokens, 2 Hs] buffer (on the GPU by one
+    launch, ops.swiglu_backward, which recomputes silu(a1) instead of reading it),
+    so [dW1; dW3] is a single dgu^T x GEMM (fp32 accumulation, one rounding per
+    element). A custom op, so that a compiled graph calls it whole: the CPU path's
+    side-by-side writes are out= views that graph capture does not trace."""
     d, hs = x.shape[-1], w1.shape[0]
     x2, dy2 = x.reshape(-1, d), dy.reshape(-1, d)
     empty = x.new_empty(0)
     dh = dy2.mm(w2)
     dw2 = dy2.t().mm(h.reshape(-1, hs)) if need_dw2 else empty
-    dgu = torch.empty(x2.shape[0], 2 * hs, dtype=dh.dtype, device=dh.device)
-    dg, du = dgu[:, :hs], dgu[:, hs:]
-    torch.mul(dh, s.reshape(-1, hs), out=du)
-    dsilu = dh * a3.reshape(-1, hs)
-    if dg.device.type == "cpu":
+    a1_2, a3_2 = a1.reshape(-1, hs), a3.reshape(-1, hs)
+    if dh.device.type == "cpu":
+        dgu = torch.empty(x2.shape[0], 2 * hs, dtype=dh.dtype, device=dh.device)
+        torch.mul(dh, F.silu(a1_2), out=dgu[:, hs:])
         # the CPU's vectorised kernel (contiguous output) and its strided one
-        # evaluate exp differently; the GPU's elementwise kernels do not
-        dg.copy_(torch.ops.aten.silu_backward(dsilu, a1.reshape(-1, hs)))
+        # evaluate exp differently
+        dgu[:, :hs].copy_(torch.ops.aten.silu_backward(dh * a3_2, a1_2))
     else:
-        torch.ops.aten.silu_backward.grad_input(dsilu, a1.reshape(-1, hs), grad_input=dg)
+        dgu = ops.swiglu_backward(dh, a1_2, a3_2)
+    dg, du = dgu[:, :hs], dgu[:, hs:]
     dx = (dg.mm(w1) + du.mm(w3)).view(x.shape) if need_dx else empty.clone()
     dw13 = dgu.t().mm(x2) if need_dw13 else empty.clone()
     return dx, dw13, dw2
 
 
 @swiglu_ffn_backward.register_fake
-def _(dy, x, w1, w2, w3, a1, a3, s, h, need_dx, need_dw13, need_dw2):
+def _(dy, x, w1, w2, w3, a1, a3, h, need_dx, need_dw13, need_dw2):
     hs, d = w1.shape
     return (x.new_empty(x.shape if need_dx else (0,)), x.new_empty((2 * hs, d) if need_dw13 else (0,)),
             x.new_empty((d, hs) if need_dw2 else (0,)))
@@ -68,8 +70,9 @@ class _SwiGLUFFN(torch.autograd.Function):
     """w2(silu(w1 x) * w3 x) for bias-free projections, with one GEMM for the
     weight gradients of w1 and w3.
 
-    Forward: the same F.linear, silu and mul calls as the three nn.Linear
-    modules (feed_forward.py:53-54), so the output is theirs bit for bit.
+    Forward: the same F.linear calls as the three nn.Linear modules
+    (feed_forward.py:53-54), and silu(a1) * a3 with torch's two roundings (on the
+    GPU one launch, ops.swiglu_forward), so the output is theirs bit for bit.
     Backward: dh = dy w2, dW2 = dy^T h, dx = (dg w1) + (du w3) and the SwiGLU
     derivative (dg = silu_backward(dh * u, g), du = dh * silu(g)) are autograd's
     own calls and roundings (swiglu_ffn_backward). dg and du are written side by
@@ -82,16 +85,15 @@ class _SwiGLUFFN(torch.autograd.Function):
     def forward(ctx, x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor) -> torch.Tensor:
         a1 = F.linear(x, w1)
         a3 = F.linear(x, w3)
-        s = F.silu(a1)
-        h = s * a3
-        ctx.save_for_backward(x, w1, w2, w3, a1, a3, s, h)
+        h = F.silu(a1) * a3 if a1.device.type == "cpu" else ops.swiglu_forward(a1, a3)
+        ctx.save_for_backward(x, w1, w2, w3, a1, a3, h)
         return F.linear(h, w2)
 
     @staticmethod
     def backward(ctx, dy: torch.Tensor):
-        x, w1, w2, w3, a1, a3, s, h = ctx.saved_tensors
+        x, w1, w2, w3, a1, a3, h = ctx.saved_tensors
         need = ctx.needs_input_grad
-        dx, dw13, dw2 = swiglu_ffn_backward(dy, x, w1, w2, w3, a1, a3, s, h, need[0], need[1] or need[3], need[2])
+        dx, dw13, dw2 = swiglu_ffn_backward(dy, x, w1, w2, w3, a1, a3, h, need[0], need[1] or need[3], need[2])
         hs = w1.shape[0]
         return (dx if need[0] else None, dw13[:hs] if need[1] else None, dw2 if need[2] else None,
                 dw13[hs:] if need[3] else None)

@@ -140,26 +140,16 @@ class GroupedExperts(Module):
         return _run_experts_for_loop(w1, w2, w3, x, num_tokens_per_expert)
 
 
-def _bf16_terms(d: torch.Tensor) -> torch.Tensor:
-    """[N, C] fp32 -> [N, 3C] bf16 (hi | mid | lo) with hi + mid + lo == d: each
-    term takes the next 8 significand bits of what the previous ones left, so
-    three cover fp32's 24."""
-    hi = d.bfloat16()
-    r = d - hi.float()
-    mid = r.bfloat16()
-    lo = (r - mid.float()).bfloat16()
-    return torch.cat([hi, mid, lo], dim=1)
-
-
 def _gate_backward_bf16(ctx, grad: torch.Tensor):
     """dx, dW (and the bias gradient) of fp32 logits = x W^T (+ b) for bf16 x and
-    W: the fp32 logit gradient is split exactly into three bf16 terms
-    (_bf16_terms), and dx, dW are bf16 GEMMs over the 3x longer sum -- exact
-    products accumulated in fp32, as the fp32 GEMMs of the autocast backward,
-    in another summation order -- rounded to x's and W's dtype once, as
-    autocast's casts do."""
+    W: the fp32 logit gradient d is split exactly into three bf16 terms
+    (ops.gate_grad_split3: hi = bf16(d), mid = bf16(d - hi), lo = bf16(d - hi -
+    mid), hi + mid + lo == d), and dx, dW are bf16 GEMMs over the 3x longer sum
+    -- exact products accumulated in fp32, as the fp32 GEMMs of the autocast
+    backward, in another summation order -- rounded to x's and W's dtype once,
+    as autocast's casts do."""
     x, w = ctx.saved_tensors
-    d3 = _bf16_terms(grad.float().contiguous())
+    d3 = ops.gate_grad_split3(grad)
     dx = dw = db = None
     if ctx.needs_input_grad[0]:
         dx = torch.mm(d3, torch.cat([w, w, w], dim=0))  # fp32 accumulation, one rounding to bf16
@@ -171,10 +161,10 @@ def _gate_backward_bf16(ctx, grad: torch.Tensor):
             # tiles for the chip; the fp32 halves are added before the one rounding
             dw3 = torch.bmm(d3.view(2, n // 2, 3 * e).transpose(1, 2), x.view(2, n // 2, -1),
                             out_dtype=torch.float32)
-            dw3 = dw3[0] + dw3[1]
         else:
             dw3 = torch.mm(d3.t(), x, out_dtype=torch.float32)
-        dw = ((dw3[:e] + dw3[e:2 * e]) + dw3[2 * e:]).to(w.dtype)
+        # bf16((hi + mid) + lo) of the (half-summed) fp32 partials, one launch
+        dw = ops.gate_dw_reduce(dw3, e)
     if ctx.has_bias and ctx.needs_input_grad[2]:
         db = grad.float().sum(0).to(ctx.b_dtype)
     return dx, dw, db
@@ -227,7 +217,7 @@ def gate_logits_f32(x: torch.Tensor, gate: nn.Linear, bf16_mfma: bool = False) -
     The logits are by default those of the reference's own call, ``gate(x)``
     under ``torch.autocast(dtype=float32)``: the same fp32 GEMM, so that top-k
     selection matches it exactly. For bf16 x and W on the GPU (outside an outer
-    autocast) that forward runs in _GateRef, whose backward takes bf16 GEMMs
+    autocast; E and D multiples of 4) that forward runs in _GateRef, whose backward takes bf16 GEMMs
     over an exact three-term split of the logit gradient instead of fp32 GEMMs;
     anything else runs the autocast region as is.
 
@@ -238,6 +228,7 @@ def gate_logits_f32(x: torch.Tensor, gate: nn.Linear, bf16_mfma: bool = False) -
     w, b = _local(gate.weight), gate.bias
     b = _local(b) if b is not None else None
     if (x.is_cuda and x.dim() == 2 and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and w.shape[0] % 4 == 0 and w.shape[1] % 4 == 0
             and (b is None or b.dtype in (torch.bfloat16, torch.float32))
             and not torch.is_autocast_enabled(x.device.type)):
         fn = _GateF32 if bf16_mfma else _GateRef

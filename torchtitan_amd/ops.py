@@ -138,6 +138,88 @@ router.register_autograd(_router_bwd, setup_context=_router_setup)
 
 
 # ---------------------------------------------------------------------------
+# the gate's backward on bf16 GEMMs: exact three-term split, dW reduction
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::gate_grad_split3", mutates_args=())
+def gate_grad_split3(grad_logits: Tensor) -> Tensor:
+    """fp32 [N, C] -> bf16 [N, 3C] (hi | mid | lo) with hi + mid + lo == grad_logits."""
+    require_gpu(grad_logits)
+    d = grad_logits.float().contiguous()
+    n, c = d.shape
+    out = torch.empty(n, 3 * c, dtype=torch.bfloat16, device=d.device)
+    call("moe_gate_grad_split3", ptr(d), n, c, ptr(out), stream_of(d))
+    return out
+
+
+@gate_grad_split3.register_fake
+def _(grad_logits):
+    n, c = grad_logits.shape
+    return grad_logits.new_empty(n, 3 * c, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("moe_mi355x::gate_dw_reduce", mutates_args=())
+def gate_dw_reduce(partials: Tensor, num_experts: int) -> Tensor:
+    """fp32 partials [3E, D] or [2, 3E, D] (token halves) -> bf16 [E, D]:
+    bf16((hi + mid) + lo) of the half sums."""
+    require_gpu(partials)
+    p = partials.float().contiguous()
+    parts = 2 if p.dim() == 3 else 1
+    d = p.shape[-1]
+    if p.shape[-2] != 3 * num_experts or (parts == 2 and p.shape[0] != 2):
+        raise ValueError(f"gate_dw_reduce: partials {tuple(p.shape)} for {num_experts} experts")
+    out = torch.empty(num_experts, d, dtype=torch.bfloat16, device=p.device)
+    call("moe_gate_dw_reduce", ptr(p), parts, num_experts, d, ptr(out), stream_of(p))
+    return out
+
+
+@gate_dw_reduce.register_fake
+def _(partials, num_experts):
+    return partials.new_empty(num_experts, partials.shape[-1], dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# shared expert SwiGLU between its GEMMs (feed_forward.py:53-54)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("moe_mi355x::swiglu_forward", mutates_args=())
+def swiglu_forward(a1: Tensor, a3: Tensor) -> Tensor:
+    """h = silu(a1) * a3 with torch's roundings; a1, a3 [..., Hs] bf16 or fp32."""
+    require_gpu(a1, a3)
+    if a1.shape != a3.shape or a1.dtype != a3.dtype:
+        raise ValueError("swiglu_forward: a1 and a3 must have one shape and dtype")
+    a1c, a3c = a1.contiguous(), a3.contiguous()
+    hs = a1.shape[-1]
+    h = torch.empty_like(a1c)
+    call("moe_swiglu_fwd", ptr(a1c), ptr(a3c), a1c.numel() // max(hs, 1), hs, _dtype_code(a1c), ptr(h),
+         stream_of(a1c))
+    return h
+
+
+@swiglu_forward.register_fake
+def _(a1, a3):
+    return torch.empty_like(a1)
+
+
+@torch.library.custom_op("moe_mi355x::swiglu_backward", mutates_args=())
+def swiglu_backward(dh: Tensor, a1: Tensor, a3: Tensor) -> Tensor:
+    """dgu [rows, 2 Hs]: silu_backward(dh * a3, a1) | dh * silu(a1), torch's roundings."""
+    require_gpu(dh, a1, a3)
+    if not (dh.shape == a1.shape == a3.shape) or not (dh.dtype == a1.dtype == a3.dtype):
+        raise ValueError("swiglu_backward: dh, a1 and a3 must have one shape and dtype")
+    hs = a1.shape[-1]
+    rows = a1.numel() // max(hs, 1)
+    dhc, a1c, a3c = dh.contiguous(), a1.contiguous(), a3.contiguous()
+    dgu = torch.empty(rows, 2 * hs, dtype=a1.dtype, device=a1.device)
+    call("moe_swiglu_bwd", ptr(dhc), ptr(a1c), ptr(a3c), rows, hs, _dtype_code(a1c), ptr(dgu), stream_of(a1c))
+    return dgu
+
+
+@swiglu_backward.register_fake
+def _(dh, a1, a3):
+    hs = a1.shape[-1]
+    return a1.new_empty(a1.numel() // max(hs, 1), 2 * hs)
+
+
+# ---------------------------------------------------------------------------
 # reorder: counting-sort permutation by expert
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("moe_mi355x::reorder", mutates_args=())
