@@ -348,7 +348,9 @@ __global__ __launch_bounds__(256) void permute_bwd_kernel(
       pos[k] = (k < K) ? tok_pos[t * K + k] : 0;
       sc[k] = (k < K && scores_sorted) ? scores_sorted[pos[k]] : 1.0f;
     }
-    constexpr int HK = MAXK / 2;  // row chunks loaded in two batches of HK
+    // row chunks loaded in batches of HK: all eight at once for K <= 8 (4 % faster
+    // than two batches of four at the Kimi shape), two batches above
+    constexpr int HK = MAXK <= 8 ? MAXK : MAXK / 2, NB = MAXK / HK;
     for (int ch = lane; ch < cpr; ch += kWave) {
       uint4 xv = make_uint4(0, 0, 0, 0);
       if (scores_sorted) xv = *(const uint4*)(x + t * D + ch * n);
@@ -356,7 +358,7 @@ __global__ __launch_bounds__(256) void permute_bwd_kernel(
 #pragma unroll
       for (int i = 0; i < n; ++i) a[i] = 0.f;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NB; ++h) {
         uint4 gk[HK];
 #pragma unroll
         for (int kk = 0; kk < HK; ++kk) {
@@ -620,6 +622,7 @@ MOE_API int moe_combine_bwd(const void* grad_out, const void* routed_output, con
                                        grad_routed, grad_scores_sorted, stream);
   } else {
     if (!slot_pos) return kErrInvalidArgument;
+    // plain stores: streaming ones measure 13 % faster alone but 9 % slower in the layer step
     if (dtype == MOE_DTYPE_BF16)
       launch_expand<uint16_t>(grad_out, n_tokens, dim, top_k, slot_pos, nullptr, grad_routed, false, stream);
     else
