@@ -945,6 +945,28 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
     // 16-column blocks are stored as 64-byte row pieces (span64) at column
     // 32 jp + 8 (lane / 16) of the wave's span ----
     const int g8 = 8 * g4;
+    // rowwise fp8, dgu and dW: the row scales of the wave's rows and the column
+    // scales of its columns are loaded before the first store (a load issued after a
+    // store, which may alias it, waits behind it: one round trip per tile instead of
+    // one per scale; dW 2.51 -> 2.07 ms, dw2 1.28 -> 1.02 ms at 32768 Kimi tokens).
+    // Rows past the segment read the segment's last row. The other epilogues keep
+    // their loads in the loop: hoisted, their 32 more live registers cost the main
+    // loop 5-12 %.
+    constexpr bool kHoist = !MX && (MODE == kDgu || MODE >= kDw13);
+    float spr[TM];
+    float4 sqc[TN];
+    if constexpr (kHoist) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = nt * BN + wn * WN + j * 16 + nql;
+        sqc[j] = *(const float4*)((MODE == kDgu ? p.sq + e64 * H : p.sq + e64 * Ntot) + n);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        if (kRowGrouped) spr[i] = p.sp[min(row0 + wm * WM + i * 16 + ml, seg1 - 1)];
+        else spr[i] = p.sp[e64 * Mfix + mt * BM + wm * WM + i * 16 + ml];
+      }
+    }
     if (MODE == kGateUp) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -984,6 +1006,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
           const float sp = MX ? 1.f : ((MODE == kDx) ? p.sp[(int64_t)r * 2 + 1] : p.sp[r]);
+          // MXFP8 dx: the parked w1 half of the row, read back before the row's stores
+          // (rowwise fp8 reads it piece by piece: its scale loads already hold the
+          // registers this would take)
+          constexpr bool kBatchPark = MODE == kDx && MX;
+          uint2 pws[kBatchPark ? TN : 1];
+          if constexpr (kBatchPark) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) pws[j] = *(const uint2*)(p.o0 + (int64_t)r * D + nt * BN + wn * WN + j * 16 + nql);
+          }
 #pragma unroll
           for (int jp = 0; jp < TN / 2; ++jp) {
             uint2 pv[2];
@@ -1000,8 +1031,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) v[q] = (acc[i][j][q] * sp) * sq[q];
               }
-              if (MODE == kDx) {
-                const uint2 pw = *(const uint2*)(p.o0 + (int64_t)r * D + n);
+              if constexpr (MODE == kDx) {
+                uint2 pw;
+                if constexpr (kBatchPark) pw = pws[j];
+                else pw = *(const uint2*)(p.o0 + (int64_t)r * D + n);
                 v[0] = bf_lo(pw.x) + round_bf(v[0]);
                 v[1] = bf_hi(pw.x) + round_bf(v[1]);
                 v[2] = bf_lo(pw.y) + round_bf(v[2]);
@@ -1019,23 +1052,35 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
         if (r < seg1) {
-          const float sp = MX ? 1.f : p.sp[r];
+          const float sp = MX ? 1.f : spr[i];
+          // the g and u pieces of half the row's columns at a time, loaded before their
+          // stores (registers for all of them at once would spill)
+          uint2 gws[TN / 2], uws[TN / 2];
 #pragma unroll
           for (int jp = 0; jp < TN / 2; ++jp) {
+            if (jp % (TN / 4) == 0) {
+#pragma unroll
+              for (int jj = 0; jj < TN / 2; ++jj) {
+                const int64_t off = (int64_t)r * H + nt * BN + wn * WN + (2 * jp + jj) * 16 + nql;
+                gws[jj] = *(const uint2*)(p.g + off);
+                uws[jj] = *(const uint2*)(p.u + off);
+              }
+            }
             uint2 pdg[2], pdu[2];
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
               const int j = 2 * jp + h2;
-              const int hh = nt * BN + wn * WN + j * 16 + nql;
-              const int64_t off = (int64_t)r * H + hh;
-              const uint2 gw = *(const uint2*)(p.g + off);
-              const uint2 uw = *(const uint2*)(p.u + off);
+              const uint2 gw = gws[j % (TN / 2)], uw = uws[j % (TN / 2)];
               const float gv[4] = {bf_lo(gw.x), bf_hi(gw.x), bf_lo(gw.y), bf_hi(gw.y)};
               const float uv[4] = {bf_lo(uw.x), bf_hi(uw.x), bf_lo(uw.y), bf_hi(uw.y)};
               float dg[4], du[4];
+              float sq4[4] = {1.f, 1.f, 1.f, 1.f};
+              if constexpr (!MX) {
+                sq4[0] = sqc[j].x; sq4[1] = sqc[j].y; sq4[2] = sqc[j].z; sq4[3] = sqc[j].w;
+              }
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
-                const float dh = round_bf(MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * H + hh + q]);
+                const float dh = round_bf(MX ? acc[i][j][q] : (acc[i][j][q] * sp) * sq4[q]);
                 const float sl = round_bf(silu_f(gv[q]));
                 const float dsl = round_bf(dh * uv[q]);
                 du[q] = dh * sl;
@@ -1057,7 +1102,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
       for (int i = 0; i < TM; ++i) {
         const int m = mt * BM + wm * WM + i * 16 + ml;
         // an expert without tokens gets zero gradients (its scales are never written)
-        const float sp = (nk > 0) ? (MX ? 1.f : p.sp[e64 * Mfix + m]) : 0.f;
+        const float sp = MX ? 1.f : spr[i];
         uint16_t* rowp;
         if (MODE == kDw13)
           rowp = (m < H) ? p.o0 + (e64 * H + m) * (int64_t)D : p.o1 + (e64 * H + (m - H)) * (int64_t)D;
@@ -1071,9 +1116,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
             const int j = 2 * jp + h2;
             const int n = nt * BN + wn * WN + j * 16 + nql;
             float v[4];
+            float sq4[4] = {1.f, 1.f, 1.f, 1.f};
+            if constexpr (!MX) {
+              sq4[0] = sqc[j].x; sq4[1] = sqc[j].y; sq4[2] = sqc[j].z; sq4[3] = sqc[j].w;
+            }
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              v[q] = (nk > 0) ? (MX ? acc[i][j][q] : (acc[i][j][q] * sp) * p.sq[e64 * Ntot + n + q]) : 0.f;
+            for (int q = 0; q < 4; ++q) v[q] = (nk > 0) ? (MX ? acc[i][j][q] : (acc[i][j][q] * sp) * sq4[q]) : 0.f;
             pv[h2] = pack4(v);
           }
           *(uint4*)(rowp + nt * BN + wn * WN + jp * 32 + g8) = span64(pv[0], pv[1], lane);
