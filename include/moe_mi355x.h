@@ -328,6 +328,21 @@ int moe_fp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int32_
                          int64_t q_expert_stride, int64_t q_row_stride, float* scale,
                          int64_t scale_expert_stride, moe_stream_t stream);
 
+/* moe_fp8_quant_cols_t with the column amax [E, b] already known (from
+ * moe_fp8_quant_rows_colamax of the same x): x is read once. */
+int moe_fp8_quant_cols_t_amax(const uint16_t* x, const float* col_amax, int32_t n_experts, int32_t a,
+                              int32_t b, uint8_t* q, int64_t q_expert_stride, int64_t q_row_stride,
+                              float* scale, int64_t scale_expert_stride, moe_stream_t stream);
+
+/* The weights' two rowwise quantizations (torchao's float8 grouped GEMM quantizes
+ * each weight along the forward's and the backward's contraction,
+ * quantization/float8.py:260-288) from two reads instead of three: x [E, a, b]
+ * bf16 -> q [E, a, b] fp8 with one scale per row (as moe_fp8_quant_rows over b),
+ * and col_amax [E, b] = the amax over a of each column (NaN ignored), max-
+ * accumulated: the caller zeroes it. b % 8 == 0, b <= 4096. */
+int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
+                               float* scale, float* col_amax, moe_stream_t stream);
+
 /* x [n_rows, cols] bf16 in expert token groups (counts) -> q [cols, padded_rows]
  * fp8 with group e at the 16-aligned offset sum_{e'<e} ceil16(count_e') and
  * zero padding up to ceil16(count_e); scale [E, cols] over the group's tokens

@@ -190,6 +190,60 @@ def test_fp8_quantizers_bit_exact(dev):
 
 
 
+@pytest.mark.parametrize("shape", [(8, 1024, 2304), (4, 2304, 1024), (3, 100, 264), (2, 37, 4096)])
+def test_fp8_weight_quantizers_from_two_reads(dev, shape):
+    """moe_fp8_quant_rows_colamax: the row-quantized bytes and scales equal the
+    oracle's (as moe_fp8_quant_rows), and the column amax equals max |x| over the
+    rows; moe_fp8_quant_cols_t_amax from that amax equals the oracle's transposed
+    quantization. With an inf and NaNs planted (which the oracle's unsaturated cast
+    and NaN-propagating amax do not model), the two-read path still equals the
+    kernels that find their own amax: moe_fp8_quant_rows and moe_fp8_quant_cols_t
+    (NaN ignored by the amax, as fmaxf does)."""
+    from torchtitan_amd import _lib, ops
+
+    e, a, b = shape
+    banner(f"fp8 weight quantizers {shape}")
+    g = torch.Generator().manual_seed(a + b)
+    w = (torch.randn(e, a, b, generator=g) * torch.exp(torch.randn(e, a, 1, generator=g) * 2)).bfloat16()
+    w[0, 3] = 0  # an all-zero row
+    stream = torch.cuda.current_stream().cuda_stream
+    transposable = a % 16 == 0 and b % 64 == 0  # the transposing quantizers' shape rule
+
+    def two_read(wd):
+        q, sc, amax = ops._quant_rows_colamax(wd)
+        qt = st = None
+        if transposable:
+            qt = torch.empty(e, b, a, dtype=torch.uint8, device=dev)
+            st = torch.empty(e, b, dtype=torch.float32, device=dev)
+            ops._quant_cols_t(wd, amax, qt, 0, b * a, a, st, 0, b)
+        return q, sc, amax, qt, st
+
+    q, sc, amax, qt, st = two_read(w.to(dev))
+    rq, rs = R.quant_fp8_rows(w.view(e * a, b))
+    assert torch.equal(q.view(e * a, b).cpu(), rq.view(torch.uint8))
+    assert torch.equal(sc.cpu(), rs.view(-1))
+    assert torch.equal(amax.cpu(), w.float().abs().amax(dim=1))
+    if transposable:
+        for i in range(e):
+            rq, rs = R.quant_fp8_rows(w[i].t())
+            assert torch.equal(qt[i].cpu(), rq.view(torch.uint8))
+            assert torch.equal(st[i].cpu(), rs.view(-1))
+    # non-finite values: against the one-read-per-layout kernels
+    w[e - 1, a // 2, 5] = float("inf")
+    w[0, 1, 7] = float("nan")
+    w[e - 1, :, 9] = float("nan")  # a column of NaN: amax 0
+    wd = w.to(dev)
+    q, sc, amax, qt, st = two_read(wd)
+    q1, s1 = ops._quant_rows(wd, b)
+    assert torch.equal(q.view(e * a, b), q1.view(e * a, b)) and torch.equal(sc, s1)
+    wf = w.float().abs()
+    assert torch.equal(amax.cpu(), torch.where(torch.isnan(wf), torch.zeros_like(wf), wf).amax(dim=1))
+    if transposable:
+        qt2, st2 = torch.empty_like(qt), torch.empty_like(st)
+        _lib.call("moe_fp8_quant_cols_t", wd.data_ptr(), e, a, b, qt2.data_ptr(), b * a, a, st2.data_ptr(), b, stream)
+        assert torch.equal(qt, qt2) and torch.equal(st, st2)
+
+
 @pytest.mark.parametrize("width", [192, 320, 384])
 def test_fp8_transposing_quantizers_slab_widths(dev, width):
     """The transposing quantizers at widths that take 64-column slabs (192, 320)
@@ -243,7 +297,7 @@ def test_fp8_grouped_swiglu_fwd_bwd(dev, name):
     dy = torch.randn(r, d, generator=g).bfloat16()
     cnt = torch.tensor(counts, dtype=torch.int64)
     xs, a, b, c = (t.to(dev).requires_grad_(True) for t in (x, w1, w2, w3))
-    y, gg, uu, hh = ops.grouped_swiglu_fp8(xs, a, b, c, cnt.to(dev))
+    y, gg, uu, hh, *_ = ops.grouped_swiglu_fp8(xs, a, b, c, cnt.to(dev))
     y.backward(dy.to(dev))
     torch.cuda.synchronize()
     # fp8 emulation

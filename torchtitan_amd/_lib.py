@@ -55,6 +55,8 @@ SIGNATURES: dict[str, list] = {
     "moe_fp8_padded_rows": [I64, I32],
     "moe_fp8_quant_rows": [P, I64, I32, P, P, P],
     "moe_fp8_quant_cols_t": [P, I32, I32, I32, P, I64, I64, P, I64, P],
+    "moe_fp8_quant_cols_t_amax": [P, P, I32, I32, I32, P, I64, I64, P, I64, P],
+    "moe_fp8_quant_rows_colamax": [P, I32, I32, I32, P, P, P, P],
     "moe_fp8_quant_tokens_t": [P, P, I64, I32, I32, I64, P, P, P],
     "moe_fp8_gemm_gate_up": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "moe_fp8_gemm_down": [P, P, P, P, P, I64, I32, I32, I32, P, P],

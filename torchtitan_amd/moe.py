@@ -89,7 +89,7 @@ def _run_experts_grouped_mm_fp8(
     """The fp8 grouped GEMMs the reference gets from torchao's
     Float8TrainingOpConfig (torchtitan/components/quantization/float8.py:260-288):
     dynamic rowwise e4m3 scaling, fp32 accumulation, bf16 outputs."""
-    y, _, _, _ = ops.grouped_swiglu_fp8(
+    y, *_ = ops.grouped_swiglu_fp8(
         x.bfloat16(), w1.bfloat16(), w2.bfloat16(), w3.bfloat16(), num_tokens_per_expert
     )
     return y.type_as(x)

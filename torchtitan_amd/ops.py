@@ -714,6 +714,32 @@ def _quant_rows(x: Tensor, cols: int) -> tuple[Tensor, Tensor]:
     return q, s
 
 
+def _quant_rows_colamax(w: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """w [E, A, B] bf16 -> (q [E, A, B] fp8 with a scale per row, scale [E * A],
+    column amax [E, B] over A): the row quantization and, on the side, what the
+    transposed one needs, from one read."""
+    e, a, b = w.shape
+    q = torch.empty(e, a, b, dtype=FP8, device=w.device)
+    s = torch.empty(e * a, dtype=torch.float32, device=w.device)
+    amax = torch.zeros(e, b, dtype=torch.float32, device=w.device)
+    call("moe_fp8_quant_rows_colamax", ptr(w), e, a, b, ptr(q), ptr(s), ptr(amax), stream_of(w))
+    return q, s, amax
+
+
+def _quant_cols_t(w: Tensor, amax: Tensor, q: Tensor, q_offset: int, q_estride: int, q_ld: int, scale: Tensor,
+                  s_offset: int, s_estride: int) -> None:
+    """Per expert and column of w [E, A, B]: the scale of the column amax and the
+    column quantized as a row of q (transposed); from the known amax when there
+    is one (one read of w), else with its own amax pass."""
+    e, a, b = w.shape
+    qp, sp = q.data_ptr() + q_offset, scale.data_ptr() + 4 * s_offset
+    if amax.numel():
+        call("moe_fp8_quant_cols_t_amax", ptr(w), ptr(amax), e, a, b, qp, q_estride, q_ld, sp, s_estride,
+             stream_of(w))
+    else:
+        call("moe_fp8_quant_cols_t", ptr(w), e, a, b, qp, q_estride, q_ld, sp, s_estride, stream_of(w))
+
+
 def _padded_rows(r: int, e: int) -> int:
     n = lib().moe_fp8_padded_rows(r, e)
     return (n + 15) // 16 * 16
@@ -731,9 +757,11 @@ def _quant_tokens_t(x: Tensor, counts: Tensor, e: int, rpad: int) -> tuple[Tenso
 @torch.library.custom_op("moe_mi355x::grouped_swiglu_fp8", mutates_args=())
 def grouped_swiglu_fp8(
     x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
-) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """fp8 e4m3 grouped SwiGLU: x, h quantized per token row, weights per
-    output row; fp32 accumulate; bf16 outputs (y, g, u, h)."""
+    output row; fp32 accumulate; bf16 outputs (y, g, u, h), then the weights'
+    column amax over the forward's output rows (w1, w3 [E, D], w2 [E, H]) that
+    the backward's transposed quantizations use."""
     require_gpu(x, w1, w2, w3, num_tokens_per_expert)
     for t, name in ((x, "x"), (w1, "w1"), (w2, "w2"), (w3, "w3")):
         if t.dtype != torch.bfloat16:
@@ -744,9 +772,9 @@ def grouped_swiglu_fp8(
     e, h_dim, _ = w1.shape
     s = stream_of(x)
     qx, sx = _quant_rows(x, d)
-    qw1, sw1 = _quant_rows(w1, d)
-    qw3, sw3 = _quant_rows(w3, d)
-    qw2, sw2 = _quant_rows(w2, h_dim)
+    qw1, sw1, am1 = _quant_rows_colamax(w1)
+    qw3, sw3, am3 = _quant_rows_colamax(w3)
+    qw2, sw2, am2 = _quant_rows_colamax(w2)
     g = x.new_empty(r, h_dim)
     u = x.new_empty(r, h_dim)
     h = x.new_empty(r, h_dim)
@@ -755,21 +783,25 @@ def grouped_swiglu_fp8(
          h_dim, ptr(g), ptr(u), ptr(h), s)
     qh, sh = _quant_rows(h, h_dim)
     call("moe_fp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
-    return y, g, u, h
+    return y, g, u, h, am1, am3, am2
 
 
 @grouped_swiglu_fp8.register_fake
 def _(x, w1, w2, w3, num_tokens_per_expert):
     r, d = x.shape
-    h_dim = w1.shape[1]
-    return x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim)
+    e, h_dim = w1.shape[0], w1.shape[1]
+    f32 = lambda *shape: x.new_empty(*shape, dtype=torch.float32)  # noqa: E731
+    return (x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim),
+            f32(e, d), f32(e, d), f32(e, h_dim))
 
 
 @torch.library.custom_op("moe_mi355x::grouped_swiglu_fp8_backward", mutates_args=())
 def grouped_swiglu_fp8_backward(
     dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
-    g: Tensor, u: Tensor, h: Tensor,
+    g: Tensor, u: Tensor, h: Tensor, amax_w1: Tensor, amax_w3: Tensor, amax_w2: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of grouped_swiglu_fp8. amax_w* are the forward's column amax of
+    the weights (empty tensors: the transposed quantizers take their own)."""
     require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
     dy = dy.to(torch.bfloat16).contiguous()
     counts = num_tokens_per_expert.to(torch.int64).contiguous()
@@ -781,7 +813,7 @@ def grouped_swiglu_fp8_backward(
     qdy, sdy = _quant_rows(dy, d)
     qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
     sw2t = torch.empty(e, h_dim, dtype=torch.float32, device=dev)
-    call("moe_fp8_quant_cols_t", ptr(w2), e, d, h_dim, ptr(qw2t), h_dim * d, d, ptr(sw2t), h_dim, s)
+    _quant_cols_t(w2.contiguous(), amax_w2.contiguous(), qw2t, 0, h_dim * d, d, sw2t, 0, h_dim)
     dgu = x.new_empty(r, 2 * h_dim)
     call("moe_fp8_gemm_bwd_dgu", ptr(qdy), ptr(sdy), ptr(qw2t), ptr(sw2t), ptr(g), ptr(u), ptr(counts), r, e, d,
          h_dim, ptr(dgu), s)
@@ -790,9 +822,8 @@ def grouped_swiglu_fp8_backward(
     qdgu, sdgu = _quant_rows(dgu, h_dim)
     qw13t = torch.empty(e, d, 2 * h_dim, dtype=FP8, device=dev)
     sw13t = torch.empty(e, 2, d, dtype=torch.float32, device=dev)
-    call("moe_fp8_quant_cols_t", ptr(w1), e, h_dim, d, ptr(qw13t), d * 2 * h_dim, 2 * h_dim, ptr(sw13t), 2 * d, s)
-    call("moe_fp8_quant_cols_t", ptr(w3), e, h_dim, d, qw13t.data_ptr() + h_dim, d * 2 * h_dim, 2 * h_dim,
-         sw13t.data_ptr() + 4 * d, 2 * d, s)
+    _quant_cols_t(w1.contiguous(), amax_w1.contiguous(), qw13t, 0, d * 2 * h_dim, 2 * h_dim, sw13t, 0, 2 * d)
+    _quant_cols_t(w3.contiguous(), amax_w3.contiguous(), qw13t, h_dim, d * 2 * h_dim, 2 * h_dim, sw13t, d, 2 * d)
     dx = x.new_empty(r, d)
     call("moe_fp8_gemm_bwd_dx", ptr(qdgu), ptr(sdgu), ptr(qw13t), ptr(sw13t), ptr(counts), r, e, d, h_dim,
          ptr(dx), s)
@@ -813,19 +844,27 @@ def grouped_swiglu_fp8_backward(
 
 
 @grouped_swiglu_fp8_backward.register_fake
-def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h):
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h, amax_w1, amax_w3, amax_w2):
     return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
 
 
-def _gs8_bwd(ctx, dy, _dg, _du, _dh):
-    x, w1, w2, w3, counts, g, u, h = ctx.saved_tensors
+def _gs8_setup(ctx, inputs, output):
+    x, w1, w2, w3, counts = inputs
+    _y, g, u, h, am1, am3, am2 = output
+    ctx.save_for_backward(x, w1, w2, w3, counts, g, u, h, am1, am3, am2)
+    ctx.mark_non_differentiable(g, u, h, am1, am3, am2)
+    ctx.set_materialize_grads(False)
+
+
+def _gs8_bwd(ctx, dy, *_unused):
+    x, w1, w2, w3, counts, g, u, h, am1, am3, am2 = ctx.saved_tensors
     if dy is None:
         return None, None, None, None, None
-    dx, dw1, dw2, dw3 = grouped_swiglu_fp8_backward(dy, x, w1, w2, w3, counts, g, u, h)
+    dx, dw1, dw2, dw3 = grouped_swiglu_fp8_backward(dy, x, w1, w2, w3, counts, g, u, h, am1, am3, am2)
     return dx, dw1, dw2, dw3, None
 
 
-grouped_swiglu_fp8.register_autograd(_gs8_bwd, setup_context=_gs_setup)
+grouped_swiglu_fp8.register_autograd(_gs8_bwd, setup_context=_gs8_setup)
 
 
 # ---------------------------------------------------------------------------
