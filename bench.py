@@ -159,6 +159,20 @@ def launch_bytes(name: str, a: tuple) -> float | None:
     if name == "moe_fp8_quant_cols_t":
         e, ra, cb = a[1], a[2], a[3]
         return 3.0 * e * ra * cb + 4.0 * e * cb
+    if name == "moe_fp8_quant_rows_colamax":  # + the [E, b] column amax written
+        e, ra, cb = a[1], a[2], a[3]
+        return 3.0 * e * ra * cb + 4.0 * e * ra + 4.0 * e * cb
+    if name == "moe_fp8_quant_cols_t_amax":  # the column amax read instead of found
+        e, ra, cb = a[2], a[3], a[4]
+        return 3.0 * e * ra * cb + 8.0 * e * cb
+    if name == "moe_swiglu_fwd":  # a1, a3 read, h written
+        return 3.0 * a[2] * a[3] * (2 if a[4] == 0 else 4)
+    if name == "moe_swiglu_bwd":  # dh, a1, a3 read, dg and du written
+        return 5.0 * a[3] * a[4] * (2 if a[5] == 0 else 4)
+    if name == "moe_gate_grad_split3":  # fp32 gradient read, three bf16 terms written
+        return 10.0 * a[1] * a[2]
+    if name == "moe_gate_dw_reduce":  # fp32 partials read, bf16 dW written
+        return 12.0 * a[1] * a[2] * a[3] + 2.0 * a[2] * a[3]
     if name == "moe_fp8_quant_tokens_t":
         rows, e, cols, padded = a[2], a[3], a[4], a[5]
         return 2.0 * rows * cols + 1.0 * padded * cols + 4.0 * e * cols + 8.0 * e
