@@ -514,6 +514,24 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     // Each lane produces 4 columns per 16-column block; pairs of blocks are stored
     // as 64-byte row pieces (span64), at column 32 jp + 8 (lane / 16) of the wave's span.
     const int g8 = 8 * (lane >> 4);
+    // gpt-oss biases: one per column, so loaded once per tile before the first store
+    // (a load issued after a store, which may alias it, waits behind it)
+    uint4 bias1[ACT == kOssGLU && MODE == kFwdGateUp ? TN / 2 : 1];
+    uint2 bias2[ACT == kOssGLU && MODE == kFwdDown ? TN : 1];
+    if constexpr (ACT == kOssGLU && MODE == kFwdGateUp) {
+#pragma unroll
+      for (int jj = 0; jj < TN / 2; ++jj) {
+        const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nq;
+        bias1[jj] = (!TAIL || hc < H) ? *(const uint4*)(p.b1 + e64 * 2 * H + 2 * hc) : make_uint4(0, 0, 0, 0);
+      }
+    }
+    if constexpr (ACT == kOssGLU && MODE == kFwdDown) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = nt * BN + wn * WN + j * 16 + nq;
+        bias2[j] = (!TAIL || n < D) ? *(const uint2*)(p.b2 + e64 * D + n) : make_uint2(0, 0);
+      }
+    }
     if (MODE == kFwdGateUp) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
@@ -529,8 +547,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
               float gv[4], uv[4], hv[4];
               if constexpr (ACT == kOssGLU) {
                 // h1 = bf16(x . mlp1^T) + bias (bf16 add), then the clamped SwiGLU
-                uint4 bw = make_uint4(0, 0, 0, 0);  // (glu, linear) x 4 columns
-                if (!TAIL || hc < H) bw = *(const uint4*)(p.b1 + e64 * 2 * H + 2 * hc);
+                const uint4 bw = bias1[jj];  // (glu, linear) x 4 columns
                 const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -596,7 +613,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
               const bool in = !TAIL || n < D;
               float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
               if (MODE == kFwdDown && ACT == kOssGLU) {  // bf16(h . mlp2^T) + mlp2_bias (bf16 add)
-                const uint2 bw = in ? *(const uint2*)(p.b2 + e64 * D + n) : make_uint2(0, 0);
+                const uint2 bw = bias2[j];
                 v[0] = round_bf(v[0]) + bf_lo(bw.x);
                 v[1] = round_bf(v[1]) + bf_hi(bw.x);
                 v[2] = round_bf(v[2]) + bf_lo(bw.y);
