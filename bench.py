@@ -191,6 +191,10 @@ def launch_bytes(name: str, a: tuple) -> float | None:
     if name == "moe_mxfp8_quant_dual_tokens":
         rows, e, cols, padded = a[2], a[3], a[4], a[5]
         return 2.0 * rows * cols + mx * rows * cols + mx * padded * cols + 8.0 * e
+    if name == "moe_mxfp8_quant_dual_tokens_gather":  # + the row indices (and scores) read
+        rows, e, cols, padded = a[5], a[6], a[7], a[8]
+        idx = (8.0 + (4.0 if a[3] else 0.0)) * rows
+        return 2.0 * rows * cols + mx * rows * cols + mx * padded * cols + 8.0 * e + idx
     return None
 
 

@@ -434,6 +434,17 @@ int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts, int64_
                                 int32_t cols, int64_t padded_rows, uint8_t* q_rows, uint8_t* scale_rows,
                                 uint8_t* q, uint8_t* scale, moe_stream_t stream);
 
+/* moe_mxfp8_quant_dual_tokens of the routed rows x[token_idx[r]] (times
+ * row_scale[r], rounded to bf16, when row_scale != NULL) read from src [n_src,
+ * cols] in place: the expert permute (moe.py:445-451, x[token_idx] * score) and
+ * the quantization of its output in one pass, without writing the routed rows.
+ * Rows whose index is outside [0, n_src) read as zeros. src must be 16-byte
+ * aligned (rows are read in 16-byte pieces). */
+int moe_mxfp8_quant_dual_tokens_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                                       const float* row_scale, const int64_t* counts, int64_t n_rows,
+                                       int32_t n_experts, int32_t cols, int64_t padded_rows, uint8_t* q_rows,
+                                       uint8_t* scale_rows, uint8_t* q, uint8_t* scale, moe_stream_t stream);
+
 /* MXFP8 g, u, h as moe_fp8_gemm_gate_up; sx [R, D/32], sw1 and sw3 [E, H, D/32]. */
 int moe_mxfp8_gemm_gate_up(const uint8_t* qx, const uint8_t* sx, const uint8_t* qw1, const uint8_t* sw1,
                            const uint8_t* qw3, const uint8_t* sw3, const int64_t* counts, int64_t n_rows,

@@ -86,7 +86,7 @@ def _opcheck_cases(dev):
 
     idx = _distinct_topk(n, e, k, dev, gen)
     top = torch.rand(n, k, generator=gen).to(dev)
-    _, _, counts, offs, slot_pos, tok_pos = ops.reorder(top, idx, e)
+    scores_sorted, token_idx, counts, offs, slot_pos, tok_pos = ops.reorder(top, idx, e)
     logits = f32(n, e, grad=True)
     _, r_idx, _, r_scores = ops.router(logits.detach(), None, e, k, 1, 0, 0, True, 2.5, False)
     cases = {
@@ -122,6 +122,19 @@ def _opcheck_cases(dev):
     outs = ops.grouped_swiglu_mxfp8(x, w1, w2, w3, counts, True)
     cases["grouped_swiglu_mxfp8_backward"] = (ops.grouped_swiglu_mxfp8_backward,
                                               (bf(r, d), x, w1, w2, w3, counts, *outs[1:]))
+    # permute -> MXFP8 experts -> combine as one op (score before the experts)
+    def core_args(shared):
+        return (bf(n, d, grad=True), bf(n, d, grad=True) if shared else None, token_idx,
+                scores_sorted.clone().requires_grad_(True), slot_pos, tok_pos, bf(e, h, d, grad=True, scale=0.05),
+                bf(e, d, h, grad=True, scale=0.05), bf(e, h, d, grad=True, scale=0.05), counts)
+
+    cases["moe_core_mxfp8"] = (ops.moe_core_mxfp8, core_args(True))
+    cases["moe_core_mxfp8_no_shared"] = (ops.moe_core_mxfp8, core_args(False))
+    xn = bf(n, d)
+    core = ops.moe_core_mxfp8(xn, None, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, counts)
+    cases["moe_core_mxfp8_backward"] = (ops.moe_core_mxfp8_backward,
+                                        (bf(n, d), xn, token_idx, scores_sorted, tok_pos, w1, w2, w3, counts,
+                                         *core[1:]))
     def f(*shape, grad=False, scale=1.0):
         return (torch.randn(*shape, generator=gen) * scale).to(dev).requires_grad_(grad)
 
@@ -160,7 +173,8 @@ OPCHECK_NAMES = ["router", "router_backward", "reorder", "reorder_backward", "pe
                  "combine", "combine_no_shared", "combine_backward", "grouped_swiglu", "grouped_swiglu_backward",
                  "grouped_swiglu_f32", "grouped_swiglu_f32_backward",
                  "grouped_swiglu_fp8", "grouped_swiglu_fp8_backward", "grouped_swiglu_mxfp8",
-                 "grouped_swiglu_mxfp8_backward", "grouped_swiglu_oss", "grouped_swiglu_oss_backward",
+                 "grouped_swiglu_mxfp8_backward", "moe_core_mxfp8", "moe_core_mxfp8_no_shared",
+                 "moe_core_mxfp8_backward", "grouped_swiglu_oss", "grouped_swiglu_oss_backward",
                  "gather_rows", "scatter_rows", "swiglu_ffn_backward", "swiglu_ffn_backward_dw_only",
                  "swiglu_forward", "swiglu_backward", "gate_grad_split3", "gate_dw_reduce"]
 

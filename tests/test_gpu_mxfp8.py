@@ -363,3 +363,71 @@ def test_mxfp8_quantizers_nan_elements(dev):
     assert torch.equal(sr[blk], rs[blk])
     el = blk.repeat_interleave(32, dim=1)
     assert torch.equal(qr[el], rq[el])
+
+
+@pytest.mark.parametrize("cols", [256, 192])
+@pytest.mark.parametrize("scaled", [True, False])
+def test_mxfp8_gathering_token_quantizer_matches_permute_then_quantize(dev, cols, scaled):
+    """moe_mxfp8_quant_dual_tokens_gather reads the routed rows x[token_idx]
+    (* score, rounded to bf16) in place: all four layouts byte-identical to the
+    permute op's output fed to moe_mxfp8_quant_dual_tokens (ragged groups, an
+    empty expert, 64-column slabs when the width is no multiple of 128)."""
+    banner(f"mxfp8 gathering token quantizer cols={cols} scaled={scaled}")
+    from torchtitan_amd import ops
+
+    g = torch.Generator().manual_seed(11)
+    n, e, k = 300, 8, 2
+    x = (torch.randn(n, cols, generator=g) * 3).bfloat16().to(dev)
+    logits = torch.randn(n, e, generator=g)
+    logits[:, 3] = -1e9  # expert 3 receives no token
+    top, idx = logits.topk(k, dim=1)
+    top = top.sigmoid().to(dev)
+    scores_sorted, token_idx, counts, _offs, slot_pos, tok_pos = ops.reorder(top, idx.to(dev), e)
+    assert counts[3].item() == 0
+    r = n * k
+    rpad = ops._mx_padded_rows(r, e)
+    routed = ops.permute(x, slot_pos, tok_pos, scores_sorted if scaled else None)
+    want = ops._mx_dual_tokens(routed, counts, e, rpad)
+    got = ops._mx_dual_tokens_gather(x, token_idx, scores_sorted if scaled else None, counts, e, rpad)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("q_rows", "s_rows", "q_t", "s_t"), got, want):
+        assert torch.equal(a, b), name
+
+
+LAYER_CASES = {
+    "shared_sigmoid": dict(bs=2, slen=512, dim=512, experts=16, top_k=4, hidden=256, shared_hidden=256),
+    "no_shared_softmax": dict(bs=1, slen=768, dim=768, experts=8, top_k=2, hidden=512, shared_hidden=0,
+                              score_func="softmax", route_norm=False, route_scale=1.0),
+}
+
+
+@pytest.mark.parametrize("name", list(LAYER_CASES))
+def test_mxfp8_layer_fused_permute_matches_separate_ops(dev, name):
+    """MoE with MXFP8 experts and the score before them: the fused op
+    (moe_core_mxfp8: permute inside the token quantizer, the combine's gather
+    inside the backward's) gives the output, the input gradient and every
+    parameter gradient bit-identical to permute -> experts -> combine."""
+    banner(f"mxfp8 layer fused permute {name}")
+    from tests.layer_util import LayerShape, build_layer
+
+    sh = LayerShape(**LAYER_CASES[name], mxfp8=True)
+    moe, x, gy = build_layer(sh, dev, seed=5)
+
+    def run(fuse):
+        moe.fuse_mxfp8_permute = fuse
+        moe.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        assert moe._fused_mxfp8_applies(xx.view(-1, sh.dim)) == fuse
+        out = moe(xx)
+        out.backward(gy)
+        torch.cuda.synchronize()
+        return out.detach(), xx.grad, {n: p.grad.clone() for n, p in moe.named_parameters()}
+
+    out_s, gx_s, gp_s = run(False)
+    out_f, gx_f, gp_f = run(True)
+    assert torch.equal(out_f, out_s)
+    assert torch.equal(gx_f, gx_s)
+    assert gp_f.keys() == gp_s.keys()
+    for n in gp_s:
+        assert torch.equal(gp_f[n], gp_s[n]), n
+    print(f"[case] {name}: out, grad_x and {len(gp_s)} parameter gradients identical", flush=True)

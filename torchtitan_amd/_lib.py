@@ -76,6 +76,7 @@ SIGNATURES: dict[str, list] = {
     "moe_mxfp8_quant_tokens_t": [P, P, I64, I32, I32, I64, P, P, P],
     "moe_mxfp8_quant_dual_cols": [P, I32, I32, I32, P, P, P, I64, I64, P, I64, I64, P],
     "moe_mxfp8_quant_dual_tokens": [P, P, I64, I32, I32, I64, P, P, P, P, P],
+    "moe_mxfp8_quant_dual_tokens_gather": [P, I64, P, P, P, I64, I32, I32, I64, P, P, P, P, P],
     "moe_mxfp8_gemm_gate_up": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "moe_mxfp8_gemm_down": [P, P, P, P, P, I64, I32, I32, I32, P, P],
     "moe_mxfp8_gemm_bwd_dgu": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P],

@@ -329,26 +329,70 @@ constexpr int kTRows = 128;  // slab rows transposed per pass
 // loads two passes ahead are issued as soon as the tile is in LDS. 128-column
 // slabs (launched whenever the width allows) write the row-wise layout in whole
 // 128-byte lines: 2-12 % faster than 64-column ones at the Kimi shapes.
-template <bool MX, bool ROWS, int COLS>
+// Rows gathered from another tensor (GATHER): slab row r is source row idx[r] of
+// src (row stride ld), times scale[r] rounded to bf16 when scale is given (the
+// expert permute x[token_idx] * score, read in place of its output). Source rows
+// outside [0, n_src) read as zeros. The indices are loaded two passes ahead of
+// the rows they address and the scale is applied when a pass is consumed, so
+// neither waits behind the row loads in flight (vector loads complete in order).
+struct RowGather {
+  const uint16_t* src = nullptr;
+  const int64_t* idx = nullptr;
+  const float* scale = nullptr;
+  int64_t ld = 0, n_src = 0;
+};
+
+template <bool MX, bool ROWS, int COLS, bool GATHER = false>
 __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows, int n_out,
                                              uint8_t* __restrict__ out, int64_t ldo, uint8_t* __restrict__ sc,
                                              int64_t sc_b, int64_t sc_k, const float* s_col, uint32_t* s_tile,
                                              uint8_t* __restrict__ qr = nullptr, int64_t ldr = 0,
-                                             uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0) {
+                                             uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0,
+                                             RowGather gather = RowGather{}) {
   constexpr int T = 4 * COLS, CPR = COLS / 8;
   const int t = threadIdx.x;
   uint4 va[4], vb[4];
-  auto load = [&](uint4 (&v)[4], int a0) {
+  int64_t ia[4], ib[4];  // GATHER: source rows of the pass two ahead of va / vb
+  float sa[4], sb[4];    // GATHER with scale: the row scales of the pass in va / vb
+  auto load_idx = [&](int64_t (&ix)[4], int a0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (t + i * T) / CPR;
+      ix[i] = a0 + r < n_rows ? gather.idx[a0 + r] : -1;
+    }
+  };
+  auto load = [&](uint4 (&v)[4], const int64_t (&ix)[4], float (&sv)[4], int a0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * T;
       const int r = c / CPR, ch = c % CPR;
-      v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+      if constexpr (GATHER) {
+        v[i] = (ix[i] >= 0 && ix[i] < gather.n_src) ? *(const uint4*)(gather.src + ix[i] * gather.ld + ch * 8)
+                                                     : make_uint4(0, 0, 0, 0);
+        if (gather.scale) sv[i] = a0 + r < n_rows ? gather.scale[a0 + r] : 0.f;
+      } else {
+        v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto apply_scales = [&](uint4 (&v)[4], const float (&sv)[4], int a0) {
+    if constexpr (GATHER) {
+      if (!gather.scale) return;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (a0 + (t + i * T) / CPR >= n_rows) continue;
+        float f[8];
+        Chunk<uint16_t>::unpack(v[i], f);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] = f[k] * sv[i];
+        v[i] = Chunk<uint16_t>::pack(f);
+      }
     }
   };
   // one pass of 128 rows held in v; v is reloaded with the pass two ahead as soon
   // as it is in LDS, so two passes' loads are in flight while one is transposed
-  auto pass = [&](uint4 (&v)[4], int a0) {
+  auto pass = [&](uint4 (&v)[4], int64_t (&ix)[4], float (&sv)[4], int a0) {
+    apply_scales(v, sv, a0);
     const uint32_t nan = has_nan8(v[0]) | has_nan8(v[1]) | has_nan8(v[2]) | has_nan8(v[3]);
     if constexpr (ROWS) {
       const bool rows_fast = wave_nan_free(nan);
@@ -375,7 +419,11 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       *(uint4*)(s_tile + r * (COLS / 2) + (((c % CPR) ^ ((r >> 4) & 7)) * 4)) = v[i];
     }
     const bool fast = !__syncthreads_or(nan != 0u);  // block-uniform: the tile holds no NaN
-    if (a0 + 2 * kTRows < n_out) load(v, a0 + 2 * kTRows);
+    if (a0 + 2 * kTRows < n_out) {
+      load(v, ix, sv, a0 + 2 * kTRows);
+      if constexpr (GATHER)
+        if (a0 + 4 * kTRows < n_out) load_idx(ix, a0 + 4 * kTRows);
+    }
     // unit (column cc, rows 16 kq .. 16 kq + 15 of the pass): 8 consecutive lanes cover one
     // output row's 128 bytes, so every store instruction writes 8 rows x 128 contiguous bytes
 #pragma unroll
@@ -420,11 +468,23 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       }
     }
   };
-  if (n_out > 0) load(va, 0);
-  if (n_out > kTRows) load(vb, kTRows);
+  if constexpr (GATHER) {
+    if (n_out > 0) load_idx(ia, 0);
+    if (n_out > kTRows) load_idx(ib, kTRows);
+  }
+  if (n_out > 0) {
+    load(va, ia, sa, 0);
+    if constexpr (GATHER)
+      if (n_out > 2 * kTRows) load_idx(ia, 2 * kTRows);
+  }
+  if (n_out > kTRows) {
+    load(vb, ib, sb, kTRows);
+    if constexpr (GATHER)
+      if (n_out > 3 * kTRows) load_idx(ib, 3 * kTRows);
+  }
   for (int a0 = 0; a0 < n_out; a0 += 2 * kTRows) {
-    pass(va, a0);
-    if (a0 + kTRows < n_out) pass(vb, a0 + kTRows);
+    pass(va, ia, sa, a0);
+    if (a0 + kTRows < n_out) pass(vb, ib, sb, a0 + kTRows);
   }
 }
 
@@ -581,12 +641,12 @@ __global__ __launch_bounds__(4 * COLS) void mx_dual_cols_kernel(const uint16_t* 
 // k-block major, s [Rpad / 32][C]. Block per (e, COLS columns); empty groups exit.
 // With ROWS, the same read also writes the row-wise layout of the group's rows
 // (qr [R][C], sr [R][C / 32]).
-template <bool ROWS, int COLS>
+template <bool ROWS, int COLS, bool GATHER = false>
 __global__ __launch_bounds__(4 * COLS) void mx_quant_tokens_t_kernel(const uint16_t* __restrict__ x,
                                                                 const int64_t* __restrict__ counts, int64_t R, int E,
                                                                 int C, int64_t Rpad, uint8_t* __restrict__ q,
                                                                 uint8_t* __restrict__ s, uint8_t* __restrict__ qr,
-                                                                uint8_t* __restrict__ sr) {
+                                                                uint8_t* __restrict__ sr, RowGather gather) {
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
   __shared__ int s_tmp[8];
   __shared__ int s_seg[3];
@@ -627,10 +687,16 @@ __global__ __launch_bounds__(4 * COLS) void mx_quant_tokens_t_kernel(const uint1
       for (int64_t br = end / kMxBlock; br < Rpad / kMxBlock; ++br) s[br * C + c0 + threadIdx.x] = 0;
   }
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
-  slab_t_quant<true, ROWS, COLS>(x + (int64_t)seg0 * C + c0, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad,
-                           s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C, nullptr, s_tile,
-                                ROWS ? qr + (int64_t)seg0 * C + c0 : nullptr, C,
-                                ROWS ? sr + (int64_t)seg0 * (C / kMxBlock) + c0 / kMxBlock : nullptr, C / kMxBlock);
+  if constexpr (GATHER) {  // this slab's rows and columns of the gathered source
+    gather.src += c0;
+    gather.idx += seg0;
+    if (gather.scale) gather.scale += seg0;
+  }
+  slab_t_quant<true, ROWS, COLS, GATHER>(GATHER ? nullptr : x + (int64_t)seg0 * C + c0, C, n, n_out,
+                                 q + (int64_t)c0 * Rpad + pstart, Rpad, s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C,
+                                 nullptr, s_tile, ROWS ? qr + (int64_t)seg0 * C + c0 : nullptr, C,
+                                 ROWS ? sr + (int64_t)seg0 * (C / kMxBlock) + c0 / kMxBlock : nullptr, C / kMxBlock,
+                                 gather);
 }
 
 // ---------------------------------------------------------------------------
@@ -1488,10 +1554,12 @@ MOE_API int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, i
   if (!x || !counts || !q || !scale) return kErrInvalidArgument;
   if (cols % 128 == 0)
     hipLaunchKernelGGL((mx_quant_tokens_t_kernel<false, 128>), dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x,
-                       counts, n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr);
+                       counts, n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr,
+                       RowGather{});
   else
     hipLaunchKernelGGL((mx_quant_tokens_t_kernel<false, 64>), dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x,
-                       counts, n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr);
+                       counts, n_rows, n_experts, cols, padded_rows, q, scale, (uint8_t*)nullptr, (uint8_t*)nullptr,
+                       RowGather{});
   return launch_status();
 }
 
@@ -1514,19 +1582,46 @@ MOE_API int moe_mxfp8_quant_dual_cols(const uint16_t* x, int32_t n_experts, int3
   return launch_status();
 }
 
-MOE_API int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
-                                        int32_t cols, int64_t padded_rows, uint8_t* q_rows, uint8_t* scale_rows,
-                                        uint8_t* q, uint8_t* scale, hipStream_t stream) {
+static int mx_dual_tokens(const uint16_t* x, RowGather gather, const int64_t* counts, int64_t n_rows,
+                          int32_t n_experts, int32_t cols, int64_t padded_rows, uint8_t* q_rows, uint8_t* scale_rows,
+                          uint8_t* q, uint8_t* scale, hipStream_t stream) {
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
   if (padded_rows < moe_mxfp8_padded_rows(n_rows, n_experts) || padded_rows % kMxPad) return kErrWorkspace;
   if (!x || !counts || !q || !scale || !q_rows || !scale_rows) return kErrInvalidArgument;
+  const bool g = gather.idx != nullptr;
+  using kernel_t = void (*)(const uint16_t*, const int64_t*, int64_t, int, int, int64_t, uint8_t*, uint8_t*, uint8_t*,
+                            uint8_t*, RowGather);
+  const kernel_t k128 = g ? mx_quant_tokens_t_kernel<true, 128, true> : mx_quant_tokens_t_kernel<true, 128, false>;
+  const kernel_t k64 = g ? mx_quant_tokens_t_kernel<true, 64, true> : mx_quant_tokens_t_kernel<true, 64, false>;
   if (cols % 128 == 0)
-    hipLaunchKernelGGL((mx_quant_tokens_t_kernel<true, 128>), dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x,
-                       counts, n_rows, n_experts, cols, padded_rows, q, scale, q_rows, scale_rows);
+    hipLaunchKernelGGL(k128, dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x, counts, n_rows, n_experts, cols,
+                       padded_rows, q, scale, q_rows, scale_rows, gather);
   else
-    hipLaunchKernelGGL((mx_quant_tokens_t_kernel<true, 64>), dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x,
-                       counts, n_rows, n_experts, cols, padded_rows, q, scale, q_rows, scale_rows);
+    hipLaunchKernelGGL(k64, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts, n_rows, n_experts, cols,
+                       padded_rows, q, scale, q_rows, scale_rows, gather);
   return launch_status();
+}
+
+MOE_API int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                        int32_t cols, int64_t padded_rows, uint8_t* q_rows, uint8_t* scale_rows,
+                                        uint8_t* q, uint8_t* scale, hipStream_t stream) {
+  return mx_dual_tokens(x, RowGather{}, counts, n_rows, n_experts, cols, padded_rows, q_rows, scale_rows, q, scale,
+                        stream);
+}
+
+MOE_API int moe_mxfp8_quant_dual_tokens_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                                               const float* row_scale, const int64_t* counts, int64_t n_rows,
+                                               int32_t n_experts, int32_t cols, int64_t padded_rows,
+                                               uint8_t* q_rows, uint8_t* scale_rows, uint8_t* q, uint8_t* scale,
+                                               hipStream_t stream) {
+  if (n_src < 0 || !token_idx || reinterpret_cast<uintptr_t>(src) % 16) return kErrInvalidArgument;
+  RowGather g;
+  g.src = src;
+  g.idx = token_idx;
+  g.scale = row_scale;
+  g.ld = cols;
+  g.n_src = n_src;
+  return mx_dual_tokens(src, g, counts, n_rows, n_experts, cols, padded_rows, q_rows, scale_rows, q, scale, stream);
 }
 
 MOE_API int moe_mxfp8_gemm_gate_up(const uint8_t* qx, const uint8_t* sx, const uint8_t* qw1, const uint8_t* sw1,

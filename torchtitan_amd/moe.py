@@ -388,6 +388,18 @@ class MoE(Module):
         layout = self.reorderer(top_scores, selected_experts_indices)
         top_scores_experts_sorted, _token_indices_experts_sorted, num_tokens_per_expert = layout
 
+        if self._fused_mxfp8_applies(x):
+            # MXFP8 experts with the score applied before them: the permute runs inside
+            # the experts' token quantizer and the combine's gather inside their
+            # backward (ops.moe_core_mxfp8), with the same results as the three ops
+            shared = self.shared_experts(x) if self.shared_experts is not None else None
+            experts = self.experts
+            out = ops.moe_core_mxfp8(
+                x, shared, _token_indices_experts_sorted, top_scores_experts_sorted, layout.slot_pos,
+                layout.tok_pos, _local(experts.w1), _local(experts.w2), _local(experts.w3), num_tokens_per_expert,
+            )[0]
+            return out.reshape(bs, slen, dim)
+
         # routed_input = x[token_idx] (* score when score_before_experts)
         routed_input = ops.permute(
             x, layout.slot_pos, layout.tok_pos,
@@ -404,6 +416,16 @@ class MoE(Module):
             None if self.score_before_experts else top_scores_experts_sorted,
         )
         return out.reshape(bs, slen, dim)
+
+    # set False to run MXFP8 experts through the separate permute, experts and combine ops
+    fuse_mxfp8_permute = True
+
+    def _fused_mxfp8_applies(self, x: torch.Tensor) -> bool:
+        experts = self.experts
+        if not (self.fuse_mxfp8_permute and type(experts) is GroupedExperts and experts.mxfp8
+                and self.score_before_experts and x.is_cuda and x.dtype == torch.bfloat16):
+            return False
+        return all(_local(w).dtype == torch.bfloat16 for w in (experts.w1, experts.w2, experts.w3))
 
     def _init_self_buffers(self, *, buffer_device: torch.device | None = None) -> None:
         assert isinstance(buffer_device, torch.device)

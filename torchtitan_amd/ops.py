@@ -1020,13 +1020,23 @@ def grouped_swiglu_mxfp8_backward(
         qht, sht = _mx_quant_tokens_t(h, counts, e, rpad)
         *_, qw2t, sw2t, qw13t, sw13t = _mx_weights(w1.contiguous(), w2.contiguous(), w3.contiguous(), True)
     # dh = dy . w2 (contraction over D)
-    qdy, sdy, qdyt, sdyt = _mx_dual_tokens(dy, counts, e, rpad)
-    dgu = x.new_empty(r, 2 * h_dim)
+    qdy = _mx_dual_tokens(dy, counts, e, rpad)
+    return _mx_experts_backward(qdy, r, d, w1, w2, w3, counts, g, u, h, qxt, sxt, qht, sht, qw2t, sw2t, qw13t,
+                                sw13t, rpad)
+
+
+def _mx_experts_backward(qdy, r, d, w1, w2, w3, counts, g, u, h, qxt, sxt, qht, sht, qw2t, sw2t, qw13t, sw13t, rpad):
+    """dx (routed rows), dw1, dw2, dw3 of the MXFP8 experts from dy's two MX
+    layouts (qdy = (q rows, e8m0 rows, q tokens^T, e8m0 tokens^T))."""
+    qdy, sdy, qdyt, sdyt = qdy
+    e, h_dim, _ = w1.shape
+    s = stream_of(g)
+    dgu = g.new_empty(r, 2 * h_dim)
     call("moe_mxfp8_gemm_bwd_dgu", ptr(qdy), ptr(sdy), ptr(qw2t), ptr(sw2t), ptr(g), ptr(u), ptr(counts), r, e, d,
          h_dim, ptr(dgu), s)
     # dx = dg . w1 + du . w3 (contraction over H; blocks never straddle the halves)
     qdgu, sdgu, qdgut, sdgut = _mx_dual_tokens(dgu, counts, e, rpad)
-    dx = x.new_empty(r, d)
+    dx = g.new_empty(r, d)
     call("moe_mxfp8_gemm_bwd_dx", ptr(qdgu), ptr(sdgu), ptr(qw13t), ptr(sw13t), ptr(counts), r, e, d, h_dim,
          ptr(dx), s)
     # weight gradients: contraction over each expert's tokens (groups padded to 32)
@@ -1062,6 +1072,129 @@ def _gsmx_bwd(ctx, dy, *_unused):
 
 
 grouped_swiglu_mxfp8.register_autograd(_gsmx_bwd, setup_context=_gsmx_setup)
+
+
+# ---------------------------------------------------------------------------
+# the routed half of MoE.forward with MXFP8 experts and the score applied before
+# them, the permute folded into the token quantizer
+# ---------------------------------------------------------------------------
+def _mx_dual_tokens_gather(src: Tensor, token_idx: Tensor, row_scale: Tensor | None, counts: Tensor, e: int,
+                           rpad: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """_mx_dual_tokens of the routed rows src[token_idx] (* row_scale, rounded to
+    bf16), read from src [N, C] in place."""
+    if src.data_ptr() % 16:  # the kernel reads rows in 16-byte pieces
+        src = src.clone()
+    r = token_idx.shape[0]
+    c = src.shape[1]
+    qr = torch.empty(r, c, dtype=FP8, device=src.device)
+    sr = torch.empty(r, c // MX_BLOCK, dtype=torch.uint8, device=src.device)
+    qt = torch.empty(c, rpad, dtype=FP8, device=src.device)
+    st = torch.empty(rpad // MX_BLOCK, c, dtype=torch.uint8, device=src.device)
+    call("moe_mxfp8_quant_dual_tokens_gather", ptr(src), src.shape[0], ptr(token_idx), ptr(row_scale), ptr(counts),
+         r, e, c, rpad, ptr(qr), ptr(sr), ptr(qt), ptr(st), stream_of(src))
+    return qr, sr, qt, st
+
+
+@torch.library.custom_op("moe_mi355x::moe_core_mxfp8", mutates_args=())
+def moe_core_mxfp8(
+    x: Tensor, shared_out: Tensor | None, token_idx: Tensor, scores_sorted: Tensor, slot_pos: Tensor,
+    tok_pos: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """out = combine(shared_out, experts(x[token_idx] * score)) with MXFP8 experts
+    (moe.py:440-470 with score_before_experts; the ops of permute,
+    grouped_swiglu_mxfp8 and combine): the routed rows are quantized straight from
+    x (moe_mxfp8_quant_dual_tokens_gather), so no routed copy of x is written, and
+    in the backward the routed gradient is quantized straight from the output's
+    gradient. Returns (out, g, u, h, then the forward's quantized layouts the
+    backward reuses)."""
+    require_gpu(x, shared_out, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, num_tokens_per_expert)
+    _check_bf16("moe_core_mxfp8", x=x, w1=w1, w2=w2, w3=w3)
+    x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    tidx = token_idx.to(torch.int64).contiguous()
+    sc = scores_sorted.float().contiguous()
+    r = tidx.shape[0]
+    d = x.shape[1]
+    e, h_dim, _ = w1.shape
+    s = stream_of(x)
+    rpad = _mx_padded_rows(r, e)
+    qx, sx, qxt, sxt = _mx_dual_tokens_gather(x, tidx, sc, counts, e, rpad)
+    qw1, sw1, qw3, sw3, qw2, sw2, qw2t, sw2t, qw13t, sw13t = _mx_weights(w1, w2, w3, True)
+    g = x.new_empty(r, h_dim)
+    u = x.new_empty(r, h_dim)
+    h = x.new_empty(r, h_dim)
+    call("moe_mxfp8_gemm_gate_up", ptr(qx), ptr(sx), ptr(qw1), ptr(sw1), ptr(qw3), ptr(sw3), ptr(counts), r, e, d,
+         h_dim, ptr(g), ptr(u), ptr(h), s)
+    qh, sh, qht, sht = _mx_dual_tokens(h, counts, e, rpad)
+    y = x.new_empty(r, d)
+    call("moe_mxfp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
+    out = combine(shared_out, y, slot_pos, tok_pos, None)
+    return out, g, u, h, qxt, sxt, qht, sht, qw2t, sw2t, qw13t, sw13t
+
+
+@moe_core_mxfp8.register_fake
+def _(x, shared_out, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, num_tokens_per_expert):
+    n, d = x.shape
+    r = token_idx.shape[0]
+    e, h_dim, _ = w1.shape
+    u8 = lambda *shape: x.new_empty(*shape, dtype=torch.uint8)  # noqa: E731
+    rpad = (r + e * 31 + 31) // 32 * 32
+    return (x.new_empty(n, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim),
+            u8(d, rpad), u8(rpad // 32, d), u8(h_dim, rpad), u8(rpad // 32, h_dim),
+            u8(e, h_dim, d), u8(e, h_dim, d // 32), u8(e, d, 2 * h_dim), u8(e, d, 2 * h_dim // 32))
+
+
+@torch.library.custom_op("moe_mi355x::moe_core_mxfp8_backward", mutates_args=())
+def moe_core_mxfp8_backward(
+    grad_out: Tensor, x: Tensor, token_idx: Tensor, scores_sorted: Tensor, tok_pos: Tensor, w1: Tensor,
+    w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor, g: Tensor, u: Tensor, h: Tensor, qxt: Tensor,
+    sxt: Tensor, qht: Tensor, sht: Tensor, qw2t: Tensor, sw2t: Tensor, qw13t: Tensor, sw13t: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(grad_x, grad_scores_sorted, dw1, dw2, dw3) of moe_core_mxfp8's out; the
+    shared output's gradient is grad_out itself (the combine adds it once)."""
+    require_gpu(grad_out, x, token_idx, scores_sorted, tok_pos, w1, w2, w3, num_tokens_per_expert, g, u, h)
+    go = grad_out.to(torch.bfloat16).contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    tidx = token_idx.to(torch.int64).contiguous()
+    r = tidx.shape[0]
+    d = x.shape[1]
+    e = w1.shape[0]
+    rpad = _mx_padded_rows(r, e)
+    qdy = _mx_dual_tokens_gather(go, tidx, None, counts, e, rpad)
+    dx_routed, dw1, dw2, dw3 = _mx_experts_backward(qdy, r, d, w1, w2, w3, counts, g, u, h, qxt, sxt, qht, sht,
+                                                    qw2t, sw2t, qw13t, sw13t, rpad)
+    grad_x, grad_s = permute_backward(dx_routed, x, tok_pos, scores_sorted, PERMUTE_BWD_ROUND_EACH)
+    return grad_x, grad_s, dw1, dw2, dw3
+
+
+@moe_core_mxfp8_backward.register_fake
+def _(grad_out, x, token_idx, scores_sorted, tok_pos, w1, w2, w3, num_tokens_per_expert, *saved):
+    r = token_idx.shape[0]
+    return (x.new_empty(x.shape), x.new_empty(r, dtype=torch.float32), torch.empty_like(w1), torch.empty_like(w2),
+            torch.empty_like(w3))
+
+
+def _core_mx_setup(ctx, inputs, output):
+    x, shared_out, token_idx, scores_sorted, _slot_pos, tok_pos, w1, w2, w3, counts = inputs
+    _out, g, u, h, *quantized = output
+    ctx.save_for_backward(x, token_idx, scores_sorted, tok_pos, w1, w2, w3, counts, g, u, h, *quantized)
+    ctx.has_shared = shared_out is not None
+    ctx.shared_dtype = shared_out.dtype if shared_out is not None else None
+    ctx.mark_non_differentiable(g, u, h, *quantized)
+    ctx.set_materialize_grads(False)
+
+
+def _core_mx_bwd(ctx, grad_out, *_unused):
+    if grad_out is None:
+        return (None,) * 10
+    x, token_idx, scores_sorted, tok_pos, w1, w2, w3, counts, g, u, h, *quantized = ctx.saved_tensors
+    grad_x, grad_s, dw1, dw2, dw3 = moe_core_mxfp8_backward(grad_out, x, token_idx, scores_sorted, tok_pos, w1, w2,
+                                                            w3, counts, g, u, h, *quantized)
+    grad_shared = grad_out.to(ctx.shared_dtype) if ctx.has_shared else None
+    return grad_x, grad_shared, None, grad_s, None, None, dw1, dw2, dw3, None
+
+
+moe_core_mxfp8.register_autograd(_core_mx_bwd, setup_context=_core_mx_setup)
 
 
 # ---------------------------------------------------------------------------
