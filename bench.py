@@ -176,6 +176,12 @@ def launch_bytes(name: str, a: tuple) -> float | None:
     if name == "moe_fp8_quant_tokens_t":
         rows, e, cols, padded = a[2], a[3], a[4], a[5]
         return 2.0 * rows * cols + 1.0 * padded * cols + 4.0 * e * cols + 8.0 * e
+    if name == "moe_fp8_quant_rows_groupamax":  # + the [E, cols] group amax written
+        rows, e, cols, pieces = a[2], a[3], a[4], a[5]
+        return 3.0 * rows * cols + 4.0 * rows * pieces + 4.0 * e * cols + 8.0 * e
+    if name == "moe_fp8_quant_tokens_t_amax":  # the group amax read instead of found
+        rows, e, cols, padded = a[3], a[4], a[5], a[6]
+        return 2.0 * rows * cols + 1.0 * padded * cols + 8.0 * e * cols + 8.0 * e
     if name == "moe_mxfp8_quant_rows":
         rows, cols = a[1], a[2]
         return 2.0 * rows * cols + mx * rows * cols

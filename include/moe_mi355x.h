@@ -339,7 +339,7 @@ int moe_fp8_quant_cols_t_amax(const uint16_t* x, const float* col_amax, int32_t 
  * quantization/float8.py:260-288) from two reads instead of three: x [E, a, b]
  * bf16 -> q [E, a, b] fp8 with one scale per row (as moe_fp8_quant_rows over b),
  * and col_amax [E, b] = the amax over a of each column (NaN ignored), max-
- * accumulated: the caller zeroes it. b % 8 == 0, b <= 4096. */
+ * accumulated: the caller zeroes it. b % 8 == 0, b <= 8192. */
 int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
                                float* scale, float* col_amax, moe_stream_t stream);
 
@@ -350,6 +350,25 @@ int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int32_t a, 
 int moe_fp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
                            int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
                            moe_stream_t stream);
+
+/* moe_fp8_quant_tokens_t with each group's column amax [E, cols] already known
+ * (from moe_fp8_quant_rows_groupamax of the same x): x is read once. */
+int moe_fp8_quant_tokens_t_amax(const uint16_t* x, const float* group_amax, const int64_t* counts,
+                                int64_t n_rows, int32_t n_experts, int32_t cols, int64_t padded_rows,
+                                uint8_t* q, float* scale, moe_stream_t stream);
+
+/* The token operands' two rowwise quantizations (torchao's float8 grouped GEMM
+ * quantizes the routed tokens, their gradient and the SwiGLU intermediates along
+ * each GEMM's contraction, quantization/float8.py:260-288) from two reads instead
+ * of three: x [n_rows, cols] bf16 in expert token groups (counts) -> q [n_rows,
+ * cols] fp8 with one scale per row piece (as moe_fp8_quant_rows over cols /
+ * pieces columns: scale[r * pieces + p], pieces 1 or 2), and group_amax [E, cols]
+ * = the amax of each column over each group's rows (NaN ignored), max-
+ * accumulated: the caller zeroes it. Rows past the last group are quantized
+ * but enter no amax. cols % (8 * pieces) == 0, cols <= 8192. */
+int moe_fp8_quant_rows_groupamax(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                 int32_t cols, int32_t pieces, uint8_t* q, float* scale, float* group_amax,
+                                 moe_stream_t stream);
 
 /* fp8 forward of _run_experts_grouped_mm (moe.py:62-67): g = (qx.qw1^T)*sx*sw1,
  * u likewise with w3, h = bf16(bf16(silu(g)) * u). sw1, sw3 [E, H]. */

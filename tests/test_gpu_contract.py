@@ -112,9 +112,9 @@ def _opcheck_cases(dev):
     cases["grouped_swiglu_fp8"] = (ops.grouped_swiglu_fp8, (bf(r, d, grad=True), bf(e, h, d, grad=True, scale=0.05),
                                                             bf(e, d, h, grad=True, scale=0.05),
                                                             bf(e, h, d, grad=True, scale=0.05), counts))
-    _, g8, u8, h8, am1, am3, am2 = ops.grouped_swiglu_fp8(x, w1, w2, w3, counts)
+    _, g8, u8, h8, *am8 = ops.grouped_swiglu_fp8(x, w1, w2, w3, counts)
     cases["grouped_swiglu_fp8_backward"] = (ops.grouped_swiglu_fp8_backward,
-                                            (bf(r, d), x, w1, w2, w3, counts, g8, u8, h8, am1, am3, am2))
+                                            (bf(r, d), x, w1, w2, w3, counts, g8, u8, h8, *am8))
     cases["grouped_swiglu_mxfp8"] = (ops.grouped_swiglu_mxfp8,
                                      (bf(r, d, grad=True), bf(e, h, d, grad=True, scale=0.05),
                                       bf(e, d, h, grad=True, scale=0.05), bf(e, h, d, grad=True, scale=0.05),

@@ -244,6 +244,82 @@ def test_fp8_weight_quantizers_from_two_reads(dev, shape):
         assert torch.equal(qt, qt2) and torch.equal(st, st2)
 
 
+TOKEN_CASES = {
+    # (rows, cols, pieces, counts): rows past the last group, an empty group, a
+    # piece boundary inside a lane's chunk run (640 columns), 64-column slabs
+    # (192), the widest rows (8192)
+    "d2304_tail": (700, 2304, 1, [100, 0, 333, 7, 200]),
+    "dgu_2x640": (513, 1280, 2, [256, 1, 256]),
+    "d192": (300, 192, 1, [17, 0, 0, 283]),
+    "d8192": (300, 8192, 1, [50, 150, 0, 100]),
+}
+
+
+@pytest.mark.parametrize("name", list(TOKEN_CASES))
+def test_fp8_token_quantizers_from_two_reads(dev, name):
+    """moe_fp8_quant_rows_groupamax: the row-quantized bytes and the scale of each
+    row piece equal the oracle's (as moe_fp8_quant_rows over cols / pieces), and
+    the amax of each (group, column) equals max |x| over the group's rows (rows
+    past the last group enter none); moe_fp8_quant_tokens_t_amax from that amax
+    equals the oracle's per-group transposed quantization. With an inf and NaNs
+    planted, both still equal the kernels that find their own amax (NaN ignored
+    by the amax, as fmaxf does)."""
+    from torchtitan_amd import ops
+
+    r, c, pieces, counts = TOKEN_CASES[name]
+    banner(f"fp8 token quantizers {name}")
+    g = torch.Generator().manual_seed(r + c)
+    x = (torch.randn(r, c, generator=g) * torch.exp(torch.randn(r, 1, generator=g) * 2)).bfloat16()
+    x[3] = 0  # an all-zero row
+    e = len(counts)
+    cnt = torch.tensor(counts, dtype=torch.int64)
+    cd = cnt.to(dev)
+    rpad = ops._padded_rows(r, e)
+
+    def absmax(t):
+        t = t.float().abs()
+        return torch.where(torch.isnan(t), torch.zeros_like(t), t).amax(dim=0)
+
+    def check_amax(amax):
+        start = 0
+        for i, n in enumerate(counts):
+            want = absmax(x[start:start + n]) if n else torch.zeros(c)
+            assert torch.equal(amax[i].cpu(), want), f"group {i}"
+            start += n
+
+    xd = x.to(dev)
+    q, sc, amax = ops._quant_rows_groupamax(xd, cd, e, pieces)
+    rq, rs = R.quant_fp8_rows(x.view(r * pieces, c // pieces))
+    assert torch.equal(q.cpu().view(r * pieces, c // pieces), rq.view(torch.uint8))
+    assert torch.equal(sc.cpu(), rs.view(-1))
+    check_amax(amax)
+    qt, st = ops._quant_tokens_t(xd, cd, e, rpad, amax)
+    qt, st = qt.cpu(), st.cpu()
+    start = pstart = 0
+    for i, n in enumerate(counts):
+        if n:
+            rq, rs = R.quant_fp8_rows(x[start:start + n].t())
+            assert torch.equal(qt[:, pstart:pstart + n], rq.view(torch.uint8)), f"group {i}"
+            assert torch.count_nonzero(qt[:, pstart + n:pstart + (n + 15) // 16 * 16]) == 0
+            assert torch.equal(st[i], rs.view(-1))
+        start += n
+        pstart += (n + 15) // 16 * 16
+    # non-finite values: against the kernels that take their own amax
+    x[5, 7] = float("inf")
+    x[1, 2] = float("nan")
+    x[:, 9] = float("nan")  # a column of NaN: amax 0
+    xd = x.to(dev)
+    q, sc, amax = ops._quant_rows_groupamax(xd, cd, e, pieces)
+    q1, s1 = ops._quant_rows(xd, c // pieces)
+    assert torch.equal(q.view(-1), q1.view(-1)) and torch.equal(sc, s1)
+    check_amax(amax)
+    qt, st = ops._quant_tokens_t(xd, cd, e, rpad, amax)
+    qt1, st1 = ops._quant_tokens_t(xd, cd, e, rpad)
+    assert torch.equal(qt[:, :pstart], qt1[:, :pstart])
+    full = cnt > 0  # empty groups write no scale
+    assert torch.equal(st[full.to(dev)], st1[full.to(dev)])
+
+
 @pytest.mark.parametrize("width", [192, 320, 384])
 def test_fp8_transposing_quantizers_slab_widths(dev, width):
     """The transposing quantizers at widths that take 64-column slabs (192, 320)

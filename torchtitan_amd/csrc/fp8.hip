@@ -272,6 +272,115 @@ __global__ __launch_bounds__(256) void quant_rows_colamax_kernel(const uint16_t*
   for (int i = threadIdx.x; i < cpr * 8; i += blockDim.x) atomicMax(&col_amax[e * B + i], s_cm[i]);
 }
 
+// x [R][C] with expert token groups (counts, consecutive in row order) quantized
+// as quant_rows_kernel does with rows of K = C / P columns (piece p of row r
+// scaled by scale[r P + p]), with the column amax of every (group, column) on the
+// side, group_amax [E][C] (fp32 bits, atomic max; the caller zeroes it), for the
+// token-transposed quantization of the same tensor (quant_tokens_t_kernel with
+// amax_in), which then reads it once instead of twice. Block b takes rows
+// [b RB, b RB + RB); for each group overlapping them, one wave per row keeps
+// per-lane running column maxima (|x|, NaN ignored as fmaxf does), merged in LDS
+// and sent with one atomic max per column when the block leaves the group. Rows
+// past the last group are quantized row-wise only.
+template <int CPL, int P>
+__global__ __launch_bounds__(256) void quant_rows_groupamax_kernel(const uint16_t* __restrict__ x,
+                                                                   const int64_t* __restrict__ counts, int64_t R,
+                                                                   int E, int C, int RB, uint8_t* __restrict__ q,
+                                                                   float* __restrict__ scale,
+                                                                   uint32_t* __restrict__ group_amax) {
+  __shared__ uint32_t s_cm[64 * CPL * 8];
+  __shared__ int64_t s_end[kMaxE + 1];  // s_end[e]: end row of group e; s_end[E] = R
+  __shared__ int s_tmp[8];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int cpr = C / 8, kc = cpr / P;  // 16-byte chunks per row and per piece
+  {
+    int cnt[4], st[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ee = threadIdx.x * 4 + i;
+      const int64_t c = ee < E ? counts[ee] : 0;
+      cnt[i] = c < 0 ? 0 : (int)(c > R ? R : c);
+    }
+    block_exclusive_scan4(cnt, st, s_tmp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ee = threadIdx.x * 4 + i;
+      if (ee < E) s_end[ee] = min((int64_t)st[i] + cnt[i], R);
+    }
+    if (threadIdx.x == 0) s_end[E] = R;
+  }
+  for (int i = threadIdx.x; i < cpr * 8; i += blockDim.x) s_cm[i] = 0u;
+  __syncthreads();
+  const int64_t lo = (int64_t)blockIdx.x * RB, hi = min(R, lo + RB);
+  if (lo >= hi) return;
+  int e = 0, top = E;  // first group whose end is past lo (s_end is non-decreasing)
+  while (e < top) {
+    const int mid = (e + top) / 2;
+    if (s_end[mid] > lo) top = mid; else e = mid + 1;
+  }
+  for (int64_t a = lo; a < hi && e <= E; ++e) {
+    const int64_t b = min(hi, s_end[e]);  // rows [a, b) of group e (e == E: past the groups)
+    if (b <= a) continue;
+    float cm[CPL][8];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cm[i][k] = 0.f;
+    for (int64_t r = a + wv; r < b; r += 4) {
+      const uint16_t* xr = x + r * C;
+      uint4 v[CPL];
+      float am[P];
+#pragma unroll
+      for (int p = 0; p < P; ++p) am[p] = 0.f;
+      uint32_t nan = 0;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < cpr ? *(const uint4*)(xr + c * 8) : make_uint4(0, 0, 0, 0);
+        const float a8 = amax8(v[i]);
+        if (P == 1 || c < kc) am[0] = fmaxf(am[0], a8);
+        else am[P - 1] = fmaxf(am[P - 1], a8);
+        nan |= has_nan8(v[i]);
+        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          cm[i][2 * k] = fmaxf(cm[i][2 * k], fabsf(bf_lo(w[k])));
+          cm[i][2 * k + 1] = fmaxf(cm[i][2 * k + 1], fabsf(bf_hi(w[k])));
+        }
+      }
+      float sp[P];
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        sp[p] = scale_of(wave_max(am[p]));
+        if (lane == 0) scale[r * P + p] = sp[p];
+      }
+      const bool fast = wave_nan_free(nan);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < cpr) *(uint2*)(q + r * C + c * 8) = quant8(v[i], (P == 1 || c < kc) ? sp[0] : sp[P - 1], fast);
+      }
+    }
+    if (e == E) break;
+    // the block leaves group e: merge the waves' maxima, one atomic per column
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + 64 * i;
+      if (c < cpr) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) atomicMax(&s_cm[c * 8 + k], __float_as_uint(cm[i][k]));
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < C; i += blockDim.x) {
+      atomicMax(&group_amax[(int64_t)e * C + i], s_cm[i]);
+      s_cm[i] = 0u;
+    }
+    __syncthreads();
+    a = b;
+  }
+}
+
 // Column amax over `n_rows` rows of a COLS-column slab (row stride ld elements)
 // -> s_amax[COLS]; every thread of the 4 COLS-thread block calls it. Four independent 16-byte
 // loads per thread are in flight per iteration.
@@ -521,11 +630,14 @@ __global__ __launch_bounds__(4 * COLS) void quant_cols_t_kernel(const uint16_t* 
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
 // 16-aligned offset pstart_e, zero padded to ceil16(count_e)), scale [E][C].
-// Block per (e, COLS columns); empty groups exit.
+// Block per (e, COLS columns); empty groups exit. With amax_in (the column amax
+// [E][C] of every group already known, from quant_rows_groupamax_kernel) the
+// amax pass is skipped and x is read once.
 template <int COLS>
 __global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ counts,
                                                              int64_t R, int E, int C, int64_t Rpad,
-                                                             uint8_t* __restrict__ q, float* __restrict__ scale) {
+                                                             uint8_t* __restrict__ q, float* __restrict__ scale,
+                                                             const float* __restrict__ amax_in) {
   __shared__ float s_red[COLS * 33];
   __shared__ float s_amax[COLS];
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
@@ -557,7 +669,12 @@ __global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t
   const int n_out = (n + kPad - 1) / kPad * kPad;
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
   const uint16_t* base = x + (int64_t)seg0 * C + c0;
-  slab_amax<COLS>(base, C, n, s_red, s_amax);
+  if (amax_in) {
+    if (threadIdx.x < COLS) s_amax[threadIdx.x] = amax_in[(int64_t)e * C + c0 + threadIdx.x];
+    __syncthreads();
+  } else {
+    slab_amax<COLS>(base, C, n, s_red, s_amax);
+  }
   if (threadIdx.x < COLS) {
     const float s = scale_of(s_amax[threadIdx.x]);
     s_amax[threadIdx.x] = s;
@@ -1379,7 +1496,7 @@ MOE_API int moe_fp8_quant_cols_t_amax(const uint16_t* x, const float* col_amax, 
 
 MOE_API int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int32_t a, int32_t b, uint8_t* q,
                                        float* scale, float* col_amax, hipStream_t stream) {
-  if (n_experts < 1 || a < 1 || b < 8 || b % 8 || b > 4096) return kErrInvalidArgument;
+  if (n_experts < 1 || a < 1 || b < 8 || b % 8 || b > 8192) return kErrInvalidArgument;
   if (!x || !q || !scale || !col_amax) return kErrInvalidArgument;
   // E x S blocks, S row slices per expert: sixteen blocks per CU (at the Kimi
   // weights 0.37 ms against 0.38-0.44 ms for two to eight per CU; a slice's
@@ -1396,23 +1513,80 @@ MOE_API int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int
     hipLaunchKernelGGL(quant_rows_colamax_kernel<4>, grid, block, 0, stream, x, a, b, rb, q, scale, cm);
   else if (chunks <= 64 * 5)
     hipLaunchKernelGGL(quant_rows_colamax_kernel<5>, grid, block, 0, stream, x, a, b, rb, q, scale, cm);
-  else
+  else if (chunks <= 64 * 8)
     hipLaunchKernelGGL(quant_rows_colamax_kernel<8>, grid, block, 0, stream, x, a, b, rb, q, scale, cm);
+  else
+    hipLaunchKernelGGL(quant_rows_colamax_kernel<16>, grid, block, 0, stream, x, a, b, rb, q, scale, cm);
+  return launch_status();
+}
+
+static int quant_tokens_t(const uint16_t* x, const float* group_amax, const int64_t* counts, int64_t n_rows,
+                          int32_t n_experts, int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
+                          hipStream_t stream) {
+  if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
+  if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
+  if (!x || !counts || !q || !scale) return kErrInvalidArgument;
+  if (cols % 128 == 0)
+    hipLaunchKernelGGL(quant_tokens_t_kernel<128>, dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x, counts,
+                       n_rows, n_experts, cols, padded_rows, q, scale, group_amax);
+  else
+    hipLaunchKernelGGL(quant_tokens_t_kernel<64>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
+                       n_rows, n_experts, cols, padded_rows, q, scale, group_amax);
   return launch_status();
 }
 
 MOE_API int moe_fp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
                                    int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
                                    hipStream_t stream) {
-  if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
-  if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
-  if (!x || !counts || !q || !scale) return kErrInvalidArgument;
-  if (cols % 128 == 0)
-    hipLaunchKernelGGL(quant_tokens_t_kernel<128>, dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x, counts,
-                       n_rows, n_experts, cols, padded_rows, q, scale);
+  return quant_tokens_t(x, nullptr, counts, n_rows, n_experts, cols, padded_rows, q, scale, stream);
+}
+
+MOE_API int moe_fp8_quant_tokens_t_amax(const uint16_t* x, const float* group_amax, const int64_t* counts,
+                                        int64_t n_rows, int32_t n_experts, int32_t cols, int64_t padded_rows,
+                                        uint8_t* q, float* scale, hipStream_t stream) {
+  if (!group_amax) return kErrInvalidArgument;
+  return quant_tokens_t(x, group_amax, counts, n_rows, n_experts, cols, padded_rows, q, scale, stream);
+}
+
+template <int P>
+static void launch_rows_groupamax(int chunks, dim3 grid, hipStream_t stream, const uint16_t* x, const int64_t* counts,
+                                  int64_t rows, int e, int cols, int rb, uint8_t* q, float* scale, uint32_t* gam) {
+  if (chunks <= 64 * 2)
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<2, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
+                       q, scale, gam);
+  else if (chunks <= 64 * 4)
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<4, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
+                       q, scale, gam);
+  else if (chunks <= 64 * 5)
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<5, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
+                       q, scale, gam);
+  else if (chunks <= 64 * 8)
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<8, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
+                       q, scale, gam);
   else
-    hipLaunchKernelGGL(quant_tokens_t_kernel<64>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
-                       n_rows, n_experts, cols, padded_rows, q, scale);
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<16, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
+                       q, scale, gam);
+}
+
+MOE_API int moe_fp8_quant_rows_groupamax(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                         int32_t cols, int32_t pieces, uint8_t* q, float* scale, float* group_amax,
+                                         hipStream_t stream) {
+  if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || (pieces != 1 && pieces != 2)) return kErrInvalidArgument;
+  if (cols < 8 * pieces || cols % (8 * pieces) || cols > 8192) return kErrInvalidArgument;
+  if (n_rows >= (int64_t)INT32_MAX / 2) return kErrUnsupportedShape;
+  if (n_rows == 0) return kOk;
+  if (!x || !counts || !q || !scale || !group_amax) return kErrInvalidArgument;
+  // blocks of RB consecutive rows, sixteen per CU (a block's atomics are one per
+  // column for each group it leaves)
+  const int64_t want = 16 * (int64_t)cu_count();
+  int64_t rb = (n_rows + want - 1) / want;
+  if (rb < 16) rb = 16;
+  const dim3 grid((unsigned)((n_rows + rb - 1) / rb));
+  uint32_t* gam = (uint32_t*)group_amax;
+  if (pieces == 1)
+    launch_rows_groupamax<1>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale, gam);
+  else
+    launch_rows_groupamax<2>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale, gam);
   return launch_status();
 }
 

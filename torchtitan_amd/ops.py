@@ -714,16 +714,48 @@ def _quant_rows(x: Tensor, cols: int) -> tuple[Tensor, Tensor]:
     return q, s
 
 
+# widest rows the row quantizers with a column amax on the side take (their
+# rows stay in registers)
+AMAX_SIDE_MAX_COLS = 8192
+
+
+def _amax_shape(e: int, cols: int) -> tuple[int, ...]:
+    """Shape of a column amax taken on the side of a row quantization: [E, cols],
+    or empty when the rows are too wide (the transposed quantizer then takes its
+    own amax pass)."""
+    return (e, cols) if cols <= AMAX_SIDE_MAX_COLS else (0,)
+
+
 def _quant_rows_colamax(w: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """w [E, A, B] bf16 -> (q [E, A, B] fp8 with a scale per row, scale [E * A],
     column amax [E, B] over A): the row quantization and, on the side, what the
     transposed one needs, from one read."""
     e, a, b = w.shape
+    if b > AMAX_SIDE_MAX_COLS:
+        q, s = _quant_rows(w, b)
+        return q.view(e, a, b), s, w.new_empty(0, dtype=torch.float32)
     q = torch.empty(e, a, b, dtype=FP8, device=w.device)
     s = torch.empty(e * a, dtype=torch.float32, device=w.device)
     amax = torch.zeros(e, b, dtype=torch.float32, device=w.device)
     call("moe_fp8_quant_rows_colamax", ptr(w), e, a, b, ptr(q), ptr(s), ptr(amax), stream_of(w))
     return q, s, amax
+
+
+def _quant_rows_groupamax(x: Tensor, counts: Tensor, e: int, pieces: int = 1) -> tuple[Tensor, Tensor, Tensor]:
+    """x [R, C] bf16 in expert token groups -> (q [R, C] fp8 with a scale per row
+    piece of C / pieces columns, scale [R * pieces], the column amax [E, C] of
+    each group): the row quantization and, on the side, what the token-transposed
+    one needs, from one read."""
+    r, c = x.shape
+    if c > AMAX_SIDE_MAX_COLS:
+        q, sc = _quant_rows(x, c // pieces)
+        return q.view(r, c), sc, x.new_empty(0, dtype=torch.float32)
+    q = torch.empty(r, c, dtype=FP8, device=x.device)
+    sc = torch.empty(r * pieces, dtype=torch.float32, device=x.device)
+    amax = torch.zeros(e, c, dtype=torch.float32, device=x.device)
+    call("moe_fp8_quant_rows_groupamax", ptr(x), ptr(counts), r, e, c, pieces, ptr(q), ptr(sc), ptr(amax),
+         stream_of(x))
+    return q, sc, amax
 
 
 def _quant_cols_t(w: Tensor, amax: Tensor, q: Tensor, q_offset: int, q_estride: int, q_ld: int, scale: Tensor,
@@ -745,23 +777,31 @@ def _padded_rows(r: int, e: int) -> int:
     return (n + 15) // 16 * 16
 
 
-def _quant_tokens_t(x: Tensor, counts: Tensor, e: int, rpad: int) -> tuple[Tensor, Tensor]:
-    """x [R, C] bf16 in expert token groups -> (q [C, rpad], scale [E, C])."""
+def _quant_tokens_t(x: Tensor, counts: Tensor, e: int, rpad: int,
+                    amax: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """x [R, C] bf16 in expert token groups -> (q [C, rpad], scale [E, C]); from
+    the groups' known column amax when there is one (one read of x), else with
+    its own amax pass."""
     r, c = x.shape
     q = torch.empty(c, rpad, dtype=FP8, device=x.device)
     s = torch.empty(e, c, dtype=torch.float32, device=x.device)
-    call("moe_fp8_quant_tokens_t", ptr(x), ptr(counts), r, e, c, rpad, ptr(q), ptr(s), stream_of(x))
+    if amax is not None and amax.numel():
+        call("moe_fp8_quant_tokens_t_amax", ptr(x), ptr(amax), ptr(counts), r, e, c, rpad, ptr(q), ptr(s),
+             stream_of(x))
+    else:
+        call("moe_fp8_quant_tokens_t", ptr(x), ptr(counts), r, e, c, rpad, ptr(q), ptr(s), stream_of(x))
     return q, s
 
 
 @torch.library.custom_op("moe_mi355x::grouped_swiglu_fp8", mutates_args=())
 def grouped_swiglu_fp8(
     x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor
-) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """fp8 e4m3 grouped SwiGLU: x, h quantized per token row, weights per
-    output row; fp32 accumulate; bf16 outputs (y, g, u, h), then the weights'
-    column amax over the forward's output rows (w1, w3 [E, D], w2 [E, H]) that
-    the backward's transposed quantizations use."""
+    output row; fp32 accumulate; bf16 outputs (y, g, u, h), then the column
+    amax the backward's transposed quantizations use, taken on the side of the
+    forward's: the weights' over their output rows (w1, w3 [E, D], w2 [E, H])
+    and x's and h's over each expert's tokens ([E, D], [E, H])."""
     require_gpu(x, w1, w2, w3, num_tokens_per_expert)
     for t, name in ((x, "x"), (w1, "w1"), (w2, "w2"), (w3, "w3")):
         if t.dtype != torch.bfloat16:
@@ -771,7 +811,7 @@ def grouped_swiglu_fp8(
     r, d = x.shape
     e, h_dim, _ = w1.shape
     s = stream_of(x)
-    qx, sx = _quant_rows(x, d)
+    qx, sx, amx = _quant_rows_groupamax(x, counts, e)
     qw1, sw1, am1 = _quant_rows_colamax(w1)
     qw3, sw3, am3 = _quant_rows_colamax(w3)
     qw2, sw2, am2 = _quant_rows_colamax(w2)
@@ -781,9 +821,9 @@ def grouped_swiglu_fp8(
     y = x.new_empty(r, d)
     call("moe_fp8_gemm_gate_up", ptr(qx), ptr(sx), ptr(qw1), ptr(sw1), ptr(qw3), ptr(sw3), ptr(counts), r, e, d,
          h_dim, ptr(g), ptr(u), ptr(h), s)
-    qh, sh = _quant_rows(h, h_dim)
+    qh, sh, amh = _quant_rows_groupamax(h, counts, e)
     call("moe_fp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
-    return y, g, u, h, am1, am3, am2
+    return y, g, u, h, am1, am3, am2, amx, amh
 
 
 @grouped_swiglu_fp8.register_fake
@@ -792,16 +832,19 @@ def _(x, w1, w2, w3, num_tokens_per_expert):
     e, h_dim = w1.shape[0], w1.shape[1]
     f32 = lambda *shape: x.new_empty(*shape, dtype=torch.float32)  # noqa: E731
     return (x.new_empty(r, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim),
-            f32(e, d), f32(e, d), f32(e, h_dim))
+            f32(*_amax_shape(e, d)), f32(*_amax_shape(e, d)), f32(*_amax_shape(e, h_dim)),
+            f32(*_amax_shape(e, d)), f32(*_amax_shape(e, h_dim)))
 
 
 @torch.library.custom_op("moe_mi355x::grouped_swiglu_fp8_backward", mutates_args=())
 def grouped_swiglu_fp8_backward(
     dy: Tensor, x: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
-    g: Tensor, u: Tensor, h: Tensor, amax_w1: Tensor, amax_w3: Tensor, amax_w2: Tensor,
+    g: Tensor, u: Tensor, h: Tensor, amax_w1: Tensor, amax_w3: Tensor, amax_w2: Tensor, amax_x: Tensor,
+    amax_h: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """Gradients of grouped_swiglu_fp8. amax_w* are the forward's column amax of
-    the weights (empty tensors: the transposed quantizers take their own)."""
+    """Gradients of grouped_swiglu_fp8. amax_* are the forward's column amax of
+    the weights and of x and h per token group (empty tensors: the transposed
+    quantizers take their own)."""
     require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
     dy = dy.to(torch.bfloat16).contiguous()
     counts = num_tokens_per_expert.to(torch.int64).contiguous()
@@ -810,7 +853,7 @@ def grouped_swiglu_fp8_backward(
     dev = x.device
     s = stream_of(x)
     # dh = dy . w2 (contraction over D): dy per row, w2 per (e, h) column over D
-    qdy, sdy = _quant_rows(dy, d)
+    qdy, sdy, amdy = _quant_rows_groupamax(dy, counts, e)
     qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
     sw2t = torch.empty(e, h_dim, dtype=torch.float32, device=dev)
     _quant_cols_t(w2.contiguous(), amax_w2.contiguous(), qw2t, 0, h_dim * d, d, sw2t, 0, h_dim)
@@ -819,7 +862,7 @@ def grouped_swiglu_fp8_backward(
          h_dim, ptr(dgu), s)
     # dx = dg . w1 + du . w3 (contraction over H): one scale per dg / du row half,
     # w1 and w3 per (e, d) column over H, written side by side as [E, D, 2H]
-    qdgu, sdgu = _quant_rows(dgu, h_dim)
+    qdgu, sdgu, amdgu = _quant_rows_groupamax(dgu, counts, e, pieces=2)
     qw13t = torch.empty(e, d, 2 * h_dim, dtype=FP8, device=dev)
     sw13t = torch.empty(e, 2, d, dtype=torch.float32, device=dev)
     _quant_cols_t(w1.contiguous(), amax_w1.contiguous(), qw13t, 0, d * 2 * h_dim, 2 * h_dim, sw13t, 0, 2 * d)
@@ -829,14 +872,14 @@ def grouped_swiglu_fp8_backward(
          ptr(dx), s)
     # weight gradients: contraction over each expert's tokens (per-group scales)
     rpad = _padded_rows(r, e)
-    qdgut, sdgut = _quant_tokens_t(dgu, counts, e, rpad)
-    qxt, sxt = _quant_tokens_t(x, counts, e, rpad)
+    qdgut, sdgut = _quant_tokens_t(dgu, counts, e, rpad, amdgu)
+    qxt, sxt = _quant_tokens_t(x, counts, e, rpad, amax_x)
     dw1 = torch.empty_like(w1)
     dw3 = torch.empty_like(w3)
     call("moe_fp8_gemm_bwd_dw13", ptr(qdgut), ptr(sdgut), ptr(qxt), ptr(sxt), ptr(counts), r, rpad, e, d, h_dim,
          ptr(dw1), ptr(dw3), s)
-    qdyt, sdyt = _quant_tokens_t(dy, counts, e, rpad)
-    qht, sht = _quant_tokens_t(h, counts, e, rpad)
+    qdyt, sdyt = _quant_tokens_t(dy, counts, e, rpad, amdy)
+    qht, sht = _quant_tokens_t(h, counts, e, rpad, amax_h)
     dw2 = torch.empty_like(w2)
     call("moe_fp8_gemm_bwd_dw2", ptr(qdyt), ptr(sdyt), ptr(qht), ptr(sht), ptr(counts), r, rpad, e, d, h_dim,
          ptr(dw2), s)
@@ -844,23 +887,23 @@ def grouped_swiglu_fp8_backward(
 
 
 @grouped_swiglu_fp8_backward.register_fake
-def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h, amax_w1, amax_w3, amax_w2):
+def _(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h, amax_w1, amax_w3, amax_w2, amax_x, amax_h):
     return x.new_empty(x.shape), torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
 
 
 def _gs8_setup(ctx, inputs, output):
     x, w1, w2, w3, counts = inputs
-    _y, g, u, h, am1, am3, am2 = output
-    ctx.save_for_backward(x, w1, w2, w3, counts, g, u, h, am1, am3, am2)
-    ctx.mark_non_differentiable(g, u, h, am1, am3, am2)
+    _y, g, u, h, *amax = output
+    ctx.save_for_backward(x, w1, w2, w3, counts, g, u, h, *amax)
+    ctx.mark_non_differentiable(g, u, h, *amax)
     ctx.set_materialize_grads(False)
 
 
 def _gs8_bwd(ctx, dy, *_unused):
-    x, w1, w2, w3, counts, g, u, h, am1, am3, am2 = ctx.saved_tensors
+    x, w1, w2, w3, counts, g, u, h, *amax = ctx.saved_tensors
     if dy is None:
         return None, None, None, None, None
-    dx, dw1, dw2, dw3 = grouped_swiglu_fp8_backward(dy, x, w1, w2, w3, counts, g, u, h, am1, am3, am2)
+    dx, dw1, dw2, dw3 = grouped_swiglu_fp8_backward(dy, x, w1, w2, w3, counts, g, u, h, *amax)
     return dx, dw1, dw2, dw3, None
 
 
