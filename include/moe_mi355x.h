@@ -314,7 +314,12 @@ int moe_grouped_col_sum(const uint16_t* src, int64_t ld_src, const int64_t* coun
  * ------------------------------------------------------------------------- */
 
 /* Rows of the token-transposed fp8 tensors: n_rows + n_experts * 15 (every
- * group starts at a multiple of 16); round it up to a multiple of 16. */
+ * group starts at a multiple of 16); round it up to a multiple of 16. Rounded up
+ * to a multiple of 128 (with 128-byte aligned tensors), every row of those
+ * tensors starts on a 128-byte line, and the transposing quantizers and the
+ * weight-gradient GEMMs read and write whole lines (each starts its passes and
+ * k-steps at the group's offset rounded down to 128 bytes, the bytes before the
+ * group masked). */
 int64_t moe_fp8_padded_rows(int64_t n_rows, int32_t n_experts);
 
 /* x [rows, cols] bf16 -> q [rows, cols] fp8, scale [rows] (one per row). */
@@ -416,7 +421,8 @@ int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const uint8_t* 
  * ------------------------------------------------------------------------- */
 
 /* Rows of the token-transposed MXFP8 tensors: n_rows + n_experts * 31 rounded
- * up to a multiple of 32 (every group starts at a multiple of 32). */
+ * up to a multiple of 32 (every group starts at a multiple of 32); a multiple of
+ * 128 is faster, as for moe_fp8_padded_rows. */
 int64_t moe_mxfp8_padded_rows(int64_t n_rows, int32_t n_experts);
 
 /* x [rows, cols] bf16 (cols % 32 == 0) -> q [rows, cols], scale [rows, cols / 32]. */

@@ -457,9 +457,10 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
                                              int64_t sc_b, int64_t sc_k, const float* s_col, uint32_t* s_tile,
                                              uint8_t* __restrict__ qr = nullptr, int64_t ldr = 0,
                                              uint8_t* __restrict__ sr = nullptr, int64_t ldsr = 0,
-                                             RowGather gather = RowGather{}) {
+                                             RowGather gather = RowGather{}, int shift = 0) {
   constexpr int T = 4 * COLS, CPR = COLS / 8;
   const int t = threadIdx.x;
+  auto in_rows = [&](int row) { return row >= 0 && row < n_rows; };
   uint4 va[4], vb[4];
   int64_t ia[4], ib[4];  // GATHER: source rows of the pass two ahead of va / vb
   float sa[4], sb[4];    // GATHER with scale: the row scales of the pass in va / vb
@@ -467,7 +468,7 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = (t + i * T) / CPR;
-      ix[i] = a0 + r < n_rows ? gather.idx[a0 + r] : -1;
+      ix[i] = in_rows(a0 + r) ? gather.idx[a0 + r] : -1;
     }
   };
   auto load = [&](uint4 (&v)[4], const int64_t (&ix)[4], float (&sv)[4], int a0) {
@@ -478,9 +479,9 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       if constexpr (GATHER) {
         v[i] = (ix[i] >= 0 && ix[i] < gather.n_src) ? *(const uint4*)(gather.src + ix[i] * gather.ld + ch * 8)
                                                      : make_uint4(0, 0, 0, 0);
-        if (gather.scale) sv[i] = a0 + r < n_rows ? gather.scale[a0 + r] : 0.f;
+        if (gather.scale) sv[i] = in_rows(a0 + r) ? gather.scale[a0 + r] : 0.f;
       } else {
-        v[i] = (a0 + r < n_rows) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+        v[i] = in_rows(a0 + r) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
       }
     }
   };
@@ -489,7 +490,7 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
       if (!gather.scale) return;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (a0 + (t + i * T) / CPR >= n_rows) continue;
+        if (!in_rows(a0 + (t + i * T) / CPR)) continue;
         float f[8];
         Chunk<uint16_t>::unpack(v[i], f);
 #pragma unroll
@@ -514,7 +515,7 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
         a = fmaxf(a, __shfl_xor(a, 1));
         a = fmaxf(a, __shfl_xor(a, 2));
         const uint32_t e = mx_exponent(a);
-        if (a0 + r < n_rows) {
+        if (in_rows(a0 + r)) {
           *(uint2*)(qr + (int64_t)(a0 + r) * ldr + ch * 8) = mx_quant8(v[i], mx_multiplier(e), rows_fast);
           if ((ch & 3) == 0) sr[(int64_t)(a0 + r) * ldsr + (ch >> 2)] = (uint8_t)e;
         }
@@ -570,28 +571,32 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
           for (int bq = 0; bq < 4; ++bq) o[q] |= e4m3(xv[4 * q + bq] * f) << (8 * bq);
         }
       }
-      if (rb < n_out) {
+      if (rb >= 0 && rb < n_out) {
         *(uint4*)(out + (int64_t)cc * ldo + rb) = make_uint4(o[0], o[1], o[2], o[3]);
         if constexpr (MX)
           if ((kq & 1) == 0) sc[(int64_t)cc * sc_b + (int64_t)(rb / kMxBlock) * sc_k] = (uint8_t)e;
       }
     }
   };
+  // passes start `shift` rows before the slab (rows < 0 are neither loaded nor
+  // stored), so that with shift = the output offset mod 128 every pass writes
+  // whole 128-byte lines of each output row
+  const int b0 = -shift;
   if constexpr (GATHER) {
-    if (n_out > 0) load_idx(ia, 0);
-    if (n_out > kTRows) load_idx(ib, kTRows);
+    if (n_out > b0) load_idx(ia, b0);
+    if (n_out > b0 + kTRows) load_idx(ib, b0 + kTRows);
   }
-  if (n_out > 0) {
-    load(va, ia, sa, 0);
+  if (n_out > b0) {
+    load(va, ia, sa, b0);
     if constexpr (GATHER)
-      if (n_out > 2 * kTRows) load_idx(ia, 2 * kTRows);
+      if (n_out > b0 + 2 * kTRows) load_idx(ia, b0 + 2 * kTRows);
   }
-  if (n_out > kTRows) {
-    load(vb, ib, sb, kTRows);
+  if (n_out > b0 + kTRows) {
+    load(vb, ib, sb, b0 + kTRows);
     if constexpr (GATHER)
-      if (n_out > 3 * kTRows) load_idx(ib, 3 * kTRows);
+      if (n_out > b0 + 3 * kTRows) load_idx(ib, b0 + 3 * kTRows);
   }
-  for (int a0 = 0; a0 < n_out; a0 += 2 * kTRows) {
+  for (int a0 = b0; a0 < n_out; a0 += 2 * kTRows) {
     pass(va, ia, sa, a0);
     if (a0 + kTRows < n_out) pass(vb, ib, sb, a0 + kTRows);
   }
@@ -683,7 +688,7 @@ __global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t
   }
   __syncthreads();
   slab_t_quant<false, false, COLS>(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, nullptr, 0, 0, s_amax,
-                             s_tile);
+                                   s_tile, nullptr, 0, nullptr, 0, RowGather{}, pstart % 128);
 }
 
 // ---------------------------------------------------------------------------
@@ -815,7 +820,7 @@ __global__ __launch_bounds__(4 * COLS) void mx_quant_tokens_t_kernel(const uint1
                                  q + (int64_t)c0 * Rpad + pstart, Rpad, s + (int64_t)(pstart / kMxBlock) * C + c0, 1, C,
                                  nullptr, s_tile, ROWS ? qr + (int64_t)seg0 * C + c0 : nullptr, C,
                                  ROWS ? sr + (int64_t)seg0 * (C / kMxBlock) + c0 / kMxBlock : nullptr, C / kMxBlock,
-                                 gather);
+                                 gather, pstart % 128);
 }
 
 // ---------------------------------------------------------------------------
@@ -949,7 +954,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
   const int G = gridDim.x;
   const int lb = (G % 8 == 0) ? ((int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
 
-  struct TileRef { int e, seg0, seg1, pst0, mt, nt, klen, nk; };
+  // ks: bytes of k the token-transposed stages start before the group (pst0 mod 128,
+  // masked), so that every stage reads whole 128-byte lines
+  struct TileRef { int e, seg0, seg1, pst0, mt, nt, klen, nk, ks; };
   auto decode = [&](int t) {
     TileRef r;
     int lo = 0, hi = E - 1;
@@ -971,7 +978,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
       r.mt = local - r.nt * MT;
     }
     r.klen = kRowGrouped ? Kfix : (s_pst[lo + 1] - r.pst0);  // bytes of k
-    r.nk = (r.klen + 127) / 128;
+    r.ks = kRowGrouped ? 0 : r.pst0 % 128;
+    r.nk = (r.klen + r.ks + 127) / 128;
     return r;
   };
 
@@ -1006,7 +1014,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
         srcP[b] = p.qp + (int64_t)rr * Kfix + chP[b];
       } else {
         okP[b] = true;
-        srcP[b] = p.qp + (int64_t)(r.mt * BM + m) * p.Rpad + r.pst0 + chP[b];
+        srcP[b] = p.qp + (int64_t)(r.mt * BM + m) * p.Rpad + (r.pst0 - r.ks) + chP[b];
       }
     }
 #pragma unroll
@@ -1024,7 +1032,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
       } else if (MODE == kDx) {
         rowp = p.qq + (e64 * D + r.nt * BN + n) * (int64_t)(2 * H);
       } else {
-        rowp = p.qq + (int64_t)(r.nt * BN + n) * p.Rpad + r.pst0;
+        rowp = p.qq + (int64_t)(r.nt * BN + n) * p.Rpad + (r.pst0 - r.ks);
       }
       srcQ[b] = rowp + chQ[b];
     }
@@ -1059,7 +1067,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
         const int sub = isP ? gl : gl - BM / 4;
         const int cpk = isP ? BM / 16 : BN / 16;  // 16-byte chunks per k-block
         kbS = sub / cpk;
-        const int64_t kb0 = r.pst0 / kMxBlock + kbS;
+        const int64_t kb0 = (r.pst0 - r.ks) / kMxBlock + kbS;
         kstrideS = isP ? Mfix : Ntot;
         srcS = (isP ? p.ep + kb0 * Mfix + r.mt * BM : p.eq + kb0 * Ntot + r.nt * BN) + (sub % cpk) * 16;
       }
@@ -1070,19 +1078,22 @@ __global__ __launch_bounds__(NW * 64, OCC) void fp8_gemm_kernel(Params p) {
     const int k0 = kt * 128;
 #pragma unroll
     for (int b = 0; b < CPW_P; ++b) {
-      const bool ok = okP[b] && k0 + chP[b] < r.klen;
+      const int kk = k0 + chP[b] - r.ks;  // k of this chunk within the group
+      const bool ok = okP[b] && kk >= 0 && kk < r.klen;
       dma16(ok ? (const void*)(srcP[b] + k0) : (const void*)kZeroRow, lds_addr(&sP[s][(wv * CPW_P + b) * 1024]));
     }
 #pragma unroll
     for (int b = 0; b < CPW_Q; ++b) {
-      const bool ok = k0 + chQ[b] < r.klen;
+      const int kk = k0 + chQ[b] - r.ks;
+      const bool ok = kk >= 0 && kk < r.klen;
       dma16(ok ? (const void*)(srcQ[b] + k0) : (const void*)kZeroRow, lds_addr(&sQ[s][(wv * CPW_Q + b) * 1024]));
     }
     if (MX) {
       if (kRowGrouped) {
         dma4(okS ? (const void*)(srcS + kt * 4) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 256]));
       } else if (wv < NW / 4) {
-        const bool ok = (4 * kt + kbS) * kMxBlock < r.klen;
+        const int kk = (4 * kt + kbS) * kMxBlock - r.ks;
+        const bool ok = kk >= 0 && kk < r.klen;
         dma16(ok ? (const void*)(srcS + 4 * kt * kstrideS) : (const void*)kUnitScales, lds_addr(&sS[s][wv * 1024]));
       }
     }
