@@ -463,7 +463,7 @@ int moe_mxfp8_quant_dual_tokens(const uint16_t* x, const int64_t* counts, int64_
  * row_scale[r], rounded to bf16, when row_scale != NULL) read from src [n_src,
  * cols] in place: the expert permute (moe.py:445-451, x[token_idx] * score) and
  * the quantization of its output in one pass, without writing the routed rows.
- * Rows whose index is outside [0, n_src) read as zeros. src must be 16-byte
+ * Rows whose index is outside [0, n_src) read as zeros. n_src >= 1; src must be 16-byte
  * aligned (rows are read in 16-byte pieces). */
 int moe_mxfp8_quant_dual_tokens_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
                                        const float* row_scale, const int64_t* counts, int64_t n_rows,

@@ -461,28 +461,49 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
   constexpr int T = 4 * COLS, CPR = COLS / 8;
   const int t = threadIdx.x;
   auto in_rows = [&](int row) { return row >= 0 && row < n_rows; };
+  // Barriers wait for LDS only: __syncthreads() would also drain the global loads
+  // of the passes ahead and the stores behind (its workgroup-scope fence is a
+  // vmcnt(0)), which left one pass in flight. The tile's NaN flag is one word
+  // per wave, written before and read after the second barrier of a pass (the
+  // next pass's writes come after its first barrier, so one set of words does).
+  __shared__ uint32_t s_wnan[T / 64];
+  auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
   uint4 va[4], vb[4];
   int64_t ia[4], ib[4];  // GATHER: source rows of the pass two ahead of va / vb
   float sa[4], sb[4];    // GATHER with scale: the row scales of the pass in va / vb
+  // Every load is issued, rows outside the slab (and passes past its end) reading
+  // a clamped row whose value is then dropped: with no load skipped on any path,
+  // the compiler counts the loads in flight and waits for one pass's rows with
+  // vmcnt(N) rather than vmcnt(0), which drained the pass ahead as well.
+  // The rows' values are zeroed where they are consumed (zero_rows), not where they
+  // are loaded: a select right after a load makes the load's wait immediate.
+  auto clamp_row = [&](int row) { return row < 0 ? 0 : (row >= n_rows ? n_rows - 1 : row); };
   auto load_idx = [&](int64_t (&ix)[4], int a0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (t + i * T) / CPR;
-      ix[i] = in_rows(a0 + r) ? gather.idx[a0 + r] : -1;
-    }
+    for (int i = 0; i < 4; ++i) ix[i] = gather.idx[clamp_row(a0 + (t + i * T) / CPR)];
   };
-  auto load = [&](uint4 (&v)[4], const int64_t (&ix)[4], float (&sv)[4], int a0) {
+  // GATHER: ok gets bit i when load i reads a row of the slab with a source row in range
+  auto load = [&](uint4 (&v)[4], const int64_t (&ix)[4], float (&sv)[4], uint32_t& ok, int a0) {
+    ok = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * T;
       const int r = c / CPR, ch = c % CPR;
       if constexpr (GATHER) {
-        v[i] = (ix[i] >= 0 && ix[i] < gather.n_src) ? *(const uint4*)(gather.src + ix[i] * gather.ld + ch * 8)
-                                                     : make_uint4(0, 0, 0, 0);
-        if (gather.scale) sv[i] = in_rows(a0 + r) ? gather.scale[a0 + r] : 0.f;
+        const bool in = in_rows(a0 + r) && ix[i] >= 0 && ix[i] < gather.n_src;
+        ok |= in ? 1u << i : 0u;
+        v[i] = *(const uint4*)(gather.src + (in ? ix[i] : 0) * gather.ld + ch * 8);
+        if (gather.scale) sv[i] = gather.scale[clamp_row(a0 + r)];
       } else {
-        v[i] = in_rows(a0 + r) ? *(const uint4*)(base + (int64_t)(a0 + r) * ld + ch * 8) : make_uint4(0, 0, 0, 0);
+        v[i] = *(const uint4*)(base + (int64_t)clamp_row(a0 + r) * ld + ch * 8);
       }
+    }
+  };
+  auto zero_rows = [&](uint4 (&v)[4], uint32_t ok, int a0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool in = GATHER ? ((ok >> i) & 1u) != 0u : in_rows(a0 + (t + i * T) / CPR);
+      if (!in) v[i] = make_uint4(0, 0, 0, 0);
     }
   };
   auto apply_scales = [&](uint4 (&v)[4], const float (&sv)[4], int a0) {
@@ -501,7 +522,8 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
   };
   // one pass of 128 rows held in v; v is reloaded with the pass two ahead as soon
   // as it is in LDS, so two passes' loads are in flight while one is transposed
-  auto pass = [&](uint4 (&v)[4], int64_t (&ix)[4], float (&sv)[4], int a0) {
+  auto pass = [&](uint4 (&v)[4], int64_t (&ix)[4], float (&sv)[4], uint32_t& ok, int a0) {
+    zero_rows(v, ok, a0);
     apply_scales(v, sv, a0);
     const uint32_t nan = has_nan8(v[0]) | has_nan8(v[1]) | has_nan8(v[2]) | has_nan8(v[3]);
     if constexpr (ROWS) {
@@ -521,19 +543,24 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
         }
       }
     }
-    __syncthreads();  // every thread's reads of the previous pass are done
+    lds_barrier();  // every thread's LDS reads of the previous pass are done
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = t + i * T;
       const int r = c / CPR;
       *(uint4*)(s_tile + r * (COLS / 2) + (((c % CPR) ^ ((r >> 4) & 7)) * 4)) = v[i];
     }
-    const bool fast = !__syncthreads_or(nan != 0u);  // block-uniform: the tile holds no NaN
-    if (a0 + 2 * kTRows < n_out) {
-      load(v, ix, sv, a0 + 2 * kTRows);
-      if constexpr (GATHER)
-        if (a0 + 4 * kTRows < n_out) load_idx(ix, a0 + 4 * kTRows);
+    {
+      const bool wave_nan = !wave_nan_free(nan);
+      if ((t & 63) == 0) s_wnan[t >> 6] = wave_nan ? 1u : 0u;
     }
+    lds_barrier();  // the tile and the flags are in LDS
+    uint32_t any_nan = 0;
+#pragma unroll
+    for (int w = 0; w < T / 64; ++w) any_nan |= s_wnan[w];
+    const bool fast = any_nan == 0u;  // block-uniform: the tile holds no NaN
+    load(v, ix, sv, ok, a0 + 2 * kTRows);
+    if constexpr (GATHER) load_idx(ix, a0 + 4 * kTRows);
     // unit (column cc, rows 16 kq .. 16 kq + 15 of the pass): 8 consecutive lanes cover one
     // output row's 128 bytes, so every store instruction writes 8 rows x 128 contiguous bytes
 #pragma unroll
@@ -583,22 +610,17 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
   // whole 128-byte lines of each output row
   const int b0 = -shift;
   if constexpr (GATHER) {
-    if (n_out > b0) load_idx(ia, b0);
-    if (n_out > b0 + kTRows) load_idx(ib, b0 + kTRows);
+    load_idx(ia, b0);
+    load_idx(ib, b0 + kTRows);
   }
-  if (n_out > b0) {
-    load(va, ia, sa, b0);
-    if constexpr (GATHER)
-      if (n_out > b0 + 2 * kTRows) load_idx(ia, b0 + 2 * kTRows);
-  }
-  if (n_out > b0 + kTRows) {
-    load(vb, ib, sb, b0 + kTRows);
-    if constexpr (GATHER)
-      if (n_out > b0 + 3 * kTRows) load_idx(ib, b0 + 3 * kTRows);
-  }
+  uint32_t oka, okb;
+  load(va, ia, sa, oka, b0);
+  if constexpr (GATHER) load_idx(ia, b0 + 2 * kTRows);
+  load(vb, ib, sb, okb, b0 + kTRows);
+  if constexpr (GATHER) load_idx(ib, b0 + 3 * kTRows);
   for (int a0 = b0; a0 < n_out; a0 += 2 * kTRows) {
-    pass(va, ia, sa, a0);
-    if (a0 + kTRows < n_out) pass(vb, ib, sb, a0 + kTRows);
+    pass(va, ia, sa, oka, a0);
+    if (a0 + kTRows < n_out) pass(vb, ib, sb, okb, a0 + kTRows);
   }
 }
 
@@ -1801,7 +1823,7 @@ MOE_API int moe_mxfp8_quant_dual_tokens_gather(const uint16_t* src, int64_t n_sr
                                                int32_t n_experts, int32_t cols, int64_t padded_rows,
                                                uint8_t* q_rows, uint8_t* scale_rows, uint8_t* q, uint8_t* scale,
                                                hipStream_t stream) {
-  if (n_src < 0 || !token_idx || reinterpret_cast<uintptr_t>(src) % 16) return kErrInvalidArgument;
+  if (n_src < 1 || !token_idx || reinterpret_cast<uintptr_t>(src) % 16) return kErrInvalidArgument;
   RowGather g;
   g.src = src;
   g.idx = token_idx;
