@@ -182,6 +182,13 @@ def launch_bytes(name: str, a: tuple) -> float | None:
     if name == "moe_fp8_quant_tokens_t_amax":  # the group amax read instead of found
         rows, e, cols, padded = a[3], a[4], a[5], a[6]
         return 2.0 * rows * cols + 1.0 * padded * cols + 8.0 * e * cols + 8.0 * e
+    if name == "moe_fp8_quant_rows_groupamax_gather":  # + the row indices (and scores) read
+        rows, e, cols = a[5], a[6], a[7]
+        return 3.0 * rows * cols + 4.0 * rows + 4.0 * e * cols + 8.0 * e + (8.0 + (4.0 if a[3] else 0.0)) * rows
+    if name == "moe_fp8_quant_tokens_t_amax_gather":
+        rows, e, cols, padded = a[6], a[7], a[8], a[9]
+        idx = (8.0 + (4.0 if a[3] else 0.0)) * rows
+        return 2.0 * rows * cols + 1.0 * padded * cols + 8.0 * e * cols + 8.0 * e + idx
     if name == "moe_mxfp8_quant_rows":
         rows, cols = a[1], a[2]
         return 2.0 * rows * cols + mx * rows * cols

@@ -375,6 +375,21 @@ int moe_fp8_quant_rows_groupamax(const uint16_t* x, const int64_t* counts, int64
                                  int32_t cols, int32_t pieces, uint8_t* q, float* scale, float* group_amax,
                                  moe_stream_t stream);
 
+/* moe_fp8_quant_rows_groupamax (pieces = 1) and moe_fp8_quant_tokens_t_amax of the
+ * routed rows x[token_idx[r]] (times row_scale[r], rounded to bf16, when row_scale
+ * != NULL) read from src [n_src, cols] in place: the expert permute (moe.py:445-451,
+ * x[token_idx] * score) and the fp8 quantizations of its output without writing
+ * the routed rows. Rows whose index is outside [0, n_src) read as zeros. n_src >= 1;
+ * src 16-byte aligned. */
+int moe_fp8_quant_rows_groupamax_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                                        const float* row_scale, const int64_t* counts, int64_t n_rows,
+                                        int32_t n_experts, int32_t cols, uint8_t* q, float* scale,
+                                        float* group_amax, moe_stream_t stream);
+int moe_fp8_quant_tokens_t_amax_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                                       const float* row_scale, const float* group_amax, const int64_t* counts,
+                                       int64_t n_rows, int32_t n_experts, int32_t cols, int64_t padded_rows,
+                                       uint8_t* q, float* scale, moe_stream_t stream);
+
 /* fp8 forward of _run_experts_grouped_mm (moe.py:62-67): g = (qx.qw1^T)*sx*sw1,
  * u likewise with w3, h = bf16(bf16(silu(g)) * u). sw1, sw3 [E, H]. */
 int moe_fp8_gemm_gate_up(const uint8_t* qx, const float* sx, const uint8_t* qw1, const float* sw1,

@@ -128,6 +128,12 @@ def _opcheck_cases(dev):
                 scores_sorted.clone().requires_grad_(True), slot_pos, tok_pos, bf(e, h, d, grad=True, scale=0.05),
                 bf(e, d, h, grad=True, scale=0.05), bf(e, h, d, grad=True, scale=0.05), counts)
 
+    cases["moe_core_fp8"] = (ops.moe_core_fp8, core_args(True))
+    cases["moe_core_fp8_no_shared"] = (ops.moe_core_fp8, core_args(False))
+    core8 = ops.moe_core_fp8(xn_ := bf(n, d), None, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, counts)
+    cases["moe_core_fp8_backward"] = (ops.moe_core_fp8_backward,
+                                      (bf(n, d), xn_, token_idx, scores_sorted, tok_pos, w1, w2, w3, counts,
+                                       *core8[1:]))
     cases["moe_core_mxfp8"] = (ops.moe_core_mxfp8, core_args(True))
     cases["moe_core_mxfp8_no_shared"] = (ops.moe_core_mxfp8, core_args(False))
     xn = bf(n, d)
@@ -173,7 +179,8 @@ OPCHECK_NAMES = ["router", "router_backward", "reorder", "reorder_backward", "pe
                  "combine", "combine_no_shared", "combine_backward", "grouped_swiglu", "grouped_swiglu_backward",
                  "grouped_swiglu_f32", "grouped_swiglu_f32_backward",
                  "grouped_swiglu_fp8", "grouped_swiglu_fp8_backward", "grouped_swiglu_mxfp8",
-                 "grouped_swiglu_mxfp8_backward", "moe_core_mxfp8", "moe_core_mxfp8_no_shared",
+                 "grouped_swiglu_mxfp8_backward", "moe_core_fp8", "moe_core_fp8_no_shared", "moe_core_fp8_backward",
+                 "moe_core_mxfp8", "moe_core_mxfp8_no_shared",
                  "moe_core_mxfp8_backward", "grouped_swiglu_oss", "grouped_swiglu_oss_backward",
                  "gather_rows", "scatter_rows", "swiglu_ffn_backward", "swiglu_ffn_backward_dw_only",
                  "swiglu_forward", "swiglu_backward", "gate_grad_split3", "gate_dw_reduce"]

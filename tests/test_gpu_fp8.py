@@ -435,3 +435,73 @@ def test_fp8_quantizers_nan_elements(dev):
     rq2, _ = R.quant_fp8_rows(xt[100:256].t())
     assert torch.equal(q2[cols, 0:100], rq0.view(torch.uint8)[cols])
     assert torch.equal(q2[:, 112:268], rq2.view(torch.uint8))
+
+
+@pytest.mark.parametrize("cols", [2304, 192])
+@pytest.mark.parametrize("scaled", [True, False])
+def test_fp8_gathering_token_quantizers_match_permute_then_quantize(dev, cols, scaled):
+    """moe_fp8_quant_rows_groupamax_gather and moe_fp8_quant_tokens_t_amax_gather
+    read the routed rows x[token_idx] (* score, rounded to bf16) in place: bytes,
+    scales and group amax identical to the permute op's output fed to the
+    non-gathering quantizers (ragged groups, an empty expert, 64-column slabs)."""
+    banner(f"fp8 gathering token quantizers cols={cols} scaled={scaled}")
+    from torchtitan_amd import ops
+
+    g = torch.Generator().manual_seed(12)
+    n, e, k = 300, 8, 2
+    x = (torch.randn(n, cols, generator=g) * 3).bfloat16().to(dev)
+    logits = torch.randn(n, e, generator=g)
+    logits[:, 5] = -1e9  # expert 5 receives no token
+    top, idx = logits.topk(k, dim=1)
+    scores_sorted, token_idx, counts, _offs, slot_pos, tok_pos = ops.reorder(top.sigmoid().to(dev), idx.to(dev), e)
+    sc = scores_sorted if scaled else None
+    routed = ops.permute(x, slot_pos, tok_pos, sc)
+    q1, s1, a1 = ops._quant_rows_groupamax(routed, counts, e)
+    q2, s2, a2 = ops._quant_rows_groupamax_gather(x, token_idx, sc, counts, e)
+    assert torch.equal(q1, q2) and torch.equal(s1, s2) and torch.equal(a1, a2)
+    rpad = ops._padded_rows(n * k, e)
+    qt1, st1 = ops._quant_tokens_t(routed, counts, e, rpad, a1)
+    qt2, st2 = ops._quant_tokens_t_gather(x, token_idx, sc, counts, e, rpad, a1)
+    used = (counts.cpu() + 15) // 16 * 16
+    assert torch.equal(qt1[:, :int(used.sum())], qt2[:, :int(used.sum())])
+    full = (counts > 0)
+    assert torch.equal(st1[full], st2[full])
+
+
+FP8_LAYER_CASES = {
+    "shared_sigmoid": dict(bs=2, slen=512, dim=512, experts=16, top_k=4, hidden=256, shared_hidden=256),
+    "no_shared_softmax": dict(bs=1, slen=768, dim=768, experts=8, top_k=2, hidden=512, shared_hidden=0,
+                              score_func="softmax", route_norm=False, route_scale=1.0),
+}
+
+
+@pytest.mark.parametrize("name", list(FP8_LAYER_CASES))
+def test_fp8_layer_fused_permute_matches_separate_ops(dev, name):
+    """MoE with fp8 experts and the score before them: the fused op (moe_core_fp8,
+    taken with MoE.fuse_fp8_permute: the permute inside the token quantizers, the
+    combine's gather inside the backward's) gives the output, the input gradient
+    and every parameter gradient bit-identical to permute -> experts -> combine."""
+    banner(f"fp8 layer fused permute {name}")
+    from tests.layer_util import LayerShape, build_layer
+
+    sh = LayerShape(**FP8_LAYER_CASES[name], fp8=True)
+    moe, x, gy = build_layer(sh, dev, seed=6)
+
+    def run(fuse):
+        moe.fuse_fp8_permute = fuse
+        moe.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        assert (moe._fused_core(xx.view(-1, sh.dim)) is not None) == fuse
+        out = moe(xx)
+        out.backward(gy)
+        torch.cuda.synchronize()
+        return out.detach(), xx.grad, {n: p.grad.clone() for n, p in moe.named_parameters()}
+
+    out_s, gx_s, gp_s = run(False)
+    out_f, gx_f, gp_f = run(True)
+    assert torch.equal(out_f, out_s)
+    assert torch.equal(gx_f, gx_s)
+    assert gp_f.keys() == gp_s.keys()
+    for n in gp_s:
+        assert torch.equal(gp_f[n], gp_s[n]), n
+    print(f"[case] {name}: out, grad_x and {len(gp_s)} parameter gradients identical", flush=True)

@@ -414,10 +414,10 @@ def test_mxfp8_layer_fused_permute_matches_separate_ops(dev, name):
     moe, x, gy = build_layer(sh, dev, seed=5)
 
     def run(fuse):
-        moe.fuse_mxfp8_permute = fuse
+        moe.fuse_permute_into_quantizers = fuse
         moe.zero_grad(set_to_none=True)
         xx = x.clone().requires_grad_(True)
-        assert moe._fused_mxfp8_applies(xx.view(-1, sh.dim)) == fuse
+        assert (moe._fused_core(xx.view(-1, sh.dim)) is not None) == fuse
         out = moe(xx)
         out.backward(gy)
         torch.cuda.synchronize()

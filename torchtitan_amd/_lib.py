@@ -60,6 +60,8 @@ SIGNATURES: dict[str, list] = {
     "moe_fp8_quant_tokens_t": [P, P, I64, I32, I32, I64, P, P, P],
     "moe_fp8_quant_tokens_t_amax": [P, P, P, I64, I32, I32, I64, P, P, P],
     "moe_fp8_quant_rows_groupamax": [P, P, I64, I32, I32, I32, P, P, P, P],
+    "moe_fp8_quant_rows_groupamax_gather": [P, I64, P, P, P, I64, I32, I32, P, P, P, P],
+    "moe_fp8_quant_tokens_t_amax_gather": [P, I64, P, P, P, P, I64, I32, I32, I64, P, P, P],
     "moe_fp8_gemm_gate_up": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "moe_fp8_gemm_down": [P, P, P, P, P, I64, I32, I32, I32, P, P],
     "moe_fp8_gemm_bwd_dgu": [P, P, P, P, P, P, P, I64, I32, I32, I32, P, P],

@@ -272,6 +272,26 @@ __global__ __launch_bounds__(256) void quant_rows_colamax_kernel(const uint16_t*
   for (int i = threadIdx.x; i < cpr * 8; i += blockDim.x) atomicMax(&col_amax[e * B + i], s_cm[i]);
 }
 
+// Rows gathered from another tensor (GATHER): row r of the operand is source row
+// idx[r] of src (row stride ld), times scale[r] rounded to bf16 when scale is
+// given (the expert permute x[token_idx] * score, read in place of its output).
+// Source rows outside [0, n_src) read as zeros.
+struct RowGather {
+  const uint16_t* src = nullptr;
+  const int64_t* idx = nullptr;
+  const float* scale = nullptr;
+  int64_t ld = 0, n_src = 0;
+};
+
+// v times s, rounded to bf16 (the permute's (x.float() * s).to(bf16))
+__device__ __forceinline__ uint4 scale_chunk(uint4 v, float s) {
+  float f[8];
+  Chunk<uint16_t>::unpack(v, f);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) f[k] = f[k] * s;
+  return Chunk<uint16_t>::pack(f);
+}
+
 // x [R][C] with expert token groups (counts, consecutive in row order) quantized
 // as quant_rows_kernel does with rows of K = C / P columns (piece p of row r
 // scaled by scale[r P + p]), with the column amax of every (group, column) on the
@@ -282,12 +302,13 @@ __global__ __launch_bounds__(256) void quant_rows_colamax_kernel(const uint16_t*
 // per-lane running column maxima (|x|, NaN ignored as fmaxf does), merged in LDS
 // and sent with one atomic max per column when the block leaves the group. Rows
 // past the last group are quantized row-wise only.
-template <int CPL, int P>
+template <int CPL, int P, bool GATHER = false>
 __global__ __launch_bounds__(256) void quant_rows_groupamax_kernel(const uint16_t* __restrict__ x,
                                                                    const int64_t* __restrict__ counts, int64_t R,
                                                                    int E, int C, int RB, uint8_t* __restrict__ q,
                                                                    float* __restrict__ scale,
-                                                                   uint32_t* __restrict__ group_amax) {
+                                                                   uint32_t* __restrict__ group_amax,
+                                                                   RowGather gather) {
   __shared__ uint32_t s_cm[64 * CPL * 8];
   __shared__ int64_t s_end[kMaxE + 1];  // s_end[e]: end row of group e; s_end[E] = R
   __shared__ int s_tmp[8];
@@ -328,6 +349,14 @@ __global__ __launch_bounds__(256) void quant_rows_groupamax_kernel(const uint16_
       for (int k = 0; k < 8; ++k) cm[i][k] = 0.f;
     for (int64_t r = a + wv; r < b; r += 4) {
       const uint16_t* xr = x + r * C;
+      bool valid = true;
+      float rs = 1.f;
+      if constexpr (GATHER) {
+        const int64_t j = gather.idx[r];
+        valid = j >= 0 && j < gather.n_src;
+        xr = gather.src + (valid ? j : 0) * gather.ld;
+        if (gather.scale) rs = gather.scale[r];
+      }
       uint4 v[CPL];
       float am[P];
 #pragma unroll
@@ -337,6 +366,10 @@ __global__ __launch_bounds__(256) void quant_rows_groupamax_kernel(const uint16_
       for (int i = 0; i < CPL; ++i) {
         const int c = lane + 64 * i;
         v[i] = c < cpr ? *(const uint4*)(xr + c * 8) : make_uint4(0, 0, 0, 0);
+        if constexpr (GATHER) {
+          if (!valid) v[i] = make_uint4(0, 0, 0, 0);
+          else if (gather.scale) v[i] = scale_chunk(v[i], rs);
+        }
         const float a8 = amax8(v[i]);
         if (P == 1 || c < kc) am[0] = fmaxf(am[0], a8);
         else am[P - 1] = fmaxf(am[P - 1], a8);
@@ -438,19 +471,9 @@ constexpr int kTRows = 128;  // slab rows transposed per pass
 // loads two passes ahead are issued as soon as the tile is in LDS. 128-column
 // slabs (launched whenever the width allows) write the row-wise layout in whole
 // 128-byte lines: 2-12 % faster than 64-column ones at the Kimi shapes.
-// Rows gathered from another tensor (GATHER): slab row r is source row idx[r] of
-// src (row stride ld), times scale[r] rounded to bf16 when scale is given (the
-// expert permute x[token_idx] * score, read in place of its output). Source rows
-// outside [0, n_src) read as zeros. The indices are loaded two passes ahead of
-// the rows they address and the scale is applied when a pass is consumed, so
-// neither waits behind the row loads in flight (vector loads complete in order).
-struct RowGather {
-  const uint16_t* src = nullptr;
-  const int64_t* idx = nullptr;
-  const float* scale = nullptr;
-  int64_t ld = 0, n_src = 0;
-};
-
+// GATHER: the slab's rows are gathered (RowGather); the indices are loaded two
+// passes ahead of the rows they address and the scale is applied when a pass is
+// consumed, so neither waits behind the row loads in flight.
 template <bool MX, bool ROWS, int COLS, bool GATHER = false>
 __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, int64_t ld, int n_rows, int n_out,
                                              uint8_t* __restrict__ out, int64_t ldo, uint8_t* __restrict__ sc,
@@ -512,11 +535,7 @@ __device__ __forceinline__ void slab_t_quant(const uint16_t* __restrict__ base, 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if (!in_rows(a0 + (t + i * T) / CPR)) continue;
-        float f[8];
-        Chunk<uint16_t>::unpack(v[i], f);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) f[k] = f[k] * sv[i];
-        v[i] = Chunk<uint16_t>::pack(f);
+        v[i] = scale_chunk(v[i], sv[i]);
       }
     }
   };
@@ -660,11 +679,11 @@ __global__ __launch_bounds__(4 * COLS) void quant_cols_t_kernel(const uint16_t* 
 // Block per (e, COLS columns); empty groups exit. With amax_in (the column amax
 // [E][C] of every group already known, from quant_rows_groupamax_kernel) the
 // amax pass is skipped and x is read once.
-template <int COLS>
+template <int COLS, bool GATHER = false>
 __global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t* __restrict__ x, const int64_t* __restrict__ counts,
                                                              int64_t R, int E, int C, int64_t Rpad,
                                                              uint8_t* __restrict__ q, float* __restrict__ scale,
-                                                             const float* __restrict__ amax_in) {
+                                                             const float* __restrict__ amax_in, RowGather gather) {
   __shared__ float s_red[COLS * 33];
   __shared__ float s_amax[COLS];
   __shared__ __attribute__((aligned(16))) uint32_t s_tile[kTRows * (COLS / 2)];
@@ -696,8 +715,13 @@ __global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t
   if ((int64_t)seg0 + n > R) n = (int)(R - seg0 > 0 ? R - seg0 : 0);
   const int n_out = (n + kPad - 1) / kPad * kPad;
   if (n == 0 || (int64_t)pstart + n_out > Rpad) return;
-  const uint16_t* base = x + (int64_t)seg0 * C + c0;
-  if (amax_in) {
+  const uint16_t* base = GATHER ? nullptr : x + (int64_t)seg0 * C + c0;
+  if constexpr (GATHER) {  // this slab's rows and columns of the gathered source
+    gather.src += c0;
+    gather.idx += seg0;
+    if (gather.scale) gather.scale += seg0;
+  }
+  if (GATHER || amax_in) {  // a gathered operand comes with its amax
     if (threadIdx.x < COLS) s_amax[threadIdx.x] = amax_in[(int64_t)e * C + c0 + threadIdx.x];
     __syncthreads();
   } else {
@@ -709,8 +733,8 @@ __global__ __launch_bounds__(4 * COLS) void quant_tokens_t_kernel(const uint16_t
     scale[(int64_t)e * C + c0 + threadIdx.x] = s;
   }
   __syncthreads();
-  slab_t_quant<false, false, COLS>(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, nullptr, 0, 0, s_amax,
-                                   s_tile, nullptr, 0, nullptr, 0, RowGather{}, pstart % 128);
+  slab_t_quant<false, false, COLS, GATHER>(base, C, n, n_out, q + (int64_t)c0 * Rpad + pstart, Rpad, nullptr, 0, 0,
+                                           s_amax, s_tile, nullptr, 0, nullptr, 0, gather, pstart % 128);
 }
 
 // ---------------------------------------------------------------------------
@@ -1557,16 +1581,21 @@ MOE_API int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int
 
 static int quant_tokens_t(const uint16_t* x, const float* group_amax, const int64_t* counts, int64_t n_rows,
                           int32_t n_experts, int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
-                          hipStream_t stream) {
+                          hipStream_t stream, RowGather gather = RowGather{}) {
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || cols < 64 || cols % 64) return kErrInvalidArgument;
   if (padded_rows < moe_fp8_padded_rows(n_rows, n_experts) || padded_rows % kPad) return kErrWorkspace;
   if (!x || !counts || !q || !scale) return kErrInvalidArgument;
+  const bool g = gather.idx != nullptr;
+  using kernel_t = void (*)(const uint16_t*, const int64_t*, int64_t, int, int, int64_t, uint8_t*, float*,
+                            const float*, RowGather);
+  const kernel_t k128 = g ? quant_tokens_t_kernel<128, true> : quant_tokens_t_kernel<128, false>;
+  const kernel_t k64 = g ? quant_tokens_t_kernel<64, true> : quant_tokens_t_kernel<64, false>;
   if (cols % 128 == 0)
-    hipLaunchKernelGGL(quant_tokens_t_kernel<128>, dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x, counts,
-                       n_rows, n_experts, cols, padded_rows, q, scale, group_amax);
+    hipLaunchKernelGGL(k128, dim3(n_experts * (cols / 128)), dim3(512), 0, stream, x, counts, n_rows, n_experts, cols,
+                       padded_rows, q, scale, group_amax, gather);
   else
-    hipLaunchKernelGGL(quant_tokens_t_kernel<64>, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts,
-                       n_rows, n_experts, cols, padded_rows, q, scale, group_amax);
+    hipLaunchKernelGGL(k64, dim3(n_experts * (cols / 64)), dim3(256), 0, stream, x, counts, n_rows, n_experts, cols,
+                       padded_rows, q, scale, group_amax, gather);
   return launch_status();
 }
 
@@ -1583,29 +1612,30 @@ MOE_API int moe_fp8_quant_tokens_t_amax(const uint16_t* x, const float* group_am
   return quant_tokens_t(x, group_amax, counts, n_rows, n_experts, cols, padded_rows, q, scale, stream);
 }
 
-template <int P>
+template <int P, bool G>
 static void launch_rows_groupamax(int chunks, dim3 grid, hipStream_t stream, const uint16_t* x, const int64_t* counts,
-                                  int64_t rows, int e, int cols, int rb, uint8_t* q, float* scale, uint32_t* gam) {
+                                  int64_t rows, int e, int cols, int rb, uint8_t* q, float* scale, uint32_t* gam,
+                                  RowGather gather) {
   if (chunks <= 64 * 2)
-    hipLaunchKernelGGL((quant_rows_groupamax_kernel<2, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
-                       q, scale, gam);
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<2, P, G>), grid, dim3(256), 0, stream, x, counts, rows, e, cols,
+                       rb, q, scale, gam, gather);
   else if (chunks <= 64 * 4)
-    hipLaunchKernelGGL((quant_rows_groupamax_kernel<4, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
-                       q, scale, gam);
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<4, P, G>), grid, dim3(256), 0, stream, x, counts, rows, e, cols,
+                       rb, q, scale, gam, gather);
   else if (chunks <= 64 * 5)
-    hipLaunchKernelGGL((quant_rows_groupamax_kernel<5, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
-                       q, scale, gam);
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<5, P, G>), grid, dim3(256), 0, stream, x, counts, rows, e, cols,
+                       rb, q, scale, gam, gather);
   else if (chunks <= 64 * 8)
-    hipLaunchKernelGGL((quant_rows_groupamax_kernel<8, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
-                       q, scale, gam);
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<8, P, G>), grid, dim3(256), 0, stream, x, counts, rows, e, cols,
+                       rb, q, scale, gam, gather);
   else
-    hipLaunchKernelGGL((quant_rows_groupamax_kernel<16, P>), grid, dim3(256), 0, stream, x, counts, rows, e, cols, rb,
-                       q, scale, gam);
+    hipLaunchKernelGGL((quant_rows_groupamax_kernel<16, P, G>), grid, dim3(256), 0, stream, x, counts, rows, e, cols,
+                       rb, q, scale, gam, gather);
 }
 
-MOE_API int moe_fp8_quant_rows_groupamax(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
-                                         int32_t cols, int32_t pieces, uint8_t* q, float* scale, float* group_amax,
-                                         hipStream_t stream) {
+static int rows_groupamax(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                          int32_t cols, int32_t pieces, uint8_t* q, float* scale, float* group_amax,
+                          hipStream_t stream, RowGather gather = RowGather{}) {
   if (n_rows < 0 || n_experts < 1 || n_experts > kMaxE || (pieces != 1 && pieces != 2)) return kErrInvalidArgument;
   if (cols < 8 * pieces || cols % (8 * pieces) || cols > 8192) return kErrInvalidArgument;
   if (n_rows >= (int64_t)INT32_MAX / 2) return kErrUnsupportedShape;
@@ -1618,11 +1648,55 @@ MOE_API int moe_fp8_quant_rows_groupamax(const uint16_t* x, const int64_t* count
   if (rb < 16) rb = 16;
   const dim3 grid((unsigned)((n_rows + rb - 1) / rb));
   uint32_t* gam = (uint32_t*)group_amax;
-  if (pieces == 1)
-    launch_rows_groupamax<1>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale, gam);
+  if (gather.idx)
+    launch_rows_groupamax<1, true>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale, gam,
+                                   gather);
+  else if (pieces == 1)
+    launch_rows_groupamax<1, false>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale,
+                                    gam, gather);
   else
-    launch_rows_groupamax<2>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale, gam);
+    launch_rows_groupamax<2, false>(cols / 8, grid, stream, x, counts, n_rows, n_experts, cols, (int)rb, q, scale,
+                                    gam, gather);
   return launch_status();
+}
+
+MOE_API int moe_fp8_quant_rows_groupamax(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                         int32_t cols, int32_t pieces, uint8_t* q, float* scale, float* group_amax,
+                                         hipStream_t stream) {
+  return rows_groupamax(x, counts, n_rows, n_experts, cols, pieces, q, scale, group_amax, stream);
+}
+
+static int row_gather(RowGather& g, const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                      const float* row_scale, int32_t cols) {
+  if (n_src < 1 || !token_idx || reinterpret_cast<uintptr_t>(src) % 16) return kErrInvalidArgument;
+  g.src = src;
+  g.idx = token_idx;
+  g.scale = row_scale;
+  g.ld = cols;
+  g.n_src = n_src;
+  return kOk;
+}
+
+MOE_API int moe_fp8_quant_rows_groupamax_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                                                const float* row_scale, const int64_t* counts, int64_t n_rows,
+                                                int32_t n_experts, int32_t cols, uint8_t* q, float* scale,
+                                                float* group_amax, hipStream_t stream) {
+  RowGather g;
+  const int st = row_gather(g, src, n_src, token_idx, row_scale, cols);
+  if (st) return st;
+  return rows_groupamax(src, counts, n_rows, n_experts, cols, 1, q, scale, group_amax, stream, g);
+}
+
+MOE_API int moe_fp8_quant_tokens_t_amax_gather(const uint16_t* src, int64_t n_src, const int64_t* token_idx,
+                                               const float* row_scale, const float* group_amax,
+                                               const int64_t* counts, int64_t n_rows, int32_t n_experts,
+                                               int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
+                                               hipStream_t stream) {
+  if (!group_amax) return kErrInvalidArgument;
+  RowGather g;
+  const int st = row_gather(g, src, n_src, token_idx, row_scale, cols);
+  if (st) return st;
+  return quant_tokens_t(src, group_amax, counts, n_rows, n_experts, cols, padded_rows, q, scale, stream, g);
 }
 
 static int fp8_params(Params& p, const int64_t* counts, int64_t n_rows, int32_t n_experts, int32_t dim,
@@ -1823,13 +1897,9 @@ MOE_API int moe_mxfp8_quant_dual_tokens_gather(const uint16_t* src, int64_t n_sr
                                                int32_t n_experts, int32_t cols, int64_t padded_rows,
                                                uint8_t* q_rows, uint8_t* scale_rows, uint8_t* q, uint8_t* scale,
                                                hipStream_t stream) {
-  if (n_src < 1 || !token_idx || reinterpret_cast<uintptr_t>(src) % 16) return kErrInvalidArgument;
   RowGather g;
-  g.src = src;
-  g.idx = token_idx;
-  g.scale = row_scale;
-  g.ld = cols;
-  g.n_src = n_src;
+  const int st = row_gather(g, src, n_src, token_idx, row_scale, cols);
+  if (st) return st;
   return mx_dual_tokens(src, g, counts, n_rows, n_experts, cols, padded_rows, q_rows, scale_rows, q, scale, stream);
 }
 

@@ -388,13 +388,15 @@ class MoE(Module):
         layout = self.reorderer(top_scores, selected_experts_indices)
         top_scores_experts_sorted, _token_indices_experts_sorted, num_tokens_per_expert = layout
 
-        if self._fused_mxfp8_applies(x):
-            # MXFP8 experts with the score applied before them: the permute runs inside
-            # the experts' token quantizer and the combine's gather inside their
-            # backward (ops.moe_core_mxfp8), with the same results as the three ops
+        core = self._fused_core(x)
+        if core is not None:
+            # fp8 or MXFP8 experts with the score applied before them: the permute runs
+            # inside the experts' token quantizers and the combine's gather inside their
+            # backward (ops.moe_core_fp8 / moe_core_mxfp8), with the same results as the
+            # three ops
             shared = self.shared_experts(x) if self.shared_experts is not None else None
             experts = self.experts
-            out = ops.moe_core_mxfp8(
+            out = core(
                 x, shared, _token_indices_experts_sorted, top_scores_experts_sorted, layout.slot_pos,
                 layout.tok_pos, _local(experts.w1), _local(experts.w2), _local(experts.w3), num_tokens_per_expert,
             )[0]
@@ -417,15 +419,30 @@ class MoE(Module):
         )
         return out.reshape(bs, slen, dim)
 
-    # set False to run MXFP8 experts through the separate permute, experts and combine ops
-    fuse_mxfp8_permute = True
+    # set False to run fp8 and MXFP8 experts through the separate permute, experts and
+    # combine ops. fp8 experts take the fused op only with fuse_fp8_permute as well:
+    # their routed x and dy are each read twice (row and token-transposed
+    # quantizations), and gathered twice that measured 0.6 % slower at 32K Kimi
+    # tokens than one permuted copy read twice (MXFP8 reads each once, both layouts
+    # from one pass, and gains 2 %)
+    fuse_permute_into_quantizers = True
+    fuse_fp8_permute = False
 
-    def _fused_mxfp8_applies(self, x: torch.Tensor) -> bool:
+    def _fused_core(self, x: torch.Tensor):
+        """The fused op for this layer's experts, or None where the separate ops run."""
         experts = self.experts
-        if not (self.fuse_mxfp8_permute and type(experts) is GroupedExperts and experts.mxfp8
-                and self.score_before_experts and x.is_cuda and x.dtype == torch.bfloat16):
-            return False
-        return all(_local(w).dtype == torch.bfloat16 for w in (experts.w1, experts.w2, experts.w3))
+        if not (self.fuse_permute_into_quantizers and type(experts) is GroupedExperts
+                and (experts.mxfp8 or experts.float8) and self.score_before_experts and x.is_cuda
+                and x.dtype == torch.bfloat16):
+            return None
+        if not all(_local(w).dtype == torch.bfloat16 for w in (experts.w1, experts.w2, experts.w3)):
+            return None
+        if experts.mxfp8:
+            return ops.moe_core_mxfp8
+        # the fp8 row quantizer keeps a row in registers to take the group amax beside it
+        if self.fuse_fp8_permute and x.shape[-1] <= ops.AMAX_SIDE_MAX_COLS:
+            return ops.moe_core_fp8
+        return None
 
     def _init_self_buffers(self, *, buffer_device: torch.device | None = None) -> None:
         assert isinstance(buffer_device, torch.device)

@@ -810,22 +810,31 @@ def grouped_swiglu_fp8(
             raise TypeError(f"grouped_swiglu_fp8 expects bfloat16 {name}, got {t.dtype}")
     x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
     counts = num_tokens_per_expert.to(torch.int64).contiguous()
-    r, d = x.shape
+    qx, sx, amx = _quant_rows_groupamax(x, counts, w1.shape[0])
+    y, g, u, h, am1, am3, am2, amh = _fp8_experts_forward(qx, sx, w1, w2, w3, counts)
+    return y, g, u, h, am1, am3, am2, amx, amh
+
+
+def _fp8_experts_forward(qx: Tensor, sx: Tensor, w1: Tensor, w2: Tensor, w3: Tensor,
+                         counts: Tensor) -> tuple[Tensor, ...]:
+    """grouped_swiglu_fp8 from the row-quantized routed rows (qx, sx): the weights'
+    quantizations, gate_up, h's quantization, down. Returns (y, g, u, h, amax_w1,
+    amax_w3, amax_w2, amax_h)."""
+    r, d = qx.shape
     e, h_dim, _ = w1.shape
-    s = stream_of(x)
-    qx, sx, amx = _quant_rows_groupamax(x, counts, e)
+    s = stream_of(w1)
     qw1, sw1, am1 = _quant_rows_colamax(w1)
     qw3, sw3, am3 = _quant_rows_colamax(w3)
     qw2, sw2, am2 = _quant_rows_colamax(w2)
-    g = x.new_empty(r, h_dim)
-    u = x.new_empty(r, h_dim)
-    h = x.new_empty(r, h_dim)
-    y = x.new_empty(r, d)
+    g = w1.new_empty(r, h_dim)
+    u = w1.new_empty(r, h_dim)
+    h = w1.new_empty(r, h_dim)
+    y = w1.new_empty(r, d)
     call("moe_fp8_gemm_gate_up", ptr(qx), ptr(sx), ptr(qw1), ptr(sw1), ptr(qw3), ptr(sw3), ptr(counts), r, e, d,
          h_dim, ptr(g), ptr(u), ptr(h), s)
     qh, sh, amh = _quant_rows_groupamax(h, counts, e)
     call("moe_fp8_gemm_down", ptr(qh), ptr(sh), ptr(qw2), ptr(sw2), ptr(counts), r, e, d, h_dim, ptr(y), s)
-    return y, g, u, h, am1, am3, am2, amx, amh
+    return y, g, u, h, am1, am3, am2, amh
 
 
 @grouped_swiglu_fp8.register_fake
@@ -849,17 +858,31 @@ def grouped_swiglu_fp8_backward(
     quantizers take their own)."""
     require_gpu(dy, x, w1, w2, w3, num_tokens_per_expert, g, u, h)
     dy = dy.to(torch.bfloat16).contiguous()
+    x = x.contiguous()
     counts = num_tokens_per_expert.to(torch.int64).contiguous()
-    r, d = x.shape
-    e, h_dim, _ = w1.shape
-    dev = x.device
-    s = stream_of(x)
-    # dh = dy . w2 (contraction over D): dy per row, w2 per (e, h) column over D
+    e = w1.shape[0]
     qdy, sdy, amdy = _quant_rows_groupamax(dy, counts, e)
+    return _fp8_experts_backward(
+        qdy, sdy, w1, w2, w3, counts, g, u, h, amax_w1, amax_w3, amax_w2, amax_h,
+        lambda rpad: _quant_tokens_t(x, counts, e, rpad, amax_x),
+        lambda rpad: _quant_tokens_t(dy, counts, e, rpad, amdy))
+
+
+def _fp8_experts_backward(qdy: Tensor, sdy: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, counts: Tensor, g: Tensor,
+                          u: Tensor, h: Tensor, amax_w1: Tensor, amax_w3: Tensor, amax_w2: Tensor, amax_h: Tensor,
+                          x_tokens_t, dy_tokens_t) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """grouped_swiglu_fp8_backward from the row-quantized output gradient (qdy,
+    sdy); x_tokens_t(rpad) and dy_tokens_t(rpad) give the token-transposed layouts
+    of the routed x and dy. Returns (dx, dw1, dw2, dw3)."""
+    r, d = qdy.shape
+    e, h_dim, _ = w1.shape
+    dev = w1.device
+    s = stream_of(w1)
+    # dh = dy . w2 (contraction over D): dy per row, w2 per (e, h) column over D
     qw2t = torch.empty(e, h_dim, d, dtype=FP8, device=dev)
     sw2t = torch.empty(e, h_dim, dtype=torch.float32, device=dev)
     _quant_cols_t(w2.contiguous(), amax_w2.contiguous(), qw2t, 0, h_dim * d, d, sw2t, 0, h_dim)
-    dgu = x.new_empty(r, 2 * h_dim)
+    dgu = w1.new_empty(r, 2 * h_dim)
     call("moe_fp8_gemm_bwd_dgu", ptr(qdy), ptr(sdy), ptr(qw2t), ptr(sw2t), ptr(g), ptr(u), ptr(counts), r, e, d,
          h_dim, ptr(dgu), s)
     # dx = dg . w1 + du . w3 (contraction over H): one scale per dg / du row half,
@@ -869,18 +892,18 @@ def grouped_swiglu_fp8_backward(
     sw13t = torch.empty(e, 2, d, dtype=torch.float32, device=dev)
     _quant_cols_t(w1.contiguous(), amax_w1.contiguous(), qw13t, 0, d * 2 * h_dim, 2 * h_dim, sw13t, 0, 2 * d)
     _quant_cols_t(w3.contiguous(), amax_w3.contiguous(), qw13t, h_dim, d * 2 * h_dim, 2 * h_dim, sw13t, d, 2 * d)
-    dx = x.new_empty(r, d)
+    dx = w1.new_empty(r, d)
     call("moe_fp8_gemm_bwd_dx", ptr(qdgu), ptr(sdgu), ptr(qw13t), ptr(sw13t), ptr(counts), r, e, d, h_dim,
          ptr(dx), s)
     # weight gradients: contraction over each expert's tokens (per-group scales)
     rpad = _padded_rows(r, e)
     qdgut, sdgut = _quant_tokens_t(dgu, counts, e, rpad, amdgu)
-    qxt, sxt = _quant_tokens_t(x, counts, e, rpad, amax_x)
+    qxt, sxt = x_tokens_t(rpad)
     dw1 = torch.empty_like(w1)
     dw3 = torch.empty_like(w3)
     call("moe_fp8_gemm_bwd_dw13", ptr(qdgut), ptr(sdgut), ptr(qxt), ptr(sxt), ptr(counts), r, rpad, e, d, h_dim,
          ptr(dw1), ptr(dw3), s)
-    qdyt, sdyt = _quant_tokens_t(dy, counts, e, rpad, amdy)
+    qdyt, sdyt = dy_tokens_t(rpad)
     qht, sht = _quant_tokens_t(h, counts, e, rpad, amax_h)
     dw2 = torch.empty_like(w2)
     call("moe_fp8_gemm_bwd_dw2", ptr(qdyt), ptr(sdyt), ptr(qht), ptr(sht), ptr(counts), r, rpad, e, d, h_dim,
@@ -1121,6 +1144,130 @@ grouped_swiglu_mxfp8.register_autograd(_gsmx_bwd, setup_context=_gsmx_setup)
 
 
 # ---------------------------------------------------------------------------
+# the routed half of MoE.forward with fp8 experts and the score applied before
+# them, the permute folded into the token quantizers
+# ---------------------------------------------------------------------------
+def _aligned(src: Tensor) -> Tensor:
+    return src.clone() if src.data_ptr() % 16 else src  # the gathering kernels read rows in 16-byte pieces
+
+
+def _quant_rows_groupamax_gather(src: Tensor, token_idx: Tensor, row_scale: Tensor | None, counts: Tensor,
+                                 e: int) -> tuple[Tensor, Tensor, Tensor]:
+    """_quant_rows_groupamax of the routed rows src[token_idx] (* row_scale, rounded
+    to bf16), read from src [N, C] in place."""
+    src = _aligned(src)
+    r, c = token_idx.shape[0], src.shape[1]
+    q = torch.empty(r, c, dtype=FP8, device=src.device)
+    sc = torch.empty(r, dtype=torch.float32, device=src.device)
+    amax = torch.zeros(e, c, dtype=torch.float32, device=src.device)
+    call("moe_fp8_quant_rows_groupamax_gather", ptr(src), src.shape[0], ptr(token_idx), ptr(row_scale), ptr(counts),
+         r, e, c, ptr(q), ptr(sc), ptr(amax), stream_of(src))
+    return q, sc, amax
+
+
+def _quant_tokens_t_gather(src: Tensor, token_idx: Tensor, row_scale: Tensor | None, counts: Tensor, e: int,
+                           rpad: int, amax: Tensor) -> tuple[Tensor, Tensor]:
+    """_quant_tokens_t (from the groups' known amax) of the routed rows
+    src[token_idx] (* row_scale, rounded to bf16), read from src in place."""
+    src = _aligned(src)
+    r, c = token_idx.shape[0], src.shape[1]
+    q = torch.empty(c, rpad, dtype=FP8, device=src.device)
+    sc = torch.empty(e, c, dtype=torch.float32, device=src.device)
+    call("moe_fp8_quant_tokens_t_amax_gather", ptr(src), src.shape[0], ptr(token_idx), ptr(row_scale), ptr(amax),
+         ptr(counts), r, e, c, rpad, ptr(q), ptr(sc), stream_of(src))
+    return q, sc
+
+
+@torch.library.custom_op("moe_mi355x::moe_core_fp8", mutates_args=())
+def moe_core_fp8(
+    x: Tensor, shared_out: Tensor | None, token_idx: Tensor, scores_sorted: Tensor, slot_pos: Tensor,
+    tok_pos: Tensor, w1: Tensor, w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """out = combine(shared_out, experts(x[token_idx] * score)) with fp8 experts
+    (moe.py:440-470 with score_before_experts; the ops of permute,
+    grouped_swiglu_fp8 and combine): the routed rows are quantized straight from x
+    (moe_fp8_quant_rows_groupamax_gather), so no routed copy of x is written, and
+    in the backward the routed gradient and the routed x are quantized straight
+    from the output's gradient and from x. Returns (out, g, u, h, then the column
+    amax of w1, w3, w2, of the routed x and of h per token group)."""
+    require_gpu(x, shared_out, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, num_tokens_per_expert)
+    _check_bf16("moe_core_fp8", x=x, w1=w1, w2=w2, w3=w3)
+    x, w1, w2, w3 = x.contiguous(), w1.contiguous(), w2.contiguous(), w3.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    tidx = token_idx.to(torch.int64).contiguous()
+    sc = scores_sorted.float().contiguous()
+    qx, sx, amx = _quant_rows_groupamax_gather(x, tidx, sc, counts, w1.shape[0])
+    y, g, u, h, am1, am3, am2, amh = _fp8_experts_forward(qx, sx, w1, w2, w3, counts)
+    out = combine(shared_out, y, slot_pos, tok_pos, None)
+    return out, g, u, h, am1, am3, am2, amx, amh
+
+
+@moe_core_fp8.register_fake
+def _(x, shared_out, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, num_tokens_per_expert):
+    n, d = x.shape
+    r = token_idx.shape[0]
+    e, h_dim, _ = w1.shape
+    f32 = lambda *shape: x.new_empty(*shape, dtype=torch.float32)  # noqa: E731
+    return (x.new_empty(n, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim),
+            f32(*_amax_shape(e, d)), f32(*_amax_shape(e, d)), f32(*_amax_shape(e, h_dim)), f32(e, d),
+            f32(*_amax_shape(e, h_dim)))
+
+
+@torch.library.custom_op("moe_mi355x::moe_core_fp8_backward", mutates_args=())
+def moe_core_fp8_backward(
+    grad_out: Tensor, x: Tensor, token_idx: Tensor, scores_sorted: Tensor, tok_pos: Tensor, w1: Tensor,
+    w2: Tensor, w3: Tensor, num_tokens_per_expert: Tensor, g: Tensor, u: Tensor, h: Tensor, amax_w1: Tensor,
+    amax_w3: Tensor, amax_w2: Tensor, amax_x: Tensor, amax_h: Tensor,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(grad_x, grad_scores_sorted, dw1, dw2, dw3) of moe_core_fp8's out; the
+    shared output's gradient is grad_out itself (the combine adds it once)."""
+    require_gpu(grad_out, x, token_idx, scores_sorted, tok_pos, w1, w2, w3, num_tokens_per_expert, g, u, h)
+    go = grad_out.to(torch.bfloat16).contiguous()
+    x = x.contiguous()
+    counts = num_tokens_per_expert.to(torch.int64).contiguous()
+    tidx = token_idx.to(torch.int64).contiguous()
+    sc = scores_sorted.float().contiguous()
+    e = w1.shape[0]
+    qdy, sdy, amdy = _quant_rows_groupamax_gather(go, tidx, None, counts, e)
+    dx_routed, dw1, dw2, dw3 = _fp8_experts_backward(
+        qdy, sdy, w1, w2, w3, counts, g, u, h, amax_w1, amax_w3, amax_w2, amax_h,
+        lambda rpad: _quant_tokens_t_gather(x, tidx, sc, counts, e, rpad, amax_x),
+        lambda rpad: _quant_tokens_t_gather(go, tidx, None, counts, e, rpad, amdy))
+    grad_x, grad_s = permute_backward(dx_routed, x, tok_pos, scores_sorted, PERMUTE_BWD_ROUND_EACH)
+    return grad_x, grad_s, dw1, dw2, dw3
+
+
+@moe_core_fp8_backward.register_fake
+def _(grad_out, x, token_idx, scores_sorted, tok_pos, w1, w2, w3, num_tokens_per_expert, *saved):
+    r = token_idx.shape[0]
+    return (x.new_empty(x.shape), x.new_empty(r, dtype=torch.float32), torch.empty_like(w1), torch.empty_like(w2),
+            torch.empty_like(w3))
+
+
+def _core_fp8_setup(ctx, inputs, output):
+    x, shared_out, token_idx, scores_sorted, _slot_pos, tok_pos, w1, w2, w3, counts = inputs
+    _out, g, u, h, *amax = output
+    ctx.save_for_backward(x, token_idx, scores_sorted, tok_pos, w1, w2, w3, counts, g, u, h, *amax)
+    ctx.has_shared = shared_out is not None
+    ctx.shared_dtype = shared_out.dtype if shared_out is not None else None
+    ctx.mark_non_differentiable(g, u, h, *amax)
+    ctx.set_materialize_grads(False)
+
+
+def _core_fp8_bwd(ctx, grad_out, *_unused):
+    if grad_out is None:
+        return (None,) * 10
+    x, token_idx, scores_sorted, tok_pos, w1, w2, w3, counts, g, u, h, *amax = ctx.saved_tensors
+    grad_x, grad_s, dw1, dw2, dw3 = moe_core_fp8_backward(grad_out, x, token_idx, scores_sorted, tok_pos, w1, w2,
+                                                          w3, counts, g, u, h, *amax)
+    grad_shared = grad_out.to(ctx.shared_dtype) if ctx.has_shared else None
+    return grad_x, grad_shared, None, grad_s, None, None, dw1, dw2, dw3, None
+
+
+moe_core_fp8.register_autograd(_core_fp8_bwd, setup_context=_core_fp8_setup)
+
+
+# ---------------------------------------------------------------------------
 # the routed half of MoE.forward with MXFP8 experts and the score applied before
 # them, the permute folded into the token quantizer
 # ---------------------------------------------------------------------------
@@ -1128,8 +1275,7 @@ def _mx_dual_tokens_gather(src: Tensor, token_idx: Tensor, row_scale: Tensor | N
                            rpad: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """_mx_dual_tokens of the routed rows src[token_idx] (* row_scale, rounded to
     bf16), read from src [N, C] in place."""
-    if src.data_ptr() % 16:  # the kernel reads rows in 16-byte pieces
-        src = src.clone()
+    src = _aligned(src)
     r = token_idx.shape[0]
     c = src.shape[1]
     qr = torch.empty(r, c, dtype=FP8, device=src.device)
