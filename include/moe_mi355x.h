@@ -313,13 +313,11 @@ int moe_grouped_col_sum(const uint16_t* src, int64_t ld_src, const int64_t* coun
  * fp8 tensors are uint8_t*.
  * ------------------------------------------------------------------------- */
 
-/* Rows of the token-transposed fp8 tensors: n_rows + n_experts * 15 (every
- * group starts at a multiple of 16); round it up to a multiple of 16. Rounded up
- * to a multiple of 128 (with 128-byte aligned tensors), every row of those
- * tensors starts on a 128-byte line, and the transposing quantizers and the
- * weight-gradient GEMMs read and write whole lines (each starts its passes and
- * k-steps at the group's offset rounded down to 128 bytes, the bytes before the
- * group masked). */
+/* Rows of the token-transposed fp8 tensors: n_rows + n_experts * 127 (every
+ * group starts at a multiple of 128); round it up to a multiple of 128. With
+ * 128-byte aligned tensors every row of those tensors, and every group in it,
+ * starts on a 128-byte line, so the transposing quantizers and the weight-gradient
+ * GEMMs read and write whole lines, with no partly empty first pass or k-step. */
 int64_t moe_fp8_padded_rows(int64_t n_rows, int32_t n_experts);
 
 /* x [rows, cols] bf16 -> q [rows, cols] fp8, scale [rows] (one per row). */
@@ -349,8 +347,8 @@ int moe_fp8_quant_rows_colamax(const uint16_t* x, int32_t n_experts, int32_t a, 
                                float* scale, float* col_amax, moe_stream_t stream);
 
 /* x [n_rows, cols] bf16 in expert token groups (counts) -> q [cols, padded_rows]
- * fp8 with group e at the 16-aligned offset sum_{e'<e} ceil16(count_e') and
- * zero padding up to ceil16(count_e); scale [E, cols] over the group's tokens
+ * fp8 with group e at the 128-aligned offset sum_{e'<e} ceil128(count_e') and
+ * zero padding up to ceil128(count_e); scale [E, cols] over the group's tokens
  * (not written for empty groups). */
 int moe_fp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,
                            int32_t cols, int64_t padded_rows, uint8_t* q, float* scale,
@@ -435,9 +433,9 @@ int moe_fp8_gemm_bwd_dw2(const uint8_t* qdyt, const float* sdyt, const uint8_t* 
  * k-block major, [padded_rows / 32, cols].
  * ------------------------------------------------------------------------- */
 
-/* Rows of the token-transposed MXFP8 tensors: n_rows + n_experts * 31 rounded
- * up to a multiple of 32 (every group starts at a multiple of 32); a multiple of
- * 128 is faster, as for moe_fp8_padded_rows. */
+/* Rows of the token-transposed MXFP8 tensors: n_rows + n_experts * 127 rounded
+ * up to a multiple of 128 (every group starts at a multiple of 128, as for
+ * moe_fp8_padded_rows). */
 int64_t moe_mxfp8_padded_rows(int64_t n_rows, int32_t n_experts);
 
 /* x [rows, cols] bf16 (cols % 32 == 0) -> q [rows, cols], scale [rows, cols / 32]. */
@@ -453,7 +451,7 @@ int moe_mxfp8_quant_cols_t(const uint16_t* x, int32_t n_experts, int32_t a, int3
                            int64_t scale_expert_stride, int64_t scale_row_stride, moe_stream_t stream);
 
 /* x [n_rows, cols] bf16 in expert token groups -> q [cols, padded_rows] with
- * group e at the 32-aligned offset sum_{e'<e} ceil32(count_e') (zero padded),
+ * group e at the 128-aligned offset sum_{e'<e} ceil128(count_e') (zero padded),
  * quantized along the tokens in blocks of 32; scale [padded_rows / 32, cols]
  * (blocks of empty groups and past the groups are not written). */
 int moe_mxfp8_quant_tokens_t(const uint16_t* x, const int64_t* counts, int64_t n_rows, int32_t n_experts,

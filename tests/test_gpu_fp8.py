@@ -122,7 +122,7 @@ def test_fp8_gemm_entry_points_match_emulation(dev):
                 qs.append((qq, ss))
             else:
                 qs.append(None)
-            pstart += (n + 15) // 16 * 16
+            pstart += (n + 127) // 128 * 128
         return q, sc, qs
 
     qdgut, sdgut, ldgu = tokens_t(dgu)
@@ -182,11 +182,11 @@ def test_fp8_quantizers_bit_exact(dev):
         if n:
             rq, rs = R.quant_fp8_rows(xt[start:start + n].t())
             assert torch.equal(q2[:, pstart:pstart + n], rq.view(torch.uint8))
-            pad = (n + 15) // 16 * 16
+            pad = (n + 127) // 128 * 128
             assert torch.count_nonzero(q2[:, pstart + n:pstart + pad]) == 0
             assert torch.equal(s2[i], rs.view(-1))
         start += n
-        pstart += (n + 15) // 16 * 16
+        pstart += (n + 127) // 128 * 128
 
 
 
@@ -300,10 +300,10 @@ def test_fp8_token_quantizers_from_two_reads(dev, name):
         if n:
             rq, rs = R.quant_fp8_rows(x[start:start + n].t())
             assert torch.equal(qt[:, pstart:pstart + n], rq.view(torch.uint8)), f"group {i}"
-            assert torch.count_nonzero(qt[:, pstart + n:pstart + (n + 15) // 16 * 16]) == 0
+            assert torch.count_nonzero(qt[:, pstart + n:pstart + (n + 127) // 128 * 128]) == 0
             assert torch.equal(st[i], rs.view(-1))
         start += n
-        pstart += (n + 15) // 16 * 16
+        pstart += (n + 127) // 128 * 128
     # non-finite values: against the kernels that take their own amax
     x[5, 7] = float("inf")
     x[1, 2] = float("nan")
@@ -350,7 +350,7 @@ def test_fp8_transposing_quantizers_slab_widths(dev, width):
             assert torch.equal(q2[:, pstart:pstart + n], rq.view(torch.uint8))
             assert torch.equal(s2[i], rs.view(-1))
         start += n
-        pstart += (n + 15) // 16 * 16
+        pstart += (n + 127) // 128 * 128
 
 CASES = {
     "ragged_e8": (8, 256, 512, [37, 0, 130, 16, 255, 1, 64, 100]),
@@ -434,7 +434,7 @@ def test_fp8_quantizers_nan_elements(dev):
     rq0, _ = R.quant_fp8_rows(xt[0:100].t())
     rq2, _ = R.quant_fp8_rows(xt[100:256].t())
     assert torch.equal(q2[cols, 0:100], rq0.view(torch.uint8)[cols])
-    assert torch.equal(q2[:, 112:268], rq2.view(torch.uint8))
+    assert torch.equal(q2[:, 128:284], rq2.view(torch.uint8))  # group 2 at ceil128(100)
 
 
 @pytest.mark.parametrize("cols", [2304, 192])
@@ -462,7 +462,7 @@ def test_fp8_gathering_token_quantizers_match_permute_then_quantize(dev, cols, s
     rpad = ops._padded_rows(n * k, e)
     qt1, st1 = ops._quant_tokens_t(routed, counts, e, rpad, a1)
     qt2, st2 = ops._quant_tokens_t_gather(x, token_idx, sc, counts, e, rpad, a1)
-    used = (counts.cpu() + 15) // 16 * 16
+    used = (counts.cpu() + 127) // 128 * 128
     assert torch.equal(qt1[:, :int(used.sum())], qt2[:, :int(used.sum())])
     full = (counts > 0)
     assert torch.equal(st1[full], st2[full])

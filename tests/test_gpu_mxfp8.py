@@ -39,7 +39,7 @@ def _u8(q):
 
 
 def _tokens_t(t, segs, rpad):
-    """Oracle token-transposed layout: q [C, rpad] with 32-aligned zero-padded
+    """Oracle token-transposed layout: q [C, rpad] with 128-aligned zero-padded
     groups, scales [rpad / 32, C] k-block major (NaN where no group writes)."""
     c = t.shape[1]
     q = torch.zeros(c, rpad, dtype=torch.uint8)
@@ -47,14 +47,14 @@ def _tokens_t(t, segs, rpad):
     per, pstart = [], 0
     for s0, n in segs:
         if n:
-            qq, ss = R.quant_mxfp8(R._pad_tokens(t[s0:s0 + n].t()))
-            n32 = qq.shape[1]
-            q[:, pstart:pstart + n32] = qq.view(torch.uint8)
-            sc[pstart // 32:pstart // 32 + n32 // 32] = ss.t()
+            qq, ss = R.quant_mxfp8(R._pad_tokens(t[s0:s0 + n].t(), 128))
+            npad = qq.shape[1]
+            q[:, pstart:pstart + npad] = qq.view(torch.uint8)
+            sc[pstart // 32:pstart // 32 + npad // 32] = ss.t()
             per.append((qq, ss))
         else:
             per.append(None)
-        pstart += (n + 31) // 32 * 32
+        pstart += (n + 127) // 128 * 128
     return q, sc, per
 
 
@@ -93,12 +93,12 @@ def test_mxfp8_quantizers_bit_exact(dev):
     r, c = int(counts.sum()), 128
     xt = torch.randn(r, c, generator=g).bfloat16()
     rpad = ops._mx_padded_rows(r, len(counts))
-    assert rpad % 32 == 0 and rpad >= r + 31 * len(counts)
+    assert rpad % 128 == 0 and rpad >= r + 127 * len(counts)
     q2, s2 = ops._mx_quant_tokens_t(xt.to(dev), counts.to(dev), len(counts), rpad)
     q2, s2 = q2.cpu(), s2.cpu()
     segs = [(int(counts[:i].sum()), int(n)) for i, n in enumerate(counts)]
     rq2, rs2, _ = _tokens_t(xt, segs, rpad)
-    used = sum((n + 31) // 32 * 32 for _, n in segs)
+    used = sum((n + 127) // 128 * 128 for _, n in segs)
     assert torch.equal(q2[:, :used], rq2[:, :used])
     assert torch.equal(s2[:used // 32], rs2[:used // 32])
     # dual: one read, both layouts
@@ -152,7 +152,7 @@ def test_mxfp8_transposing_quantizers_slab_widths(dev, width):
     rpad = ops._mx_padded_rows(r, len(counts))
     segs = [(int(counts[:i].sum()), int(n)) for i, n in enumerate(counts)]
     rq2, rs2, _ = _tokens_t(xt, segs, rpad)
-    used = sum((n + 31) // 32 * 32 for _, n in segs)
+    used = sum((n + 127) // 128 * 128 for _, n in segs)
     q2, s2 = ops._mx_quant_tokens_t(xt.to(dev), counts.to(dev), len(counts), rpad)
     assert torch.equal(q2.cpu()[:, :used], rq2[:, :used]) and torch.equal(s2.cpu()[:used // 32], rs2[:used // 32])
     dqr, dsr, dqt, dst = ops._mx_dual_tokens(xt.to(dev), counts.to(dev), len(counts), rpad)
@@ -352,7 +352,7 @@ def test_mxfp8_quantizers_nan_elements(dev):
         ok = torch.ones(128, rpad // 32, dtype=torch.bool)  # (column, k-block) pairs without a NaN
         ok[5, 0] = False
         ok[70, (128 + 100) // 32] = False
-        used = (128 + 160) // 32
+        used = (128 + 256) // 32
         ok[:, used:] = False
         assert torch.equal(st_.t()[ok], rs2.t()[ok])
         el = ok.repeat_interleave(32, dim=1)

@@ -12,7 +12,7 @@
 //        [E, A, B] tensor, written transposed as [E, B, A];
 //      - moe_fp8_quant_tokens_t: per expert token group, one scale per column c
 //        of a [R, C] tensor, written transposed as [C, Rpad] with every group
-//        starting at a multiple of 16 tokens (zero padded).
+//        starting at a multiple of 128 tokens (zero padded).
 //    so that every GEMM below reads both operands contiguous along k.
 //  * fp8 grouped GEMMs, C[m][n] = (sum_k qP[m][k] qQ[n][k]) * sP[m] * sQ[n],
 //    on v_mfma_scale_f32_16x16x128_f8f6f4 (unit MX scales): forward gate_up
@@ -56,7 +56,7 @@ typedef int v8i_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kFp8Max = 448.0f;
-constexpr int kPad = 16;
+constexpr int kPad = 128;  // token-group alignment of the token-transposed layouts (whole 128-byte lines)
 constexpr int kMaxE = 1024;
 
 // float -> float8_e4m3fn, round to nearest even, saturating at +-448.
@@ -117,7 +117,7 @@ __device__ __forceinline__ float scale_of(float amax) {
 }
 
 constexpr int kMxBlock = 32;  // MXFP8 scaling block (k elements per e8m0 scale)
-constexpr int kMxPad = 32;    // MXFP8 token-group alignment
+constexpr int kMxPad = 128;   // MXFP8 token-group alignment
 
 // e8m0 exponent of an MX block from its amax (RCEIL):
 // clamp(ceil(log2(amax / 448)), -127, 127) + 127, 255 for NaN.
@@ -455,7 +455,7 @@ constexpr int kTRows = 128;  // slab rows transposed per pass
 // Quantizes a [n_rows x COLS] bf16 slab (row stride ld; COLS 64 or 128, a block of
 // 4 COLS threads) transposed: output row b
 // (slab column b) holds n_out values at out + b * ldo, rows >= n_rows zero
-// (n_out a multiple of 16, and of 32 for MX).
+// (n_out a multiple of 16, and of 32 for MX; the token groups use 128).
 //  * fp8 (MX false): column b scaled by s_col[b];
 //  * MX: one e8m0 scale per (column b, 32-row block k) at sc + b * sc_b + k * sc_k;
 //  * ROWS (MX): the same read also quantizes the slab along its columns (the
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(4 * COLS) void quant_cols_t_kernel(const uint16_t* 
 }
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
-// 16-aligned offset pstart_e, zero padded to ceil16(count_e)), scale [E][C].
+// 128-aligned offset pstart_e, zero padded to ceil128(count_e)), scale [E][C].
 // Block per (e, COLS columns); empty groups exit. With amax_in (the column amax
 // [E][C] of every group already known, from quant_rows_groupamax_kernel) the
 // amax pass is skipped and x is read once.
@@ -806,7 +806,7 @@ __global__ __launch_bounds__(4 * COLS) void mx_dual_cols_kernel(const uint16_t* 
 }
 
 // x [R][C] with expert token groups (counts) -> q [C][Rpad] (group e at the
-// 32-aligned offset pstart_e, zero padded to ceil32(count_e)) and the scales
+// 128-aligned offset pstart_e, zero padded to ceil128(count_e)) and the scales
 // k-block major, s [Rpad / 32][C]. Block per (e, COLS columns); empty groups exit.
 // With ROWS, the same read also writes the row-wise layout of the group's rows
 // (qr [R][C], sr [R][C / 32]).

@@ -773,8 +773,8 @@ def _quant_cols_t(w: Tensor, amax: Tensor, q: Tensor, q_offset: int, q_estride: 
 
 
 def _padded_rows(r: int, e: int) -> int:
-    """Width of the token-transposed layout: a multiple of 128, so that with every
-    row 128-byte aligned the transposing quantizer writes whole lines."""
+    """Width of the token-transposed layout (token groups 128-aligned): a multiple
+    of 128, so that every row and every group in it starts on a 128-byte line."""
     n = lib().moe_fp8_padded_rows(r, e)
     return (n + 127) // 128 * 128
 
@@ -952,7 +952,7 @@ def _mx_quant_rows(x: Tensor, cols: int) -> tuple[Tensor, Tensor]:
 
 
 def _mx_padded_rows(r: int, e: int) -> int:
-    """As _padded_rows (token groups 32-aligned): r + 31 e rounded up to 128."""
+    """As _padded_rows: r + 127 e rounded up to 128 (token groups 128-aligned)."""
     return (int(lib().moe_mxfp8_padded_rows(r, e)) + 127) // 128 * 128
 
 
@@ -1064,7 +1064,7 @@ def _(x, w1, w2, w3, num_tokens_per_expert, for_backward=False):
     u8 = lambda *shape: x.new_empty(*shape, dtype=torch.uint8)  # noqa: E731
     if not for_backward:
         return (*bf, *(u8(0) for _ in range(8)))
-    rpad = (r + e * 31 + 127) // 128 * 128  # _mx_padded_rows
+    rpad = (r + e * 127 + 127) // 128 * 128  # _mx_padded_rows
     return (*bf, u8(d, rpad), u8(rpad // 32, d), u8(h_dim, rpad), u8(rpad // 32, h_dim),
             u8(e, h_dim, d), u8(e, h_dim, d // 32), u8(e, d, 2 * h_dim), u8(e, d, 2 * h_dim // 32))
 
@@ -1330,7 +1330,7 @@ def _(x, shared_out, token_idx, scores_sorted, slot_pos, tok_pos, w1, w2, w3, nu
     r = token_idx.shape[0]
     e, h_dim, _ = w1.shape
     u8 = lambda *shape: x.new_empty(*shape, dtype=torch.uint8)  # noqa: E731
-    rpad = (r + e * 31 + 127) // 128 * 128  # _mx_padded_rows
+    rpad = (r + e * 127 + 127) // 128 * 128  # _mx_padded_rows
     return (x.new_empty(n, d), x.new_empty(r, h_dim), x.new_empty(r, h_dim), x.new_empty(r, h_dim),
             u8(d, rpad), u8(rpad // 32, d), u8(h_dim, rpad), u8(rpad // 32, h_dim),
             u8(e, h_dim, d), u8(e, h_dim, d // 32), u8(e, d, 2 * h_dim), u8(e, d, 2 * h_dim // 32))
