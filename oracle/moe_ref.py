@@ -430,7 +430,9 @@ class MoECfg:
     score_before_experts: bool = True
     use_grouped_mm: bool = True
     has_shared: bool = False
-    expert_kind: str = "swiglu"  # or "gptoss" (gpt_oss/moe.py GptOssGroupedExperts)
+    # "swiglu"; "gptoss" (gpt_oss/moe.py GptOssGroupedExperts); "fp8" / "mxfp8": the
+    # SwiGLU experts on the fp8 or MXFP8 emulations below (forward only)
+    expert_kind: str = "swiglu"
     swiglu_limit: float = 7.0
 
 
@@ -587,6 +589,12 @@ def moe_forward_reference_ops(params: dict, x: torch.Tensor, cfg: MoECfg, aux: d
                             cfg.swiglu_limit, routed_input, counts, **kw)
         if aux is not None:
             aux["counts"] = counts
+    elif cfg.expert_kind in ("fp8", "mxfp8"):
+        # the experts as the float8 / MXFP8 converters swap them in (torchao's grouped
+        # GEMMs, restated by experts_fp8_forward / experts_mxfp8_forward); forward only
+        run = experts_fp8_forward if cfg.expert_kind == "fp8" else experts_mxfp8_forward
+        routed_output = run(params["w1"], params["w2"], params["w3"], routed_input.bfloat16(), counts)[0]
+        routed_output = routed_output.type_as(routed_input)
     elif cfg.use_grouped_mm:
         w1, w2, w3 = params["w1"], params["w2"], params["w3"]
         offsets = torch.cumsum(counts, dim=0, dtype=torch.int32)
@@ -756,7 +764,7 @@ def quant_mxfp8(x: torch.Tensor, dim: int = -1):
 
 def mx_dequant(q: torch.Tensor, e: torch.Tensor) -> torch.Tensor:
     """fp64 values q * 2^(e - 127) of an MX tensor quantized along its last dim."""
-    f = torch.ldexp(torch.ones(e.shape, dtype=torch.float64), e.to(torch.float64) - E8M0_BIAS)
+    f = torch.ldexp(torch.ones(e.shape, dtype=torch.float64, device=e.device), e.to(torch.float64) - E8M0_BIAS)
     return q.double() * f.repeat_interleave(MX_BLOCK, dim=-1)
 
 

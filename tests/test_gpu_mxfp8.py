@@ -431,3 +431,33 @@ def test_mxfp8_layer_fused_permute_matches_separate_ops(dev, name):
     for n in gp_s:
         assert torch.equal(gp_f[n], gp_s[n]), n
     print(f"[case] {name}: out, grad_x and {len(gp_s)} parameter gradients identical", flush=True)
+
+
+def test_mxfp8_layer_hook_on_experts_keeps_the_experts_call(dev):
+    """The fused MXFP8 op reads the expert weights without calling the experts
+    module; a forward hook on that module turns the fusion off, so the hook sees
+    the call, and the results are those of the separate ops."""
+    banner("mxfp8 layer with a hook on the experts")
+    from tests.layer_util import LayerShape, build_layer
+
+    sh = LayerShape(**LAYER_CASES["shared_sigmoid"], mxfp8=True)
+    moe, x, gy = build_layer(sh, dev, seed=6)
+    xx = x.clone().requires_grad_(True)
+    assert moe._fused_core(xx.view(-1, sh.dim)) is not None
+    moe.zero_grad(set_to_none=True)
+    ref = moe(xx)
+    ref.backward(gy)
+    gx_ref = xx.grad.clone()
+    seen = []
+    handle = moe.experts.register_forward_hook(lambda m, a, o: seen.append(a[0].shape))
+    try:
+        assert moe._fused_core(xx.view(-1, sh.dim)) is None
+        moe.zero_grad(set_to_none=True)
+        xx.grad = None
+        out = moe(xx)
+        out.backward(gy)
+        torch.cuda.synchronize()
+    finally:
+        handle.remove()
+    assert seen == [(sh.bs * sh.slen * sh.top_k, sh.dim)]
+    assert torch.equal(out, ref) and torch.equal(xx.grad, gx_ref)

@@ -150,6 +150,66 @@ def test_feed_forward_with_bias_keeps_module_autograd():
     assert ff.w1.bias.grad is not None and x.grad is not None
 
 
+def _ffn(d=64, hs=128):
+    return FeedForward.Config(w1=Linear.Config(in_features=d, out_features=hs),
+                              w2=Linear.Config(in_features=hs, out_features=d),
+                              w3=Linear.Config(in_features=d, out_features=hs)).build()
+
+
+def test_feed_forward_trains_under_cpu_autocast():
+    """Under CPU autocast F.linear returns bf16 activations of fp32 weights: the
+    shared expert runs the three modules (autograd), as the reference does, and
+    its forward and backward complete with the module path's results."""
+    torch.manual_seed(0)
+    ff = _ffn()
+    x = torch.randn(64, 64, requires_grad=True)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        assert not ff._fused_backward_applies(x)
+        out = ff(x)
+        ref = ff.w2(torch.nn.functional.silu(ff.w1(x)) * ff.w3(x))
+    assert out.dtype == torch.bfloat16 and torch.equal(out, ref)
+    out.float().sum().backward()
+    assert x.grad is not None and all(lin.weight.grad is not None for lin in (ff.w1, ff.w2, ff.w3))
+
+
+@pytest.mark.parametrize("where", ["pre", "post", "global"])
+def test_feed_forward_hooks_see_the_linear_calls(where):
+    """A hook on a projection (or a global module hook) keeps the three module
+    calls, so the hook runs; without hooks the fused function reads the weights."""
+    ff = _ffn(16, 24)
+    x = torch.randn(8, 16, requires_grad=True)
+    assert ff._fused_backward_applies(x)
+    seen = []
+    if where == "pre":
+        handle = ff.w1.register_forward_pre_hook(lambda m, a: seen.append(m))
+    elif where == "post":
+        handle = ff.w2.register_forward_hook(lambda m, a, o: seen.append(m))
+    else:
+        handle = torch.nn.modules.module.register_module_forward_hook(lambda m, a, o: seen.append(m))
+    try:
+        assert not ff._fused_backward_applies(x)
+        ff(x).sum().backward()
+    finally:
+        handle.remove()
+    assert any(isinstance(m, Linear) for m in seen)
+    assert ff._fused_backward_applies(x)
+
+
+def test_feed_forward_linear_subclass_keeps_its_forward():
+    """A Linear subclass with its own forward is called, not bypassed."""
+
+    class Doubled(Linear):
+        def forward(self, x):
+            return 2 * super().forward(x)
+
+    ff = _ffn(16, 24)
+    ff.w2.__class__ = Doubled
+    x = torch.randn(8, 16, requires_grad=True)
+    assert not ff._fused_backward_applies(x)
+    h = torch.nn.functional.silu(ff.w1(x)) * ff.w3(x)
+    assert torch.equal(ff(x), 2 * torch.nn.functional.linear(h, ff.w2.weight))
+
+
 KIMI_48B = SimpleNamespace(
     hidden_size=2304, num_experts=256, num_experts_per_token=8, moe_intermediate_size=1024,
     moe_renormalize=True, moe_router_activation_func="sigmoid", num_shared_experts=1,

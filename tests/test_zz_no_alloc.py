@@ -70,6 +70,8 @@ def test_reorder_noalloc_rejects_sizes_past_its_scratch(dev):
     lib = _lib.lib()
     n, e, k = 600000, 256, 8  # 2 * ceil(n / 256) * 256 * 4 bytes > 4 MiB
     assert lib.moe_reorder_workspace_bytes(n, e) > SCRATCH_BYTES
-    p = ctypes.c_void_p(1)  # never dereferenced: the size check comes first
+    # null pointers: whichever check ran first, the call returns an error and
+    # launches nothing
+    p = ctypes.c_void_p(None)
     st = lib.moe_reorder_noalloc(p, p, n, k, e, p, p, p, p, p, p, torch.cuda.current_stream(dev).cuda_stream)
     assert st == MOE_ERR_WORKSPACE

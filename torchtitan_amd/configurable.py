@@ -105,3 +105,22 @@ class Module(nn.Module, Configurable):
 
     def _init_self_buffers(self, *, buffer_device: torch.device | None = None) -> None:
         pass
+
+
+def called_plainly(*modules: nn.Module) -> bool:
+    """True when calling each module would run only its own ``forward``: no
+    forward or backward hooks registered on it, and none registered globally.
+
+    A fused path that reads a submodule's parameters instead of calling the
+    submodule is taken only then, so that hooks always see the calls they were
+    registered for."""
+    from torch.nn.modules import module as _m
+
+    if (_m._global_forward_hooks or _m._global_forward_pre_hooks or _m._global_backward_hooks
+            or _m._global_backward_pre_hooks):
+        return False
+    for mod in modules:
+        if (mod._forward_hooks or mod._forward_pre_hooks or mod._backward_hooks
+                or mod._backward_pre_hooks):
+            return False
+    return True

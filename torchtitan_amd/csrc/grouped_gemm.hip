@@ -638,10 +638,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     } else if (MODE == kBwdDgu) {
       // dh = bf16(dy . w2) is gathered into the 64-byte span layout first, so g and u
       // are read, and dg and du written, as 16-byte pieces of 64 contiguous bytes per row.
-      // The g and u pieces of a 16-row block are loaded together, and the next block's
-      // are in flight while this block computes and stores: one memory round trip per
-      // tile is exposed instead of one per piece (the loads would otherwise wait behind
-      // each piece's stores, which may alias them).
+      // The g and u pieces of a 16-row block are loaded together, in one batch before
+      // the block's stores: one exposed memory round trip per 16-row block instead of
+      // one per piece (a load issued after a store, which may alias it, waits behind it).
       uint4 gbuf[1][TN / 2], ubuf[1][TN / 2];
       auto load_gu = [&](int i, int b) {
         const int r = row0 + wm * WM + i * 16 + ml;

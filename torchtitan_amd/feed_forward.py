@@ -9,7 +9,7 @@ import torch
 import torch.nn.functional as F
 
 from . import ops
-from .configurable import Module
+from .configurable import Module, called_plainly
 from .linear import Linear
 
 __all__ = ["FeedForward", "compute_ffn_hidden_dim"]
@@ -113,8 +113,13 @@ class FeedForward(Module):
         self.w3 = config.w3.build()
 
     def _fused_backward_applies(self, x: torch.Tensor) -> bool:
+        # the fused function reads the three weights instead of calling the Linear
+        # modules: only for plain Linear modules without hooks, outside autocast of
+        # x's device type (where F.linear would return another dtype than the weights')
         lins = (self.w1, self.w2, self.w3)
-        if any(lin.bias is not None for lin in lins) or torch.is_autocast_enabled():
+        if any(type(lin) is not Linear or lin.bias is not None for lin in lins):
+            return False
+        if torch.is_autocast_enabled(x.device.type) or not called_plainly(*lins):
             return False
         if not torch.is_grad_enabled() or not (x.requires_grad or any(lin.weight.requires_grad for lin in lins)):
             return False

@@ -20,7 +20,7 @@ import torch
 from torch import nn
 
 from . import ops
-from .configurable import Module
+from .configurable import Module, called_plainly
 from .feed_forward import FeedForward
 from .linear import Linear
 
@@ -434,6 +434,10 @@ class MoE(Module):
         if not (self.fuse_permute_into_quantizers and type(experts) is GroupedExperts
                 and (experts.mxfp8 or experts.float8) and self.score_before_experts and x.is_cuda
                 and x.dtype == torch.bfloat16):
+            return None
+        # the fused op reads the expert weights without calling the experts module:
+        # not where hooks on that module expect its call
+        if not called_plainly(experts):
             return None
         if not all(_local(w).dtype == torch.bfloat16 for w in (experts.w1, experts.w2, experts.w3)):
             return None
