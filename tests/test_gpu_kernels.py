@@ -40,6 +40,11 @@ ROUTER_CASES = {
     "ties_sigmoid_e64_k4": (2048, 64, 4, "sigmoid", None, None, False, 1.0, False, False, 5),
     "ties_group_e32_g4": (1024, 32, 4, "sigmoid", 4, 2, True, 1.0, False, False, 3),
     "force_load_balance": (1000, 16, 3, "sigmoid", None, None, True, 1.0, False, True, 0),
+    # eight experts per lane, K past a wave's eighth, ties and a bias
+    "ties_sigmoid_e512_k16": (1024, 512, 16, "sigmoid", None, None, True, 1.0, True, False, 4),
+    # E not a multiple of 64 with five experts per lane
+    "softmax_e320_k10": (1024, 320, 10, "softmax", None, None, True, 2.0, False, False, 0),
+    "ties_group_e512_g16_k12": (1024, 512, 12, "sigmoid", 16, 5, True, 1.0, True, False, 6),
 }
 
 
@@ -294,3 +299,4 @@ def test_grouped_swiglu_vs_torch_grouped_mm(dev, name):
     for k, (a, b) in pairs.items():
         assert diff[k] <= 1e-4 * a.numel(), (k, diff[k], a.numel())
         assert rel_err(a, b) <= 2.0 ** -7, (k, rel_err(a, b))
+
