@@ -20,7 +20,7 @@ stream for the per-kernel table and the roofline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
                        [--workload kimi|dsv3|zipf|kimi_fp8|kimi_mxfp8|gptoss_20b|c1|c1_grouped]
-                       [--no-cpu-baseline] [--cpu-tokens N] [--gemm-ceiling]
+                       [--no-cpu-baseline] [--cpu-tokens N] [--gemm-ceiling] [--mover-ceiling]
 """
 
 from __future__ import annotations
@@ -454,6 +454,47 @@ def gemm_ceiling(w: dict, dev: torch.device, reps: int = 10) -> dict:
     return out
 
 
+def mover_ceiling(w: dict, dev: torch.device, reps: int = 10) -> dict:
+    """torch's own kernels on the movers' shapes of workload w (R = N*K routed rows of D
+    bf16): a fill of R rows (writes only), a copy of R rows (read and write), the row
+    gather x[token] of N rows into R (the unscored permute's traffic) and the sum over
+    the K rows of each token of a token-major [N, K, D] array (the combine's reads and
+    writes without its random gather). What plain streaming kernels reach for these
+    read/write mixes on this GPU; not part of the step."""
+    n, d, k = w["bs"] * w["slen"], w["dim"], w["top_k"]
+    r = n * k
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(n, d, generator=gen, device=dev).bfloat16()
+    big = torch.randn(r, d, generator=gen, device=dev).bfloat16()
+    dst = torch.empty_like(big)
+    tok = torch.randint(0, n, (r,), generator=gen, device=dev)
+    row = 2 * d
+    cases = {  # name: (fn, bytes read, bytes written)
+        "fill": (lambda: dst.zero_(), 0, r * row),
+        "copy": (lambda: dst.copy_(big), r * row, r * row),
+        "gather_rows": (lambda: torch.index_select(x, 0, tok, out=dst), n * row, r * row),
+        "sum_k_rows": (lambda: torch.sum(big.view(n, k, d), dim=1), r * row, n * row),
+    }
+    out = {}
+    for name, (fn, rd, wr) in cases.items():
+        for _ in range(3):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ts = []
+        for _ in range(reps):
+            ev[0].record()
+            fn()
+            ev[1].record()
+            ev[1].synchronize()
+            ts.append(ev[0].elapsed_time(ev[1]))
+        ms = statistics.median(ts)
+        gbs = (rd + wr) / (ms * 1e-3) / 1e9
+        out[name] = {"read_bytes": rd, "write_bytes": wr, "ms": round(ms, 4), "gbs": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        print(f"[bench] torch {name}: {ms:.4f} ms {gbs:.1f} GB/s", file=sys.stderr, flush=True)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -464,6 +505,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="also time the vendor library on uniform-batch equivalents of the six expert GEMMs")
+    ap.add_argument("--mover-ceiling", action="store_true",
+                    help="also time torch's fill, copy, row gather and K-row sum on the movers' shapes")
     ap.add_argument("--cpu-tokens", type=int, default=None,
                     help="tokens in the CPU baseline sample (default: all for kimi, 1024 for dsv3, else 8192)")
     args = ap.parse_args()
@@ -623,6 +666,8 @@ def main() -> int:
     }
     if args.gemm_ceiling:
         line["library_gemm_uniform_batch"] = gemm_ceiling(w, dev)
+    if args.mover_ceiling:
+        line["torch_streaming_kernels"] = mover_ceiling(w, dev)
     print(json.dumps(line), flush=True)
     return 0
 
