@@ -86,6 +86,13 @@ def test_router_bit_exact(dev, name):
     assert torch.equal(idx, t_idx)
     assert torch.equal(counts, t_counts)
     assert torch.equal(top, t_top)
+    # 4. without the histogram: the same selection and scores, no counts
+    top2, idx2, counts2, scores2 = o.router(
+        logits.to(dev), b.to(dev) if b is not None else None, e, k, o.SCORE_FUNCS[sf],
+        groups or 0, limited or 0, norm, scale, flb, False,
+    )
+    assert torch.equal(top2, top) and torch.equal(idx2, idx) and torch.equal(scores2, scores)
+    assert counts2.numel() == 0
 
 
 @pytest.mark.parametrize("name", ["kimi_sigmoid_bias_e256_k8", "tiny_softmax_e8_k2", "dsv3_group_limited"])
@@ -300,3 +307,42 @@ def test_grouped_swiglu_vs_torch_grouped_mm(dev, name):
         assert diff[k] <= 1e-4 * a.numel(), (k, diff[k], a.numel())
         assert rel_err(a, b) <= 2.0 ** -7, (k, rel_err(a, b))
 
+
+
+def test_layer_counts_routing_once(dev):
+    """With its own router and reorderer the layer takes the per-expert counts from the
+    reorder's histogram only (moe.py:312-317; the router's, moe.py:269-274, is the same
+    on one GPU): output, gradients and tokens_per_expert equal the two-histogram path's,
+    and a hook on the router brings the router's own call back."""
+    from tests.layer_util import LayerShape, build_layer
+
+    banner("layer routing counted once vs twice")
+    sh = LayerShape(bs=2, slen=512, dim=512, experts=16, top_k=4, hidden=256, shared_hidden=256)
+    moe, x, gy = build_layer(sh, dev, seed=5)
+
+    def run(once):
+        moe.count_routing_once = once
+        moe.zero_grad(set_to_none=True)
+        moe.tokens_per_expert.zero_()
+        xx = x.clone().requires_grad_(True)
+        assert moe._routing_counted_once() == once
+        out = moe(xx)
+        out.backward(gy)
+        torch.cuda.synchronize()
+        return out.detach(), xx.grad, moe.tokens_per_expert.clone(), {n: p.grad.clone() for n, p in moe.named_parameters()}
+
+    a, b = run(False), run(True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    assert a[2].sum().item() == sh.bs * sh.slen * sh.top_k
+    for n in a[3]:
+        assert torch.equal(a[3][n], b[3][n]), n
+    seen = []
+    handle = moe.router.register_forward_hook(lambda m, i, o: seen.append(o[2].clone()))
+    try:
+        assert not moe._routing_counted_once()
+        moe.tokens_per_expert.zero_()
+        moe(x)
+        torch.cuda.synchronize()
+        assert len(seen) == 1 and torch.equal(seen[0].float(), moe.tokens_per_expert)
+    finally:
+        handle.remove()

@@ -26,26 +26,33 @@ constexpr int kMaxTopK = 32;
 
 // ---------------------------------------------------------------------------
 // Occupancy words: bits[e][w] bit l set <=> token (block*256 + 64*w + l) chose e.
+// ev[j] receives the token's expert of slot j (-1 past K or outside [0, E)). The K
+// loads are issued together (slots past K re-read slot K - 1, always in bounds).
 // ---------------------------------------------------------------------------
+template <int MAXK>
 __device__ __forceinline__ void build_occupancy(uint64_t (*bits)[4], const int64_t* __restrict__ idx,
-                                                int64_t n_tokens, int K, int E) {
+                                                int64_t n_tokens, int K, int E, int (&ev)[MAXK]) {
   for (int i = threadIdx.x; i < E * 4; i += blockDim.x) (&bits[0][0])[i] = 0ull;
-  __syncthreads();
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * kBlockTokens + threadIdx.x;
-  if (t < n_tokens) {
-    for (int j = 0; j < K; ++j) {
-      const int64_t e = idx[t * K + j];
-      if (e >= 0 && e < E) atomicOr((unsigned long long*)&bits[e][wv], 1ull << lane);
-    }
-  }
+  int64_t raw[MAXK];
+#pragma unroll
+  for (int j = 0; j < MAXK; ++j) raw[j] = t < n_tokens ? idx[t * K + (j < K ? j : K - 1)] : -1;
+#pragma unroll
+  for (int j = 0; j < MAXK; ++j) ev[j] = (j < K && raw[j] >= 0 && raw[j] < E) ? (int)raw[j] : -1;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < MAXK; ++j)
+    if (ev[j] >= 0) atomicOr((unsigned long long*)&bits[ev[j]][wv], 1ull << lane);
   __syncthreads();
 }
 
+template <int MAXK>
 __global__ __launch_bounds__(256) void hist_kernel(const int64_t* __restrict__ idx, int64_t n_tokens,
                                                    int K, int E, int32_t* __restrict__ block_hist) {
   __shared__ uint64_t bits[kMaxExperts][4];
-  build_occupancy(bits, idx, n_tokens, K, E);
+  int ev[MAXK];
+  build_occupancy<MAXK>(bits, idx, n_tokens, K, E, ev);
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     block_hist[(int64_t)blockIdx.x * E + e] =
         __popcll(bits[e][0]) + __popcll(bits[e][1]) + __popcll(bits[e][2]) + __popcll(bits[e][3]);
@@ -133,42 +140,52 @@ struct ScatterParams {
   int32_t* tok_pos;         // [N, K] a token's sorted positions, ascending
 };
 
+// MAXK >= K bounds the per-token arrays and the slot-rank compares (K x K at run time).
+// All loads (expert ids, scores, block bases) are issued before the first store: a load
+// issued after a store waits for it (one counter), which would cost a round trip per slot.
+template <int MAXK>
 __global__ __launch_bounds__(256) void scatter_kernel(ScatterParams p) {
   __shared__ uint64_t bits[kMaxExperts][4];
-  build_occupancy(bits, p.idx, p.n_tokens, p.K, p.E);
+  int ev[MAXK];
+  build_occupancy<MAXK>(bits, p.idx, p.n_tokens, p.K, p.E, ev);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * kBlockTokens + threadIdx.x;
   if (t >= p.n_tokens) return;
   const int K = p.K, E = p.E;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int32_t* base = p.block_base + (int64_t)blockIdx.x * E;
-  int ev[kMaxTopK];
-  int pv[kMaxTopK];
+  int pv[MAXK];
+  float sv[MAXK];
 #pragma unroll
-  for (int j = 0; j < kMaxTopK; ++j) {
-    ev[j] = -1;
-    pv[j] = 0;
-    if (j < K) {
-      const int64_t e = p.idx[t * K + j];
-      if (e >= 0 && e < E) {
-        int rank = __popcll(bits[e][wv] & below);
-        for (int w = 0; w < wv; ++w) rank += __popcll(bits[e][w]);
-        const int pos = base[e] + rank;
-        ev[j] = (int)e;
-        pv[j] = pos;
-        p.token_idx[pos] = t;
-        if (p.scores_sorted) p.scores_sorted[pos] = p.top_scores[t * K + j];
-        p.slot_pos[t * K + j] = pos;
-      }
+  for (int j = 0; j < MAXK; ++j) sv[j] = p.scores_sorted ? p.top_scores[t * K + (j < K ? j : K - 1)] : 0.0f;
+#pragma unroll
+  for (int j = 0; j < MAXK; ++j) pv[j] = base[ev[j] >= 0 ? ev[j] : 0];
+#pragma unroll
+  for (int j = 0; j < MAXK; ++j) {
+    if (ev[j] >= 0) {
+      const int e = ev[j];
+      int rank = __popcll(bits[e][wv] & below);
+      for (int w = 0; w < wv; ++w) rank += __popcll(bits[e][w]);
+      pv[j] += rank;
+    } else {
+      pv[j] = 0;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MAXK; ++j) {
+    if (ev[j] >= 0) {
+      p.token_idx[pv[j]] = t;
+      if (p.scores_sorted) p.scores_sorted[pv[j]] = sv[j];
+      p.slot_pos[t * K + j] = pv[j];
     }
   }
   // positions are monotone in the expert id, so ascending position == ascending expert
 #pragma unroll
-  for (int j = 0; j < kMaxTopK; ++j) {
+  for (int j = 0; j < MAXK; ++j) {
     if (j < K) {
       int r = 0;
 #pragma unroll
-      for (int i = 0; i < kMaxTopK; ++i) r += (i < K) && (ev[i] < ev[j]);
+      for (int i = 0; i < MAXK; ++i) r += (i < K) && (ev[i] < ev[j]);
       p.tok_pos[t * K + r] = pv[j];
     }
   }
@@ -414,6 +431,14 @@ static int stream_grid(int64_t work, int per_block = 256, int cap = 8192) {
 
 using namespace moe;
 
+static void launch_hist(const int64_t* idx, int64_t n_tokens, int top_k, int n_experts, int32_t* block_hist,
+                        hipStream_t stream) {
+  const dim3 grid((unsigned)((n_tokens + kBlockTokens - 1) / kBlockTokens));
+  if (top_k <= 8) hipLaunchKernelGGL(hist_kernel<8>, grid, dim3(256), 0, stream, idx, n_tokens, top_k, n_experts, block_hist);
+  else if (top_k <= 16) hipLaunchKernelGGL(hist_kernel<16>, grid, dim3(256), 0, stream, idx, n_tokens, top_k, n_experts, block_hist);
+  else hipLaunchKernelGGL(hist_kernel<kMaxTopK>, grid, dim3(256), 0, stream, idx, n_tokens, top_k, n_experts, block_hist);
+}
+
 MOE_API int64_t moe_reorder_workspace_bytes(int64_t n_tokens, int32_t n_experts) {
   const int64_t nb = (n_tokens + kBlockTokens - 1) / kBlockTokens;
   return 2 * nb * n_experts * (int64_t)sizeof(int32_t);
@@ -434,9 +459,7 @@ MOE_API int moe_histogram(const int64_t* selected_experts, int64_t n_tokens, int
   if (workspace_bytes < moe_reorder_workspace_bytes(n_tokens, n_experts)) return kErrWorkspace;
   const int nb = (int)((n_tokens + kBlockTokens - 1) / kBlockTokens);
   int32_t* block_hist = (int32_t*)workspace;
-  if (nb > 0)
-    hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
-                       top_k, n_experts, block_hist);
+  if (nb > 0) launch_hist(selected_experts, n_tokens, top_k, n_experts, block_hist, stream);
   hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_hist, nb, n_experts,
                      (int32_t*)nullptr, counts, offsets);
   return launch_status();
@@ -451,15 +474,15 @@ static int reorder_launch(const int64_t* selected_experts, const float* top_scor
   const int nb = (int)((n_tokens + kBlockTokens - 1) / kBlockTokens);
   int32_t* block_hist = workspace;
   int32_t* block_base = block_hist + (int64_t)nb * n_experts;
-  if (nb > 0)
-    hipLaunchKernelGGL(hist_kernel, dim3(nb), dim3(256), 0, stream, selected_experts, n_tokens,
-                       top_k, n_experts, block_hist);
+  if (nb > 0) launch_hist(selected_experts, n_tokens, top_k, n_experts, block_hist, stream);
   hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_hist, nb, n_experts,
                      block_base, counts, offsets);
   if (nb > 0) {
     ScatterParams p{selected_experts, top_scores, block_base, n_tokens, top_k, n_experts,
                     token_idx, scores_sorted, slot_pos, tok_pos};
-    hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(256), 0, stream, p);
+    if (top_k <= 8) hipLaunchKernelGGL(scatter_kernel<8>, dim3(nb), dim3(256), 0, stream, p);
+    else if (top_k <= 16) hipLaunchKernelGGL(scatter_kernel<16>, dim3(nb), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(scatter_kernel<kMaxTopK>, dim3(nb), dim3(256), 0, stream, p);
   }
   return launch_status();
 }

@@ -294,6 +294,9 @@ class TokenChoiceTopKRouter(Module):
     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """x [bs*slen, dim] -> (top_scores [N,K] f32, selected_experts_indices [N,K] i64,
         num_tokens_per_expert [E] i64)."""
+        return self._route(x, expert_bias, True)
+
+    def _route(self, x: torch.Tensor, expert_bias: torch.Tensor | None, with_counts: bool):
         # fp32 gate logits, as in the reference (moe.py:230-232)
         logits = gate_logits_f32(x, self.gate, self.gate_bf16_mfma)
         if self.score_func not in ops.SCORE_FUNCS:
@@ -302,7 +305,7 @@ class TokenChoiceTopKRouter(Module):
         top_scores, selected, counts, _scores = ops.router(
             logits, expert_bias, self.num_experts, self.top_k, ops.SCORE_FUNCS[self.score_func],
             groups, limited, bool(self.route_norm), float(self.route_scale),
-            bool(self._debug_force_load_balance),
+            bool(self._debug_force_load_balance), with_counts,
         )
         return top_scores, selected, counts
 
@@ -381,11 +384,18 @@ class MoE(Module):
         bs, slen, dim = x.shape
         x = x.view(-1, dim)
 
-        top_scores, selected_experts_indices, num_tokens_per_expert = self.router(x, self.expert_bias)
-        with torch.no_grad():
-            self.tokens_per_expert.add_(num_tokens_per_expert)
-
-        layout = self.reorderer(top_scores, selected_experts_indices)
+        if self._routing_counted_once():
+            # the module's own router and reorderer: the router's histogram (moe.py:269-274)
+            # equals the reorderer's (moe.py:312-317) on one GPU, so it is taken once, there
+            top_scores, selected_experts_indices, _ = self.router._route(x, self.expert_bias, False)
+            layout = self.reorderer(top_scores, selected_experts_indices)
+            with torch.no_grad():
+                self.tokens_per_expert.add_(layout[2])
+        else:
+            top_scores, selected_experts_indices, num_tokens_per_expert = self.router(x, self.expert_bias)
+            with torch.no_grad():
+                self.tokens_per_expert.add_(num_tokens_per_expert)
+            layout = self.reorderer(top_scores, selected_experts_indices)
         top_scores_experts_sorted, _token_indices_experts_sorted, num_tokens_per_expert = layout
 
         core = self._fused_core(x)
@@ -427,6 +437,13 @@ class MoE(Module):
     # from one pass, and gains 2 %)
     fuse_permute_into_quantizers = True
     fuse_fp8_permute = False
+
+    # one histogram for the router and the reorderer where both are this module's own
+    count_routing_once = True
+
+    def _routing_counted_once(self) -> bool:
+        return (self.count_routing_once and type(self.router) is TokenChoiceTopKRouter
+                and type(self.reorderer) is TokenReorderer and called_plainly(self.router, self.reorderer))
 
     def _fused_core(self, x: torch.Tensor):
         """The fused op for this layer's experts, or None where the separate ops run."""

@@ -58,8 +58,12 @@ def router(
     route_norm: bool,
     route_scale: float,
     force_load_balance: bool,
+    with_counts: bool = True,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """Returns (top_scores [N,K] f32, selected_experts [N,K] i64, counts [E] i64, scores [N,E] f32)."""
+    """Returns (top_scores [N,K] f32, selected_experts [N,K] i64, counts [E] i64, scores [N,E] f32).
+    with_counts=False skips the histogram (moe.py:269-274) and returns an empty counts
+    tensor, for callers that take the counts from the reorder that follows (its own
+    histogram, moe.py:312-317, the same counts on one GPU)."""
     require_gpu(logits, expert_bias)
     logits = logits.float().contiguous()
     n = logits.shape[0]
@@ -68,28 +72,29 @@ def router(
     scores = torch.empty_like(logits)
     top_scores = torch.empty(n, top_k, dtype=torch.float32, device=dev)
     idx = torch.empty(n, top_k, dtype=torch.int64, device=dev)
-    counts = torch.empty(num_experts, dtype=torch.int64, device=dev)
+    counts = torch.empty(num_experts if with_counts else 0, dtype=torch.int64, device=dev)
     s = stream_of(logits)
     call(
         "moe_router_fwd", ptr(logits), ptr(bias), n, num_experts, top_k, score_func, num_expert_groups,
             num_limited_groups, int(route_norm), route_scale, int(force_load_balance),
             ptr(scores), ptr(top_scores), ptr(idx), s,
     )
-    ws = _workspace(n, num_experts, dev)
-    call(
-        "moe_histogram", ptr(idx), n, top_k, num_experts, ptr(ws), ws.numel(), ptr(counts), None, s
-    )
+    if with_counts:
+        ws = _workspace(n, num_experts, dev)
+        call(
+            "moe_histogram", ptr(idx), n, top_k, num_experts, ptr(ws), ws.numel(), ptr(counts), None, s
+        )
     return top_scores, idx, counts, scores
 
 
 @router.register_fake
 def _(logits, expert_bias, num_experts, top_k, score_func, num_expert_groups, num_limited_groups,
-      route_norm, route_scale, force_load_balance):
+      route_norm, route_scale, force_load_balance, with_counts=True):
     n = logits.shape[0]
     return (
         logits.new_empty(n, top_k, dtype=torch.float32),
         logits.new_empty(n, top_k, dtype=torch.int64),
-        logits.new_empty(num_experts, dtype=torch.int64),
+        logits.new_empty(num_experts if with_counts else 0, dtype=torch.int64),
         logits.new_empty(logits.shape, dtype=torch.float32),
     )
 
@@ -117,7 +122,7 @@ def _(grad_top_scores, scores, selected_experts, score_func, route_norm, route_s
 
 
 def _router_setup(ctx, inputs, output):
-    (_logits, _bias, _e, _k, score_func, _g, _gk, route_norm, route_scale, _flb) = inputs
+    (_logits, _bias, _e, _k, score_func, _g, _gk, route_norm, route_scale, _flb, _wc) = inputs
     _top, idx, counts, scores = output
     ctx.save_for_backward(scores, idx)
     ctx.cfg = (score_func, route_norm, route_scale)
@@ -131,7 +136,7 @@ def _router_bwd(ctx, g_top, _g_idx, _g_counts, _g_scores):
     if g_top is None:
         g_top = torch.zeros(idx.shape, dtype=torch.float32, device=idx.device)
     grad_logits = router_backward(g_top, scores, idx, score_func, route_norm, route_scale)
-    return grad_logits, None, None, None, None, None, None, None, None, None
+    return grad_logits, None, None, None, None, None, None, None, None, None, None
 
 
 router.register_autograd(_router_bwd, setup_context=_router_setup)
