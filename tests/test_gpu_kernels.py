@@ -119,9 +119,16 @@ def test_router_backward(dev, name):
     assert rel_err(lg.grad, l64.grad) < 1e-5
 
 
-def test_reorder_exact(dev):
-    banner("reorder")
-    n, e, k = 5000, 64, 6
+# (tokens, experts, top-k): the scan folded into the scatter (per-block counts of at most
+# 32768 words, E a multiple of 4), and the separate scan kernel (E = 62; 157 x 512 words)
+REORDER_CASES = {"fused_e64": (5000, 64, 6), "kimi_fused_e256": (16384, 256, 8),
+                 "scan_e62": (5000, 62, 6), "scan_e512": (40000, 512, 8)}
+
+
+@pytest.mark.parametrize("name", list(REORDER_CASES))
+def test_reorder_exact(dev, name):
+    banner(f"reorder {name}")
+    n, e, k = REORDER_CASES[name]
     logits, _ = _router_inputs(n, e, 0, False, seed=7)
     o = ops()
     top, idx, _, _ = o.router(logits.to(dev), None, e, k, 1, 0, 0, False, 1.0, False)

@@ -131,7 +131,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(const int32_t* __res
 struct ScatterParams {
   const int64_t* idx;         // [N, K]
   const float* top_scores;    // [N, K] nullable
-  const int32_t* block_base;  // [NB, E]
+  const int32_t* block_base;  // [NB, E] (the separate scan), or
+  const int32_t* block_hist;  // [NB, E] with the scan done in each block (FUSED_SCAN)
+  int n_blocks;
+  int64_t* counts;            // [E] nullable; FUSED_SCAN: written by block 0
+  int32_t* offsets;           // [E] nullable; FUSED_SCAN: written by block 0
   int64_t n_tokens;
   int K, E;
   int64_t* token_idx;       // [R] token of each sorted position
@@ -143,17 +147,57 @@ struct ScatterParams {
 // MAXK >= K bounds the per-token arrays and the slot-rank compares (K x K at run time).
 // All loads (expert ids, scores, block bases) are issued before the first store: a load
 // issued after a store waits for it (one counter), which would cost a round trip per slot.
-template <int MAXK>
+// FUSED_SCAN: for small histograms (n_blocks x E <= kFusedScanMax) each block forms its
+// own bases from the per-block counts — every expert's total over all blocks, their
+// exclusive scan over the experts, plus the expert's count in the blocks before this one —
+// which saves the scan kernel's launch; block 0 writes counts and offsets.
+constexpr int kFusedScanMax = 32768;
+
+template <int MAXK, bool FUSED_SCAN>
 __global__ __launch_bounds__(256) void scatter_kernel(ScatterParams p) {
   __shared__ uint64_t bits[kMaxExperts][4];
+  __shared__ int s_base[FUSED_SCAN ? kMaxExperts : 1];
+  __shared__ int s_tmp[4];
+  const int K = p.K, E = p.E;
+  if constexpr (FUSED_SCAN) {
+    // thread t owns experts 4t .. 4t + 3 (E <= 1024 = 4 x 256 threads)
+    int tot[4] = {0, 0, 0, 0}, pre[4] = {0, 0, 0, 0};
+    const int e0 = 4 * (int)threadIdx.x;
+    constexpr int kB = 8;
+    for (int b0 = 0; b0 < p.n_blocks; b0 += kB) {
+      int4 v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j)
+        v[j] = (b0 + j < p.n_blocks && e0 < E) ? *(const int4*)(p.block_hist + (int64_t)(b0 + j) * E + e0)
+                                               : make_int4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int in = b0 + j < (int)blockIdx.x;
+        tot[0] += v[j].x; tot[1] += v[j].y; tot[2] += v[j].z; tot[3] += v[j].w;
+        if (in) { pre[0] += v[j].x; pre[1] += v[j].y; pre[2] += v[j].z; pre[3] += v[j].w; }
+      }
+    }
+    int start[4];
+    block_exclusive_scan4(tot, start, s_tmp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + i;
+      if (e < E) {
+        s_base[e] = start[i] + pre[i];
+        if (blockIdx.x == 0) {
+          if (p.counts) p.counts[e] = tot[i];
+          if (p.offsets) p.offsets[e] = start[i] + tot[i];
+        }
+      }
+    }
+  }
   int ev[MAXK];
-  build_occupancy<MAXK>(bits, p.idx, p.n_tokens, p.K, p.E, ev);
+  build_occupancy<MAXK>(bits, p.idx, p.n_tokens, K, E, ev);  // its barriers publish s_base
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * kBlockTokens + threadIdx.x;
   if (t >= p.n_tokens) return;
-  const int K = p.K, E = p.E;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int32_t* base = p.block_base + (int64_t)blockIdx.x * E;
+  const int32_t* base = FUSED_SCAN ? s_base : p.block_base + (int64_t)blockIdx.x * E;
   int pv[MAXK];
   float sv[MAXK];
 #pragma unroll
@@ -475,14 +519,24 @@ static int reorder_launch(const int64_t* selected_experts, const float* top_scor
   int32_t* block_hist = workspace;
   int32_t* block_base = block_hist + (int64_t)nb * n_experts;
   if (nb > 0) launch_hist(selected_experts, n_tokens, top_k, n_experts, block_hist, stream);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_hist, nb, n_experts,
-                     block_base, counts, offsets);
+  // (16-byte reads of each block's counts: E a multiple of 4)
+  const bool fused = nb > 0 && n_experts % 4 == 0 && (int64_t)nb * n_experts <= kFusedScanMax;
+  if (!fused)
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_hist, nb, n_experts,
+                       block_base, counts, offsets);
   if (nb > 0) {
-    ScatterParams p{selected_experts, top_scores, block_base, n_tokens, top_k, n_experts,
-                    token_idx, scores_sorted, slot_pos, tok_pos};
-    if (top_k <= 8) hipLaunchKernelGGL(scatter_kernel<8>, dim3(nb), dim3(256), 0, stream, p);
-    else if (top_k <= 16) hipLaunchKernelGGL(scatter_kernel<16>, dim3(nb), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(scatter_kernel<kMaxTopK>, dim3(nb), dim3(256), 0, stream, p);
+    ScatterParams p{selected_experts, top_scores, block_base, block_hist, nb, counts, offsets,
+                    n_tokens, top_k, n_experts, token_idx, scores_sorted, slot_pos, tok_pos};
+    const dim3 grid(nb), block(256);
+    if (fused) {
+      if (top_k <= 8) hipLaunchKernelGGL((scatter_kernel<8, true>), grid, block, 0, stream, p);
+      else if (top_k <= 16) hipLaunchKernelGGL((scatter_kernel<16, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((scatter_kernel<kMaxTopK, true>), grid, block, 0, stream, p);
+    } else {
+      if (top_k <= 8) hipLaunchKernelGGL((scatter_kernel<8, false>), grid, block, 0, stream, p);
+      else if (top_k <= 16) hipLaunchKernelGGL((scatter_kernel<16, false>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((scatter_kernel<kMaxTopK, false>), grid, block, 0, stream, p);
+    }
   }
   return launch_status();
 }
