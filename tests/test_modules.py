@@ -379,3 +379,45 @@ def test_gate_dw_reduce_reassembles_the_gradient(halves):
     assert not torch.equal(gate_dw_reduce(p, e), want)
     if halves:
         assert not torch.equal(gate_dw_reduce(parts[0], e), want)
+
+
+def test_routing_counted_once_only_for_the_modules_own_router_and_reorderer():
+    """The layer takes the per-expert counts from the reorder alone only when its router and
+    reorderer are the module's own types, unhooked, and count_routing_once is set; otherwise
+    the router's forward (with its own histogram, moe.py:269-274) is called as in the
+    reference, so hooks and subclasses see it."""
+    from torchtitan_amd.moe import TokenReorderer
+
+    with torch.device("meta"):
+        moe = _cfg().build()
+    assert moe._routing_counted_once()
+    moe.count_routing_once = False
+    assert not moe._routing_counted_once()
+    moe.count_routing_once = True
+    for mod in (moe.router, moe.reorderer):
+        h = mod.register_forward_hook(lambda m, i, o: None)
+        assert not moe._routing_counted_once()
+        h.remove()
+        h = mod.register_forward_pre_hook(lambda m, i: None)
+        assert not moe._routing_counted_once()
+        h.remove()
+    g = torch.nn.modules.module.register_module_forward_hook(lambda m, i, o: None)
+    try:
+        assert not moe._routing_counted_once()
+    finally:
+        g.remove()
+    assert moe._routing_counted_once()
+
+    class Router(TokenChoiceTopKRouter):
+        pass
+
+    class Reorderer(TokenReorderer):
+        pass
+
+    with torch.device("meta"):
+        sub = _cfg().build()
+    sub.router.__class__ = Router
+    assert not sub._routing_counted_once()
+    sub.router.__class__ = TokenChoiceTopKRouter
+    sub.reorderer.__class__ = Reorderer
+    assert not sub._routing_counted_once()
