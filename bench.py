@@ -118,7 +118,8 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
     n = w["bs"] * w["slen"]
     d, e, k, h = w["dim"], w["experts"], w["top_k"], w["hidden"]
     r = n * k
-    b = 2  # bf16 rows
+    b = 4 if w.get("fp32") else 2  # row bytes per element (fp32 activations on the c1 workloads)
+    sb = w.get("score_before", True)
     # bwd_dw (fp32 kernels) is one launch per weight: 2 R D H each
     flops = {"gate_up": 4, "down": 2, "bwd_dgu": 2, "bwd_dx": 4, "bwd_dw13": 4, "bwd_dw1": 4, "bwd_dw2": 2,
              "bwd_dw": 2}
@@ -132,14 +133,20 @@ def kernel_work(name: str, w: dict) -> tuple[str, float]:
         "moe_histogram": 8 * n * k + 8 * e,
         # ids read twice (histogram + scatter), sorted scores/token ids and two int32 maps written
         "moe_reorder": 16 * n * k + 4 * n * k + 4 * r + 8 * r + 8 * n * k,
-        # x read once, K copies written, slot map + sorted scores read
-        "moe_permute": n * d * b + r * d * b + 4 * n * k + 4 * r,
-        # routed rows + shared rows read, out written, tok map + scores read
-        "moe_combine": r * d * b + 2 * n * d * b + 4 * n * k,
-        # grad_out read, K copies written (score_before) or + routed rows read (score_after)
-        "moe_combine_bwd": n * d * b + r * d * b + 4 * n * k,
-        # grad_routed read, x read, grad_x written, score grads written
-        "moe_permute_bwd": r * d * b + 2 * n * d * b + 4 * n * k + 8 * r,
+        # x read once, K copies written, slot map read (+ sorted scores when the score
+        # multiplies the expert inputs)
+        "moe_permute": n * d * b + r * d * b + 4 * n * k + (4 * r if sb else 0),
+        # routed rows + shared rows read, out written, tok map read (+ sorted scores when the
+        # score multiplies the expert outputs)
+        "moe_combine": r * d * b + 2 * n * d * b + 4 * n * k + (0 if sb else 4 * r),
+        # score before the experts: the gather grad_out[token] into K copies; after them:
+        # grad_out and the routed rows read, the scaled copies and score gradients written
+        "moe_combine_bwd": (n * d * b + r * d * b + 4 * n * k) if sb else
+                           (n * d * b + 2 * r * d * b + 4 * n * k + 8 * r),
+        # grad_routed read, grad_x written (+ x read and score gradients written when the
+        # score multiplies the expert inputs)
+        "moe_permute_bwd": (r * d * b + 2 * n * d * b + 4 * n * k + 8 * r) if sb else
+                           (r * d * b + n * d * b + 4 * n * k),
         "moe_reorder_bwd": 4 * r + 4 * n * k + 4 * n * k,
         "moe_router_bwd": 4 * n * k + 8 * n * k + 4 * n * e + 4 * n * e,
     }
