@@ -45,6 +45,9 @@ ROUTER_CASES = {
     # E not a multiple of 64 with five experts per lane
     "softmax_e320_k10": (1024, 320, 10, "softmax", None, None, True, 2.0, False, False, 0),
     "ties_group_e512_g16_k12": (1024, 512, 12, "sigmoid", 16, 5, True, 1.0, True, False, 6),
+    # two experts per lane with ties and a bias; four per lane with E not a multiple of 64
+    "ties_sigmoid_bias_e128_k8": (2048, 128, 8, "sigmoid", None, None, True, 2.5, True, False, 4),
+    "ties_softmax_e200_k7": (2048, 200, 7, "softmax", None, None, False, 1.0, False, False, 3),
 }
 
 
