@@ -786,7 +786,10 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 // 128 x 256 tiles, four waves, two workgroups per CU; gate_up over a long
 // contraction (D >= 4096) runs the same tile as eight 64 x 64 waves with 64-wide
 // k-steps (whole 128-byte rows per copy) and three stages at one workgroup per CU
-// (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower). dgu runs the
+// (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower); down over a short
+// contraction (H <= 1024) runs 256 x 256 tiles of eight 64 x 128 waves with 64-wide
+// k-steps, two stages, one workgroup per CU (Kimi 0.81 -> 0.76-0.77 ms in the layer step;
+// at H = 2048 it is 6 % slower, and gate_up gains nothing from it). dgu runs the
 // forward tile too: its epilogue reads g and u and writes dg and du, and with two
 // workgroups per CU one's epilogue overlaps the other's MFMAs (against one
 // eight-wave 128 x 512 workgroup: DSv3 3.15 -> 2.81 ms, Kimi -1.5 %). dx and dW run
@@ -802,6 +805,12 @@ static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
     if constexpr (MODE == kFwdGateUp && ACT == kSwiGLU) {
       if (p.D >= 4096) {  // long contractions: 128-byte rows per stage, eight 64 x 64 waves
         launch_cfg<MODE, 8, 2, 4, 4, 3, true, 1, ACT, 64>(p, R, stream);
+        return;
+      }
+    }
+    if constexpr (MODE == kFwdDown && ACT == kSwiGLU) {
+      if (p.H <= 1024) {  // short contractions: 256 x 256 tiles, whole 128-byte rows per copy
+        launch_cfg<MODE, 8, 4, 4, 8, 2, true, 1, ACT, 64>(p, R, stream);
         return;
       }
     }
