@@ -219,6 +219,9 @@ GEMM_CASES = {
     "tails_d2880_h2880": (3, 2880, 2880, [300, 0, 77]),
     # D a multiple of 384: the dx kernel's 128 x 384 tile, w1 half parked in registers
     "dx_d768_h320": (5, 768, 320, [90, 0, 300, 129, 17]),
+    # tall experts (875 rows each on average): gate_up and down on their 256 x 256 tiles with
+    # 64-wide k-steps, partial last n-tiles (2H = 384, D = 320) and an empty expert
+    "tall_tails_d320_h192": (4, 320, 192, [1000, 0, 1500, 1000]),
 }
 
 
@@ -283,18 +286,20 @@ def test_grouped_swiglu_deterministic(dev):
 # tensor's largest magnitude (dx sums two bf16 halves, so a flip in one half
 # can exceed the ulp of the element itself). Shapes cover
 # the dx kernel's register park (D % 384 == 0) and its in-memory park (D % 512 == 0).
-BIT_CASES = {
-    "d768_h512": (16, 768, 512, 3),
-    "d1024_h512": (8, 1024, 512, 5),
+BIT_CASES = {  # experts, D, H, seed, expert rows drawn from [lo, hi)
+    "d768_h512": (16, 768, 512, 3, 0, 400),
+    "d1024_h512": (8, 1024, 512, 5, 0, 400),
+    # tall experts: the forward on its 256 x 256 tiles
+    "tall_d768_h512": (6, 768, 512, 7, 700, 1400),
 }
 
 
 @pytest.mark.parametrize("name", list(BIT_CASES))
 def test_grouped_swiglu_vs_torch_grouped_mm(dev, name):
-    e, d, h, seed = BIT_CASES[name]
+    e, d, h, seed, lo, hi = BIT_CASES[name]
     banner(f"grouped swiglu vs torch._grouped_mm {name}")
     g = torch.Generator().manual_seed(seed)
-    counts = torch.randint(0, 400, (e,), generator=g)
+    counts = torch.randint(lo, hi, (e,), generator=g)
     counts[1] = 0
     x, w1, w2, w3, dy, cnt = _gemm_inputs(e, d, h, counts.tolist(), seed=seed)
     o = ops()
