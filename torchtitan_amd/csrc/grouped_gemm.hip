@@ -788,11 +788,11 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 // k-steps (whole 128-byte rows per copy) and three stages at one workgroup per CU
 // (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower). 256 x 256 tiles of
 // eight 64 x 128 waves with 64-wide k-steps, two stages, one workgroup per CU pay where
-// the experts are tall: down over a short contraction (H <= 1024) with at least 512 rows
-// per expert on average (Kimi, 512: 0.81 -> 0.76-0.77 ms in the layer step; at DSv3, H =
-// 2048 and 256 rows, 6 % slower), gate_up from 768 rows per expert (32K Kimi tokens, 1024
-// rows: 2.95 -> 2.72 ms; at 512 rows within 2 %), with either epilogue (gpt-oss-20b, 2048
-// rows per expert: 2.55 -> 2.27-2.44 ms). dgu runs the
+// the experts are tall: down from 512 rows per expert on average (Kimi, 512: 0.81 -> 0.76-
+// 0.77 ms in the layer step; gpt-oss-20b, 2048 rows, H = 2880: 1.21-1.23 -> 1.04-1.16 ms;
+// at DSv3, 256 rows, 6 % slower), gate_up from 768 rows per expert (32K Kimi tokens, 1024
+// rows: 2.95 -> 2.72 ms; at 512 rows within 2 %; gpt-oss-20b 2.55 -> 2.27-2.44 ms), with
+// either epilogue. dgu runs the
 // forward tile too: its epilogue reads g and u and writes dg and du, and with two
 // workgroups per CU one's epilogue overlaps the other's MFMAs (against one
 // eight-wave 128 x 512 workgroup: DSv3 3.15 -> 2.81 ms, Kimi -1.5 %). dx and dW run
@@ -821,8 +821,8 @@ static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
         return;
       }
     }
-    if constexpr (MODE == kFwdDown && ACT == kSwiGLU) {
-      if (p.H <= 1024 && R >= 512 * (int64_t)p.E) {  // short contractions over tall experts
+    if constexpr (MODE == kFwdDown) {
+      if (R >= 512 * (int64_t)p.E) {  // tall experts
         launch_cfg<MODE, 8, 4, 4, 8, 2, true, 1, ACT, 64>(p, R, stream);
         return;
       }
