@@ -788,11 +788,11 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 // k-steps (whole 128-byte rows per copy) and three stages at one workgroup per CU
 // (DSv3, D = 7168: 6.25 -> 5.46 ms; at D = 2304 it is 6 % slower). 256 x 256 tiles of
 // eight 64 x 128 waves with 64-wide k-steps, two stages, one workgroup per CU pay where
-// the experts are tall: down from 512 rows per expert on average (Kimi, 512: 0.81 -> 0.76-
-// 0.77 ms in the layer step; gpt-oss-20b, 2048 rows, H = 2880: 1.21-1.23 -> 1.04-1.16 ms;
-// at DSv3, 256 rows, 6 % slower), gate_up from 768 rows per expert (32K Kimi tokens, 1024
-// rows: 2.95 -> 2.72 ms; at 512 rows within 2 %; gpt-oss-20b 2.55 -> 2.27-2.44 ms), with
-// either epilogue. dgu runs the
+// the experts are tall, from 512 rows per expert on average, with either epilogue: down
+// (Kimi, 512 rows: 0.81 -> 0.76-0.77 ms in the layer step; gpt-oss-20b, 2048 rows, H = 2880:
+// 1.21-1.23 -> 1.04-1.16 ms; at DSv3, 256 rows, 6 % slower) and gate_up (Kimi 1.58-1.59 ->
+// 1.54-1.55 ms in the layer step; 32K Kimi tokens, 1024 rows: 2.95 -> 2.72 ms; gpt-oss-20b
+// 2.55 -> 2.27-2.44 ms). dgu runs the
 // forward tile too: its epilogue reads g and u and writes dg and du, and with two
 // workgroups per CU one's epilogue overlaps the other's MFMAs (against one
 // eight-wave 128 x 512 workgroup: DSv3 3.15 -> 2.81 ms, Kimi -1.5 %). dx and dW run
@@ -810,13 +810,13 @@ static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
         launch_cfg<MODE, 8, 2, 4, 4, 3, true, 1, ACT, 64>(p, R, stream);
         return;
       }
-      if (R >= 768 * (int64_t)p.E) {  // tall experts: 256 x 256 tiles, whole 128-byte rows
+      if (R >= 512 * (int64_t)p.E) {  // tall experts: 256 x 256 tiles, whole 128-byte rows
         launch_cfg<MODE, 8, 4, 4, 8, 2, true, 1, ACT, 64>(p, R, stream);
         return;
       }
     }
     if constexpr (MODE == kFwdGateUp && ACT == kOssGLU) {
-      if (R >= 768 * (int64_t)p.E) {  // tall experts (gpt-oss-20b: 2048 rows per expert)
+      if (R >= 512 * (int64_t)p.E) {  // tall experts (gpt-oss-20b: 2048 rows per expert)
         launch_cfg<MODE, 8, 4, 4, 8, 2, true, 1, ACT, 64>(p, R, stream);
         return;
       }
