@@ -54,6 +54,7 @@
 
 #include "common.h"
 
+
 namespace moe {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -197,6 +198,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
   constexpr int CPW_P = BM * BK / 512 / NW, CPW_Q = BN * BK / 512 / NW;  // 1 KB copies per wave and stage
   static_assert(CPW_P * 512 * NW == BM * BK && CPW_Q * 512 * NW == BN * BK, "copies per wave");
   constexpr int CPW = CPW_P + CPW_Q;
+  constexpr int kIlvSpan = 4;  // pipelined k-steps: the slots the next stage's copies spread over
   constexpr int CHP = BM / 8, CHQ = BN / 8;          // 16-byte chunks per k-row (k-major tiles)
   static_assert(BM % 64 == 0 && BN % 64 == 0 && CPW <= 30, "tile");
   static_assert(TN % 2 == 0 && (MODE != kFwdGateUp || TN % 4 == 0), "epilogue block pairs");
@@ -366,11 +368,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     }
   };
 
-  // stage kt of tile r into LDS buffer s
-  auto issue = [&](const TileRef& r, int kt, int s) {
+  // copy c (P copies first, then Q) of stage kt of tile r into LDS buffer s
+  auto issue_copy = [&](const TileRef& r, int kt, int s, int c) {
     const int k0 = kt * BK;
-#pragma unroll
-    for (int b = 0; b < CPW_P; ++b) {
+    if (c < CPW_P) {
+      const int b = c;
       const uint16_t* src = srcP[b] + kt * stepP;
       if constexpr (T::kPT) {
         if (r.seg0 + k0 + klP[b] >= r.seg1 || (TAIL && !inP[b])) src = (const uint16_t*)kZeroRow;
@@ -378,9 +380,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
         if (klP[b] >= r.seg1) src = (const uint16_t*)kZeroRow;
       }
       dma16(src, lds_addr(&sP[s][(wv * CPW_P + b) * 512]));
-    }
-#pragma unroll
-    for (int b = 0; b < CPW_Q; ++b) {
+    } else {
+      const int b = c - CPW_P;
       const uint16_t* src = srcQ[b] + kt * stepQ;
       if constexpr (MODE == kBwdDx) {
         if (k0 >= H) src = srcQ3[b] + (int64_t)(k0 - H) * p.w13_rstride;
@@ -391,6 +392,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       if (TAIL && !inQ[b]) src = (const uint16_t*)kZeroRow;
       dma16(src, lds_addr(&sQ[s][(wv * CPW_Q + b) * 512]));
     }
+  };
+  // stage kt of tile r into LDS buffer s
+  auto issue = [&](const TileRef& r, int kt, int s) {
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) issue_copy(r, kt, s, c);
   };
 
   // One stream of copy stages across this workgroup's tiles: the copy cursor
@@ -410,10 +416,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
     }
     ik = 0;
   };
-  auto issue_next = [&]() {
-    issue(ir, ik, gi % NS);
+  auto advance = [&]() {
     ++gi;
     if (++ik == ir.nk) seek(ct_i + G);
+  };
+  auto issue_next = [&]() {
+    issue(ir, ik, gi % NS);
+    advance();
   };
   seek(lb);
 #pragma unroll
@@ -495,15 +504,79 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
           }
         }
       };
+      // Software-pipelined k-step: slots of 2 x TM MFMAs (two 16-column blocks of one
+      // 32-wide k half); each slot first reads the next slot's B fragments from LDS,
+      // then issues its MFMAs, then its share of the next stage's copies (nx: there is
+      // a next stage, into LDS buffer sn), which are spread over the first kIlvSpan
+      // slots. In the plain schedule every wave issues all its copies right after the
+      // barrier and each pair of B fragments is waited for right before its MFMAs: a
+      // copy issue that stalls on a full texture queue then holds every MFMA of the
+      // wave behind it, and the LDS latency is exposed once per slot. Same MFMAs in
+      // the same order as the plain schedule, so the accumulators are bit-identical.
+      auto compute_ilv = [&](int s, bool nx, int sn) {
+        const uint16_t* cP = sP[s];
+        const uint16_t* cQ = sQ[s];
+        constexpr int JP = TN / 2, NSL = KH * JP, SPAN = kIlvSpan < NSL ? kIlvSpan : NSL;
+        bf16x8_t af[TM], bq[2][2];
+        auto load_a = [&](int kh) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            if (!decltype(full)::value && i >= tmv) continue;
+            if constexpr (T::kPT) af[i] = frag_km<BM>(cP, wm * WM + i * 16, lane);
+            else af[i] = frag_rm<BK>(cP, wm * WM + i * 16 + ml, lane, kh);
+          }
+        };
+        auto load_b = [&](int sl) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int j = 2 * (sl % JP) + h;
+            if constexpr (T::kQT) bq[sl & 1][h] = frag_km<BN>(cQ, wn * WN + j * 16, lane);
+            else bq[sl & 1][h] = frag_rm<BK>(cQ, wn * WN + j * 16 + ml, lane, sl / JP);
+          }
+        };
+        load_a(0);
+        load_b(0);
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl) {
+          const int kh = sl / JP, jp = sl % JP;
+          if (sl > 0 && jp == 0) load_a(kh);
+          if (sl + 1 < NSL) load_b(sl + 1);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+              if (!decltype(full)::value && i >= tmv) continue;
+              acc[i][2 * jp + h] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[sl & 1][h], af[i], acc[i][2 * jp + h], 0, 0, 0);
+            }
+          }
+#pragma unroll
+          for (int c = 0; c < CPW; ++c)
+            if (nx && c * SPAN / CPW == sl) issue_copy(ir, ik, sn, c);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      // Pipelined: the tiles with 64-wide k-steps (forward modes only). With 32-wide
+      // k-steps (the 128 x 256 forward tile, dgu, dx, dW) the plain schedule measured
+      // faster. Waves with a partial row block keep the plain schedule too (their
+      // conditional MFMAs with the pipeline's registers spill).
+      constexpr bool kIlv = BK == 64 && decltype(full)::value;
       for (int kt = 0; kt < nk; ++kt) {
         // stage gc has landed in every wave once at most the one stage issued after it
         // is outstanding (stores of the previous epilogue only add to the count); the
         // barrier also retires every wave's reads of the buffer refilled next
         if (NS == 3 && gi - gc >= 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(CPW) : "memory");
         else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (ct_i < total_tiles) issue_next();
-        if (MODE == kBwdDx && ACT == kSwiGLU && kt == kt_half) park_dx_half();
-        if (decltype(full)::value || tmv > 0) compute(gc % NS);
+        if constexpr (kIlv) {
+          const bool nx = ct_i < total_tiles;
+          if (MODE == kBwdDx && ACT == kSwiGLU && kt == kt_half) park_dx_half();
+          compute_ilv(gc % NS, nx, gi % NS);
+          if (nx) advance();
+        } else {
+          if (ct_i < total_tiles) issue_next();
+          if (MODE == kBwdDx && ACT == kSwiGLU && kt == kt_half) park_dx_half();
+          if (decltype(full)::value || tmv > 0) compute(gc % NS);
+        }
         ++gc;
       }
     };
@@ -543,29 +616,36 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
               const int jj = 2 * jp + h2;
-              const int hc = nt * (BN / 2) + wn * (WN / 2) + jj * 16 + nq;
-              float gv[4], uv[4], hv[4];
-              if constexpr (ACT == kOssGLU) {
-                // h1 = bf16(x . mlp1^T) + bias (bf16 add), then the clamped SwiGLU
-                const uint4 bw = bias1[jj];  // (glu, linear) x 4 columns
-                const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
+              // Column pairs are rounded to packed bf16 once; the fp32 operands of the
+              // activation are read back from the packed words (exact), so each value
+              // takes one NaN-canonicalizing conversion. The epilogue is VALU-bound:
+              // rounding each value to fp32-held bf16 and then packing it again cost
+              // a third of its instructions.
+              uint32_t gq[2], uq[2], hq[2];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                  gv[q] = round_bf(round_bf(acc[i][2 * jj][q]) + bf_lo(bb[q]));
-                  uv[q] = round_bf(round_bf(acc[i][2 * jj + 1][q]) + bf_hi(bb[q]));
-                  hv[q] = oss_glu(gv[q], uv[q], p.limit, p.alpha);
+              for (int q2 = 0; q2 < 2; ++q2) {
+                const int q = 2 * q2;
+                uint32_t gw = pack_bf2(acc[i][2 * jj][q], acc[i][2 * jj][q + 1]);
+                uint32_t uw = pack_bf2(acc[i][2 * jj + 1][q], acc[i][2 * jj + 1][q + 1]);
+                if constexpr (ACT == kOssGLU) {
+                  // h1 = bf16(x . mlp1^T) + bias (bf16 add), then the clamped SwiGLU;
+                  // bias word of column c: (glu, linear)
+                  const uint4 bw = bias1[jj];
+                  const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
+                  gw = pack_bf2(bf_lo(gw) + bf_lo(bb[q]), bf_hi(gw) + bf_lo(bb[q + 1]));
+                  uw = pack_bf2(bf_lo(uw) + bf_hi(bb[q]), bf_hi(uw) + bf_hi(bb[q + 1]));
+                  hq[q2] = pack_bf2(oss_glu(bf_lo(gw), bf_lo(uw), p.limit, p.alpha),
+                                    oss_glu(bf_hi(gw), bf_hi(uw), p.limit, p.alpha));
+                } else {
+                  const uint32_t sw = pack_bf2(silu_f(bf_lo(gw)), silu_f(bf_hi(gw)));  // bf16(silu(g))
+                  hq[q2] = pack_bf2(bf_lo(sw) * bf_lo(uw), bf_hi(sw) * bf_hi(uw));
                 }
-              } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                  gv[q] = round_bf(acc[i][2 * jj][q]);
-                  uv[q] = round_bf(acc[i][2 * jj + 1][q]);
-                  hv[q] = round_bf(silu_f(gv[q])) * uv[q];
-                }
+                gq[q2] = gw;
+                uq[q2] = uw;
               }
-              pg[h2] = pack4(gv);
-              pu[h2] = pack4(uv);
-              ph[h2] = pack4(hv);
+              pg[h2] = make_uint2(gq[0], gq[1]);
+              pu[h2] = make_uint2(uq[0], uq[1]);
+              ph[h2] = make_uint2(hq[0], hq[1]);
             }
             const int hc = nt * (BN / 2) + wn * (WN / 2) + jp * 32 + g8;
             const uint4 sg = span64(pg[0], pg[1], lane), su = span64(pu[0], pu[1], lane),
@@ -678,7 +758,19 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
               const float dh = (q & 1) ? bf_hi(dhw[q >> 1]) : bf_lo(dhw[q >> 1]);
               const float gv = (q & 1) ? bf_hi(gww[q >> 1]) : bf_lo(gww[q >> 1]);
               const float uv = (q & 1) ? bf_hi(uww[q >> 1]) : bf_lo(uww[q >> 1]);
-              if constexpr (ACT == kOssGLU) {
+              if constexpr (ACT == kSwiGLU) {
+                // column pairs: the two bf16 roundings of a pair are one conversion
+                // (the epilogue is VALU-bound), read back exactly from the packed word
+                if (q & 1) continue;
+                const float dh1 = bf_hi(dhw[q >> 1]), gv1 = bf_hi(gww[q >> 1]), uv1 = bf_hi(uww[q >> 1]);
+                const uint32_t slw = pack_bf2(silu_f(gv), silu_f(gv1));  // bf16(silu(g))
+                const uint32_t dsw = pack_bf2(dh * uv, dh1 * uv1);       // bf16(dh . u)
+                du[q] = dh * bf_lo(slw);
+                du[q + 1] = dh1 * bf_hi(slw);
+                const float sg = 1.0f / (1.0f + expf(-gv)), sg1 = 1.0f / (1.0f + expf(-gv1));
+                dg[q] = bf_lo(dsw) * sg * (1.0f + gv * (1.0f - sg));
+                dg[q + 1] = bf_hi(dsw) * sg1 * (1.0f + gv1 * (1.0f - sg1));
+              } else {
                 // autograd of oss_glu, each bf16 op's gradient rounded to bf16
                 const float L = p.limit, al = p.alpha;
                 const float xg = gv > L ? L : gv;
@@ -692,12 +784,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
                 const float dxg = round_bf(da * s) + round_bf(dz * al);
                 dg[q] = gv <= L ? dxg : 0.f;                           // clamp(max=L) backward
                 du[q] = (uv >= -L && uv <= L) ? dl : 0.f;              // clamp(-L, L) backward
-              } else {
-                const float sl = round_bf(silu_f(gv));
-                const float dsl = round_bf(dh * uv);
-                du[q] = dh * sl;
-                const float sg = 1.0f / (1.0f + expf(-gv));
-                dg[q] = dsl * sg * (1.0f + gv * (1.0f - sg));
               }
             }
             const int64_t o2 = (int64_t)r * (2 * H) + hh;
