@@ -291,6 +291,8 @@ BIT_CASES = {  # experts, D, H, seed, expert rows drawn from [lo, hi)
     "d1024_h512": (8, 1024, 512, 5, 0, 400),
     # tall experts: the forward on its 256 x 256 tiles
     "tall_d768_h512": (6, 768, 512, 7, 700, 1400),
+    # H = 2048: dw13's 16 m-tiles per expert take the blocked tile order
+    "dw13_blocked_d512_h2048": (4, 512, 2048, 9, 100, 500),
 }
 
 

@@ -285,6 +285,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
       const int mtiles = (r.seg1 - r.seg0 + BM - 1) / BM;
       r.nt = local / mtiles;
       r.mt = local - r.nt * mtiles;
+    } else if (MODE == kBwdDw13 && MT >= 16 && MT % 4 == 0) {
+      // blocks of 4 m-tiles by every n-tile, so that the 32 consecutive tiles one XCD
+      // runs together share 4 dgu slices and 8 x slices instead of 16 and 2 (DSv3,
+      // 16 m-tiles by 28 n-tiles per expert: 6.85 -> 6.37 ms; no gain for dw2, and
+      // at 8 m-tiles, Kimi, the plain order already shares both operands)
+      const int blk = local / (NT * 4), rem = local - blk * NT * 4;
+      r.nt = rem / 4;
+      r.mt = blk * 4 + (rem - r.nt * 4);
     } else {
       r.nt = local / MT;
       r.mt = local - r.nt * MT;
