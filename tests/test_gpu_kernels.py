@@ -282,7 +282,9 @@ def test_grouped_swiglu_deterministic(dev):
 # moe.py:53-70). Both accumulate in fp32 and round to bf16 at the same points;
 # at the benchmark shapes every element is identical, at other shapes torch's
 # GEMM may order the k sum differently, which flips a rounding in a few elements:
-# at most 1e-4 of the elements may differ, by at most one bf16 ulp of the
+# at these shapes at most 1e-4 of the elements may differ (where torch splits a
+# long k sum, as at D >= 4096 with a few hundred rows per expert, a few tenths of
+# a percent do), by at most one bf16 ulp of the
 # tensor's largest magnitude (dx sums two bf16 halves, so a flip in one half
 # can exceed the ulp of the element itself). Shapes cover
 # the dx kernel's register park (D % 384 == 0) and its in-memory park (D % 512 == 0).
