@@ -915,6 +915,14 @@ static void launch_mode(const GemmParams& p, int64_t R, hipStream_t stream) {
         return;
       }
     }
+    if constexpr (MODE == kFwdDown && ACT == kSwiGLU) {
+      // short experts with a long contraction (DSv3: H = 2048, 256 rows per expert):
+      // gate_up's long-contraction tile (DSv3 down 2.72-2.74 -> 2.54-2.55 ms in the layer)
+      if (p.H >= 2048 && R < 512 * (int64_t)p.E) {
+        launch_cfg<MODE, 8, 2, 4, 4, 3, true, 1, ACT, 64>(p, R, stream);
+        return;
+      }
+    }
     if constexpr (MODE == kFwdDown) {
       if (R >= 512 * (int64_t)p.E) {  // tall experts
         launch_cfg<MODE, 8, 4, 4, 8, 2, true, 1, ACT, 64>(p, R, stream);
