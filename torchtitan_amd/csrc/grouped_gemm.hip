@@ -886,7 +886,9 @@ static void launch_cfg(const GemmParams& p, int64_t R, hipStream_t stream) {
 // (Kimi, 512 rows: 0.81 -> 0.76-0.77 ms in the layer step; gpt-oss-20b, 2048 rows, H = 2880:
 // 1.21-1.23 -> 1.04-1.16 ms; at DSv3, 256 rows, 6 % slower) and gate_up (Kimi 1.58-1.59 ->
 // 1.54-1.55 ms in the layer step; 32K Kimi tokens, 1024 rows: 2.95 -> 2.72 ms; gpt-oss-20b
-// 2.55 -> 2.27-2.44 ms). dgu runs the
+// 2.55 -> 2.27-2.44 ms). Both 64-wide configurations run the software-pipelined
+// k-step (compute_ilv); down over a long contraction with short experts (H >= 2048,
+// DSv3) takes gate_up's long-contraction tile. dgu runs the
 // forward tile too: its epilogue reads g and u and writes dg and du, and with two
 // workgroups per CU one's epilogue overlaps the other's MFMAs (against one
 // eight-wave 128 x 512 workgroup: DSv3 3.15 -> 2.81 ms, Kimi -1.5 %). dx and dW run
