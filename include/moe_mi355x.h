@@ -224,6 +224,14 @@ int moe_grouped_gemm_bwd_dw13(const uint16_t* dgu, const uint16_t* x, const int6
 int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, const int64_t* counts,
                              int64_t n_rows, int32_t n_experts, int32_t dim, int32_t hidden,
                              uint16_t* dw2, moe_stream_t stream);
+/* No counterpart in the reference; for tests: the pointwise arithmetic of the
+ * gate_up and bwd_dgu SwiGLU epilogues on its own. For bf16 g[0..n), writes fp32
+ * silu[i] = g/(1+exp(-g)) and sigmoid[i] = 1/(1+exp(-g)) exactly as those
+ * epilogues compute them before rounding (a pair 2i, 2i+1 takes the fast form
+ * when both lie in its range, as a block of the epilogues does), so that they can
+ * be compared with torch's silu and sigmoid over every bf16 value. */
+int moe_swiglu_pointwise_f32(const uint16_t* g, float* silu, float* sigmoid, int64_t n,
+                             moe_stream_t stream);
 
 /* ---- fp32 experts: _run_experts_for_loop in the input dtype --------------
  * Replace the per-expert fp32 matmuls of torchtitan/models/common/moe.py:24-50

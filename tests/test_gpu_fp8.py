@@ -76,6 +76,8 @@ def test_fp8_gemm_entry_points_match_emulation(dev):
     eg = per_expert(lambda i, sl: R._fp8_mm(qx[sl], sx[sl], qw1[i], sw1[i]).bfloat16())
     eu = per_expert(lambda i, sl: R._fp8_mm(qx[sl], sx[sl], qw3[i], sw3[i]).bfloat16())
     assert _rel(g_, eg) <= GEMM_TOL and _rel(u_, eu) <= GEMM_TOL
+    # the epilogue's h from its own g and u is torch's silu(g) * u bit for bit
+    assert torch.equal(h_, F.silu(g_) * u_)
     # down
     qh, sh = R.quant_fp8_rows(hh)
     qw2, sw2 = R.quant_fp8_rows(w2)

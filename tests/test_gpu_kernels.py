@@ -419,3 +419,110 @@ def test_layer_counts_routing_once(dev):
         assert len(seen) == 1 and torch.equal(seen[0].float(), moe.tokens_per_expert)
     finally:
         handle.remove()
+
+
+# Every bf16 bit pattern, in-range values (where the epilogues use the reciprocal
+# form: -80 <= g <= 3.38e38) first so that those pieces take that form, the rest
+# (below -80, infinities, NaNs) after.
+def _bf16_patterns_split():
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    v = bits.view(torch.bfloat16)
+    f = v.float()
+    fast = (f >= -80.0) & (f <= 3.38e38)
+    return v[fast], v[~fast]
+
+
+def test_swiglu_pointwise_every_bf16(dev):
+    """The SwiGLU epilogues' silu and sigmoid (moe.py:62-67 through torch's silu
+    and its backward) for all 65536 bf16 inputs, in fp32 before any rounding,
+    equal torch's F.silu and torch.sigmoid of the same values on the device: the
+    reciprocal-and-correction form is the IEEE quotient wherever it is used."""
+    banner("swiglu pointwise, every bf16 input")
+    from torchtitan_amd import _lib
+
+    fast, rest = _bf16_patterns_split()
+    assert fast.numel() % 2 == 0
+    for order in ("split", "natural"):
+        g = torch.cat([fast, rest]) if order == "split" else torch.cat([fast, rest]).view(torch.int16).sort().values.view(torch.bfloat16)
+        g = g.to(dev)
+        silu = torch.empty(g.numel(), dtype=torch.float32, device=dev)
+        sig = torch.empty_like(silu)
+        _lib.call("moe_swiglu_pointwise_f32", g.data_ptr(), silu.data_ptr(), sig.data_ptr(), g.numel(),
+                  _lib.stream_of(g))
+        ref_silu = torch.nn.functional.silu(g.float())
+        ref_sig = torch.sigmoid(g.float())
+        for name, a, b in (("silu", silu, ref_silu), ("sigmoid", sig, ref_sig)):
+            same = (a.view(torch.int32) == b.view(torch.int32)) | (torch.isnan(a) & torch.isnan(b))
+            bad = (~same).nonzero().flatten()[:8].cpu()
+            assert bad.numel() == 0, (order, name, [(float(g[i].float()), float(a[i]), float(b[i])) for i in bad])
+
+
+def _fill_rows(vals, rows, cols):
+    """vals repeated to fill [rows, cols] row by row."""
+    n = rows * cols
+    rep = (n + vals.numel() - 1) // vals.numel()
+    return vals.repeat(rep)[:n].view(rows, cols)
+
+
+@pytest.mark.parametrize("rows", [320, 1280])
+def test_gate_up_epilogue_every_bf16(dev, rows):
+    """gate_up with one-hot token rows, so that g = x.w1^T is w1's entries exactly
+    and covers every finite bf16 value: h equals torch's silu(g) * u bit for bit,
+    in the pieces that take the reciprocal form (rows 0-207 of each 320) and in
+    the ones that divide (rows 208-319)."""
+    banner(f"gate_up epilogue, every finite bf16 g, {rows} rows")
+    from torchtitan_amd import _lib
+
+    d, h = 320, 256
+    fast, rest = _bf16_patterns_split()
+    rest = rest[torch.isfinite(rest.float())]
+    gt = torch.cat([_fill_rows(fast, 208, h), _fill_rows(rest, 112, h)])  # [320, H]: g of token row r
+    gen = torch.Generator().manual_seed(11)
+    w1 = gt.t().contiguous().view(1, h, d)
+    w3 = (torch.randn(1, h, d, generator=gen) * 2).bfloat16()
+    x = torch.zeros(rows, d, dtype=torch.bfloat16)
+    x[torch.arange(rows), torch.arange(rows) % d] = 1.0
+    x, w1, w3 = x.to(dev), w1.to(dev), w3.to(dev)
+    counts = torch.tensor([rows], dtype=torch.int64, device=dev)
+    g = torch.empty(rows, h, dtype=torch.bfloat16, device=dev)
+    u, hh = torch.empty_like(g), torch.empty_like(g)
+    _lib.call("moe_grouped_gemm_gate_up", x.data_ptr(), w1.data_ptr(), w3.data_ptr(), counts.data_ptr(), rows, 1,
+              d, h, g.data_ptr(), u.data_ptr(), hh.data_ptr(), _lib.stream_of(x))
+    # g is w1's entry itself, except that -0 comes out +0 and the MFMA may flush
+    # subnormal operands
+    gt_rows = gt.to(dev)[torch.arange(rows, device=dev) % d]
+    tiny = gt_rows.float().abs() < 2.0 ** -126
+    assert bool(((g.view(torch.int16) == gt_rows.view(torch.int16)) | tiny).all())
+    ref = torch.nn.functional.silu(g) * u
+    same = (hh.view(torch.int16) == ref.view(torch.int16)) | (torch.isnan(hh) & torch.isnan(ref))
+    assert bool(same.all()), int((~same).sum())
+
+
+@pytest.mark.parametrize("rows", [320, 1280])
+def test_dgu_epilogue_every_bf16(dev, rows):
+    """bwd_dgu with one-hot output-gradient rows, so that dh = dy.w2 is w2's entries
+    exactly, on g covering every bf16 value (NaNs and infinities included): dg and
+    du equal torch's autograd of silu(g) * u bit for bit (NaNs as NaNs)."""
+    banner(f"dgu epilogue, every bf16 g, {rows} rows")
+    from torchtitan_amd import _lib
+
+    d, h = 320, 256
+    fast, rest = _bf16_patterns_split()
+    gt = torch.cat([_fill_rows(fast, 208, h), _fill_rows(rest, 112, h)])
+    gen = torch.Generator().manual_seed(12)
+    g = gt[torch.arange(rows) % d].contiguous()
+    u = (torch.randn(rows, h, generator=gen) * 2).bfloat16()
+    w2 = (torch.randn(1, d, h, generator=gen) * 2).bfloat16()
+    dy = torch.zeros(rows, d, dtype=torch.bfloat16)
+    dy[torch.arange(rows), torch.arange(rows) % d] = 1.0
+    g, u, w2, dy = g.to(dev), u.to(dev), w2.to(dev), dy.to(dev)
+    counts = torch.tensor([rows], dtype=torch.int64, device=dev)
+    dgu = torch.empty(rows, 2 * h, dtype=torch.bfloat16, device=dev)
+    _lib.call("moe_grouped_gemm_bwd_dgu", dy.data_ptr(), w2.data_ptr(), g.data_ptr(), u.data_ptr(),
+              counts.data_ptr(), rows, 1, d, h, dgu.data_ptr(), _lib.stream_of(dy))
+    dh = w2[0][torch.arange(rows, device=dev) % d]
+    gr, ur = g.clone().requires_grad_(True), u.clone().requires_grad_(True)
+    (torch.nn.functional.silu(gr) * ur).backward(dh)
+    for name, a, b in (("dg", dgu[:, :h], gr.grad), ("du", dgu[:, h:], ur.grad)):
+        same = (a.view(torch.int16) == b.view(torch.int16)) | (torch.isnan(a) & torch.isnan(b))
+        assert bool(same.all()), (name, int((~same).sum()))

@@ -207,6 +207,8 @@ def test_mxfp8_gemm_entry_points_match_emulation(dev):
     print(f"[case] gate_up g {_rel(g_, eg):.2e} u {_rel(u_, eu):.2e}", flush=True)
     assert _rel(g_, eg) <= GEMM_TOL and _rel(u_, eu) <= GEMM_TOL
     assert _rel(h_, F.silu(eg) * eu) <= GEMM_TOL
+    # the epilogue's h from its own g and u is torch's silu(g) * u bit for bit
+    assert torch.equal(h_, F.silu(g_) * u_)
     # down
     qh, sh = R.quant_mxfp8(hh)
     qw2, sw2 = R.quant_mxfp8(w2)

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, list] = {
     "moe_grouped_gemm_bwd_dx": [P, P, P, P, I64, I32, I32, I32, P, P],
     "moe_grouped_gemm_bwd_dw13": [P, P, P, I64, I32, I32, I32, P, P, P],
     "moe_grouped_gemm_bwd_dw2": [P, P, P, I64, I32, I32, I32, P, P],
+    "moe_swiglu_pointwise_f32": [P, P, P, I64, P],
     "moe_grouped_gemm_f32_gate_up": [P, P, P, P, I64, I32, I32, I32, P, P, P, P],
     "moe_grouped_gemm_f32_down": [P, P, P, I64, I32, I32, I32, P, P],
     "moe_grouped_gemm_f32_bwd_dgu": [P, P, P, P, P, I64, I32, I32, I32, P, P, P],

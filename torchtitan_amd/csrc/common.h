@@ -57,6 +57,38 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// silu(g) = g / d and sigmoid(g) = 1 / d with d = 1 + exp(-g), the quotients rounded
+// as IEEE division rounds them (torch's kernels divide), without the general
+// division's scaling and fix-up steps: the hardware reciprocal estimate refined by one
+// Newton step on fused multiply-adds, then the quotient corrected once by its exact
+// fused residual (Markstein, IBM J. Res. Dev. 34(1), 1990). For g in [-80, 3.38e38]
+// d lies in [1, 2^116] and nothing over- or underflows; the results equal IEEE
+// division there for every bf16 g (a GPU test compares all 65536 of them with
+// torch's silu and sigmoid, -0 included), and a NaN g gives NaN either way. A piece of values
+// with any g below -80 or above 3.38e38 in any lane takes the division (kFast false).
+struct SiluSig { float silu, sig; };
+__device__ __forceinline__ bool silu_fast_range(float g_min, float g_max) {
+  return g_min >= -80.0f && g_max <= 3.38e38f;  // fminf / fmaxf drop NaN
+}
+// the same for every active lane of the wave, so that the choice is a scalar branch
+// between two straight paths rather than both paths under lane masks
+__device__ __forceinline__ bool silu_fast_wave(float g_min, float g_max) {
+  return __builtin_expect(__builtin_amdgcn_ballot_w64(!silu_fast_range(g_min, g_max)) == 0, 1);
+}
+__device__ __forceinline__ float silu_den(float g) { return 1.0f + expf(-g); }
+template <bool kFast>
+__device__ __forceinline__ SiluSig silu_sig(float g, float d) {
+  if constexpr (kFast) {
+    float y = __builtin_amdgcn_rcpf(d);
+    y = fmaf(fmaf(-d, y, 1.0f), y, y);
+    const float q = g * y;
+    // the quotient has g's sign (d > 0); the correction alone would turn -0 into +0
+    return {copysignf(fmaf(fmaf(-d, q, g), y, q), g), y};
+  } else {
+    return {g / d, 1.0f / d};
+  }
+}
+
 // Epilogue stores in 64-byte row pieces. An accumulator tile leaves lane (r, g),
 // r = lane % 16, g = lane / 16, with 4 consecutive columns 4g .. 4g + 3 of row r
 // in each 16-column block; for two adjacent blocks (lo, hi) packed to bf16, this

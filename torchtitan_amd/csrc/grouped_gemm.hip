@@ -617,7 +617,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = row0 + wm * WM + i * 16 + ml;
-        if (r < seg1) {
+        // one 16-row block's columns, silu in its fast or its dividing form
+        auto block = [&](auto fast_c) {
+          constexpr bool kFast = decltype(fast_c)::value;
 #pragma unroll
           for (int jp = 0; jp < TN / 4; ++jp) {
             uint2 pg[2], pu[2], ph[2];
@@ -645,7 +647,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
                   hq[q2] = pack_bf2(oss_glu(bf_lo(gw), bf_lo(uw), p.limit, p.alpha),
                                     oss_glu(bf_hi(gw), bf_hi(uw), p.limit, p.alpha));
                 } else {
-                  const uint32_t sw = pack_bf2(silu_f(bf_lo(gw)), silu_f(bf_hi(gw)));  // bf16(silu(g))
+                  const float g0 = bf_lo(gw), g1 = bf_hi(gw);
+                  const uint32_t sw = pack_bf2(silu_sig<kFast>(g0, silu_den(g0)).silu,
+                                               silu_sig<kFast>(g1, silu_den(g1)).silu);  // bf16(silu(g))
                   hq[q2] = pack_bf2(bf_lo(sw) * bf_lo(uw), bf_hi(sw) * bf_hi(uw));
                 }
                 gq[q2] = gw;
@@ -663,6 +667,24 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
             *(uint4*)(p.out_g + off) = sg;
             *(uint4*)(p.out_u + off) = su;
             *(uint4*)(p.out_h + off) = sh;
+          }
+        };
+        if (r < seg1) {
+          if constexpr (ACT == kSwiGLU) {
+            // the range of the block's gate values, taken before their rounding to
+            // bf16, which keeps them inside it
+            float g_min = acc[i][0][0], g_max = acc[i][0][0];
+#pragma unroll
+            for (int jj = 0; jj < TN / 2; ++jj)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                g_min = fminf(g_min, acc[i][2 * jj][q]);
+                g_max = fmaxf(g_max, acc[i][2 * jj][q]);
+              }
+            if (silu_fast_wave(g_min, g_max)) block(std::true_type{});
+            else block(std::false_type{});
+          } else {
+            block(std::true_type{});
           }
         }
       }
@@ -771,11 +793,20 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_gemm_kernel(GemmParams p
                 // (the epilogue is VALU-bound), read back exactly from the packed word
                 if (q & 1) continue;
                 const float dh1 = bf_hi(dhw[q >> 1]), gv1 = bf_hi(gww[q >> 1]), uv1 = bf_hi(uww[q >> 1]);
-                const uint32_t slw = pack_bf2(silu_f(gv), silu_f(gv1));  // bf16(silu(g))
-                const uint32_t dsw = pack_bf2(dh * uv, dh1 * uv1);       // bf16(dh . u)
+                const float d0 = silu_den(gv), d1 = silu_den(gv1);
+                SiluSig f0, f1;
+                if (silu_fast_wave(fminf(gv, gv1), fmaxf(gv, gv1))) {
+                  f0 = silu_sig<true>(gv, d0);
+                  f1 = silu_sig<true>(gv1, d1);
+                } else {
+                  f0 = silu_sig<false>(gv, d0);
+                  f1 = silu_sig<false>(gv1, d1);
+                }
+                const uint32_t slw = pack_bf2(f0.silu, f1.silu);   // bf16(silu(g))
+                const uint32_t dsw = pack_bf2(dh * uv, dh1 * uv1);  // bf16(dh . u)
                 du[q] = dh * bf_lo(slw);
                 du[q + 1] = dh1 * bf_hi(slw);
-                const float sg = 1.0f / (1.0f + expf(-gv)), sg1 = 1.0f / (1.0f + expf(-gv1));
+                const float sg = f0.sig, sg1 = f1.sig;
                 dg[q] = bf_lo(dsw) * sg * (1.0f + gv * (1.0f - sg));
                 dg[q + 1] = bf_hi(dsw) * sg1 * (1.0f + gv1 * (1.0f - sg1));
               } else {
@@ -1041,6 +1072,40 @@ MOE_API int moe_grouped_gemm_bwd_dw2(const uint16_t* dy, const uint16_t* h, cons
   if (!dw2 || (n_rows > 0 && (!dy || !h))) return kErrInvalidArgument;
   p.dy = dy; p.h = h; p.out_dw2 = dw2;
   launch_mode<kBwdDw2>(p, n_rows, stream);
+  return launch_status();
+}
+
+// The SwiGLU epilogues' pointwise arithmetic on its own: fp32 silu(g) and sigmoid(g)
+// of bf16 g as gate_up and dgu compute them, so that tests can compare every bf16
+// input with torch's. Each pair (2i, 2i + 1) takes the fast form when both lie in its
+// range, as a piece of the epilogues does when it lies in it for every lane.
+__global__ void __launch_bounds__(256) swiglu_pointwise_kernel(const uint16_t* __restrict__ g,
+                                                               float* __restrict__ silu,
+                                                               float* __restrict__ sig, int64_t n) {
+  const int64_t i = 2 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (i >= n) return;
+  const bool two = i + 1 < n;
+  const float g0 = bf2f(g[i]), g1 = two ? bf2f(g[i + 1]) : 0.0f;
+  const bool fast = silu_fast_range(fminf(g0, g1), fmaxf(g0, g1));
+  const float d0 = silu_den(g0), d1 = silu_den(g1);
+  const SiluSig r0 = fast ? silu_sig<true>(g0, d0) : silu_sig<false>(g0, d0);
+  const SiluSig r1 = fast ? silu_sig<true>(g1, d1) : silu_sig<false>(g1, d1);
+  silu[i] = r0.silu;
+  sig[i] = r0.sig;
+  if (two) {
+    silu[i + 1] = r1.silu;
+    sig[i + 1] = r1.sig;
+  }
+}
+
+MOE_API int moe_swiglu_pointwise_f32(const uint16_t* g, float* silu, float* sigmoid, int64_t n,
+                                     hipStream_t stream) {
+  if (n < 0) return kErrInvalidArgument;
+  if (n == 0) return kOk;
+  if (!g || !silu || !sigmoid) return kErrInvalidArgument;
+  const int64_t blocks = ((n + 1) / 2 + 255) / 256;
+  if (blocks > 0x7fffffff) return kErrInvalidArgument;
+  swiglu_pointwise_kernel<<<(unsigned)blocks, 256, 0, stream>>>(g, silu, sigmoid, n);
   return launch_status();
 }
 
