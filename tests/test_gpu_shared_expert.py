@@ -124,3 +124,29 @@ def test_swiglu_kernels_match_torch_ops_and_autograd(dev, case):
     assert dgu.shape == (rows, 2 * hs)
     assert torch.equal(dgu[:, :hs], ra1.grad)
     assert torch.equal(dgu[:, hs:], ra3.grad)
+
+
+def test_swiglu_kernels_every_bf16(dev):
+    """The shared expert's SwiGLU kernels on a1 covering every bf16 value (the values
+    where they divide in the reciprocal form in rows 0-207, the rest after): h, dg
+    and du equal torch's ops and autograd bit for bit, NaNs as NaNs."""
+    from tests.test_gpu_kernels import _bf16_patterns_split, _fill_rows
+    from torchtitan_amd import ops
+
+    banner("swiglu kernels, every bf16 a1")
+    hs = 256
+    fast, rest = _bf16_patterns_split()
+    a1 = torch.cat([_fill_rows(fast, 208, hs), _fill_rows(rest, 112, hs)]).to(dev)
+    g = torch.Generator().manual_seed(5)
+    a3 = (torch.randn(a1.shape, generator=g) * 2).bfloat16().to(dev)
+    dh = (torch.randn(a1.shape, generator=g) * 2).bfloat16().to(dev)
+
+    def same(a, b):
+        return bool(((a.view(torch.int16) == b.view(torch.int16)) | (torch.isnan(a) & torch.isnan(b))).all())
+
+    assert same(ops.swiglu_forward(a1, a3), F.silu(a1) * a3)
+    ra1, ra3 = a1.clone().requires_grad_(True), a3.clone().requires_grad_(True)
+    (F.silu(ra1) * ra3).backward(dh)
+    dgu = ops.swiglu_backward(dh, a1, a3)
+    assert same(dgu[:, :hs], ra1.grad)
+    assert same(dgu[:, hs:], ra3.grad)

@@ -78,7 +78,22 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // torch's GPU formulas in the op math type: silu(x) = x / (1 + exp(-x)),
 // silu_backward(dy, x) = dy * sigmoid * (1 + x * (1 - sigmoid)) with
-// sigmoid = 1 / (1 + exp(-x)); the exponential is computed once for both.
+// sigmoid = 1 / (1 + exp(-x)); the exponential is computed once for both. For bf16
+// the vector kernels divide in the reciprocal form of the grouped GEMMs' epilogues
+// (silu_sig in common.h: IEEE division's results for every bf16 input) where a
+// chunk's values lie in its range in every lane.
+
+// the range of a chunk's V values, for silu_fast_wave
+template <int V>
+__device__ __forceinline__ bool chunk_fast(const float (&g)[V]) {
+  float lo = g[0], hi = g[0];
+#pragma unroll
+  for (int q = 1; q < V; ++q) {
+    lo = fminf(lo, g[q]);
+    hi = fmaxf(hi, g[q]);
+  }
+  return silu_fast_wave(lo, hi);
+}
 
 // h = rnd(rnd(silu(a1)) * a3), T = bf16 (rnd = round to bf16) or fp32 (rnd = identity)
 template <typename T>
@@ -91,8 +106,16 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ a
     float g[V], u[V], o[V];
     Chunk<T>::unpack(*(const uint4*)(a1 + i * V), g);
     Chunk<T>::unpack(*(const uint4*)(a3 + i * V), u);
+    float d[V];
 #pragma unroll
-    for (int q = 0; q < V; ++q) o[q] = Chunk<T>::round(g[q] / (1.0f + expf(-g[q]))) * u[q];
+    for (int q = 0; q < V; ++q) d[q] = silu_den(g[q]);
+    if (sizeof(T) == 2 && chunk_fast<V>(g)) {
+#pragma unroll
+      for (int q = 0; q < V; ++q) o[q] = Chunk<T>::round(silu_sig<true>(g[q], d[q]).silu) * u[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < V; ++q) o[q] = Chunk<T>::round(silu_sig<false>(g[q], d[q]).silu) * u[q];
+    }
     *(uint4*)(h + i * V) = Chunk<T>::pack(o);
   }
 }
@@ -115,11 +138,21 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ d
     Chunk<T>::unpack(*(const uint4*)(dh + off), d);
     Chunk<T>::unpack(*(const uint4*)(a1 + off), g);
     Chunk<T>::unpack(*(const uint4*)(a3 + off), u);
+    float den[V];
+    SiluSig f[V];
+#pragma unroll
+    for (int q = 0; q < V; ++q) den[q] = silu_den(g[q]);
+    if (sizeof(T) == 2 && chunk_fast<V>(g)) {
+#pragma unroll
+      for (int q = 0; q < V; ++q) f[q] = silu_sig<true>(g[q], den[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < V; ++q) f[q] = silu_sig<false>(g[q], den[q]);
+    }
 #pragma unroll
     for (int q = 0; q < V; ++q) {
-      const float e = expf(-g[q]);
-      const float s = Chunk<T>::round(g[q] / (1.0f + e));
-      const float sg = 1.0f / (1.0f + e);
+      const float s = Chunk<T>::round(f[q].silu);
+      const float sg = f[q].sig;
       const float dsl = Chunk<T>::round(d[q] * u[q]);
       du[q] = d[q] * s;
       dg[q] = dsl * sg * (1.0f + g[q] * (1.0f - sg));
