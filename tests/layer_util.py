@@ -95,9 +95,18 @@ def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
     return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
 
 
+def elem_err(a: torch.Tensor, b: torch.Tensor, floor: float) -> float:
+    """The element-wise relative error max |a - b| / (|b| + floor * max |b|): elements
+    far below the tensor's scale, where a reordered sum may cancel, are measured
+    against `floor` times its largest magnitude instead of their own."""
+    a, b = a.detach().float(), b.detach().float()
+    fl = floor * b.abs().max().clamp_min(1e-30)
+    return ((a - b).abs() / (b.abs() + fl)).max().item()
+
+
 def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape) -> dict:
     """Runs both sides forward + backward from the same x and returns
-    {name: (rel_err, bit_identical)}; asserts that routing (indices, counts, top
+    {name: (rel_err, bit_identical, elem_err at floors 1e-3 and 1e-5)}; asserts that routing (indices, counts, top
     scores) is bit-exact, each side running its own fp32 gate."""
     d = sh.dim
     xa = x.clone().requires_grad_(True)
@@ -165,7 +174,8 @@ def compare_with_reference(moe, x: torch.Tensor, g: torch.Tensor, sh: LayerShape
     else:
         for k in ("w1", "w2", "w3"):
             pairs[f"grad_{k}"] = (getattr(moe.experts, k).grad, params[k].grad)
-    res = {k: (rel_err(a, b), bool(torch.equal(a, b))) for k, (a, b) in pairs.items()}
+    res = {k: (rel_err(a, b), bool(torch.equal(a, b)), elem_err(a, b, 1e-3), elem_err(a, b, 1e-5))
+           for k, (a, b) in pairs.items()}
     res["_counts"] = counts.cpu()
     res.update(res_extra)
     return res

@@ -19,7 +19,14 @@ run by torch on the same GPU (oracle.moe_forward_reference_ops):
 
 Routing (indices, counts, top scores) must be bit-exact; the output and all
 gradients within 1e-2 normwise relative error (max |ours - ref| / max |ref|),
-0.1 for the fp8 and MXFP8 layers against the bf16 reference. The gpt-oss bias
+0.1 for the fp8 and MXFP8 layers against the bf16 reference. Element by element,
+|ours - ref| / (|ref| + 1e-3 max |ref|): the bf16 SwiGLU layers' output and
+expert-weight gradients are bit-identical (asserted), their gate gradient is
+within 1e-2 and their input gradient within 1e-1. The input gradient adds the
+gate backward's term, whose exact three-way bf16 split sums in another order
+than the reference's fp32 GEMM: one rounding flip of a term larger than the
+result, where the terms cancel, shows up as a relative error of a few percent in
+that element (measured 3-7e-2; 1.2-2.5e-3 normwise). The gpt-oss bias
 gradients are compared with the exact (fp64) per-expert sums of the reference's
 own row gradients: the reference accumulates them into bf16 parameters with
 bf16 atomics (index_add behind repeat_interleave), which this layer does in fp32.
@@ -48,6 +55,10 @@ SHAPES = {
 }
 
 TOL = {"kimi_fp8": 0.1, "kimi_mxfp8": 0.1}
+# bf16 SwiGLU layers: tensors that must equal the reference bit for bit, and
+# element-wise bounds (floor 1e-3 of the maximum) for the others
+BIT_IDENTICAL = {"kimi", "zipf", "dsv3"}
+ELEM_TOL = {"grad_x": 0.1, "grad_gate": 1e-2}
 
 
 @pytest.mark.parametrize("name", list(SHAPES))
@@ -65,10 +76,16 @@ def test_layer_at_benchmark_shape(dev, name):
           f"empty experts {int((counts == 0).sum())}", flush=True)
     print(f"[case] {name}: " + ", ".join(f"{k} {v[0]:.2e}{' (bit-identical)' if v[1] else ''}"
                                           for k, v in res.items()), flush=True)
+    print(f"[case] {name} element-wise (floor 1e-3 / 1e-5 of the max): "
+          + ", ".join(f"{k} {v[2]:.2e} / {v[3]:.2e}" for k, v in res.items()), flush=True)
     if name == "zipf":
         assert int((counts == 0).sum()) >= 20 and counts.max() > 5 * counts.float().mean()
     tol = TOL.get(name, 1e-2)
     bad = {k: v[0] for k, v in res.items() if not v[0] <= tol}
     assert not bad, bad
+    if name in BIT_IDENTICAL:
+        assert all(res[k][1] for k in ("out", "grad_w1", "grad_w2", "grad_w3")), res
+        bad = {k: res[k][2] for k, t in ELEM_TOL.items() if not res[k][2] <= t}
+        assert not bad, bad
     del moe, x, g
     torch.cuda.empty_cache()
