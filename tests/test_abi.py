@@ -81,6 +81,11 @@ def test_host_side_validation_returns_status_codes(lib):
     assert lib.moe_fp8_gemm_down(null, null, null, null, null, 8, 4, 768 + 64, 256, null, null) == -2
     assert lib.moe_mxfp8_gemm_down(null, null, null, null, null, 8, 4, 768 + 64, 256, null, null) == -2
     assert lib.moe_grouped_gemm_bwd_dw2(null, null, null, 8, 0, 256, 256, null, null) == -1
+    # the SwiGLU epilogues' pointwise test entry: a negative count or missing buffers
+    # are refused, an empty one is a no-op
+    assert lib.moe_swiglu_pointwise_f32(null, null, null, -1, null) == -1
+    assert lib.moe_swiglu_pointwise_f32(null, null, null, 4, null) == -1
+    assert lib.moe_swiglu_pointwise_f32(null, null, null, 0, null) == 0
 
 
 def test_status_codes_map_to_exceptions():
