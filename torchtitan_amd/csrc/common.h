@@ -95,7 +95,25 @@ __device__ __forceinline__ SiluSig silu_sig(float g, float d) {
 // returns the 8 columns 8g .. 8g + 7 of the 32-column span [lo | hi] of row r,
 // gathered from the lanes of the same row, so that the four lanes of a row store
 // 64 contiguous bytes with one 16-byte store each (instead of 32 bytes per block).
+// The exchange is two lane-half swaps and two lane-row swaps of gfx950 (no LDS):
+// with lo(g), hi(g) the pairs of lane row g (16 lanes), swapping the upper 32 lanes
+// of lo with the lower 32 of hi gives [lo0 lo1 hi0 hi1] / [lo2 lo3 hi2 hi3], and
+// swapping the odd rows of the first with the even rows of the second gives
+// [lo0 lo2 hi0 hi2] / [lo1 lo3 hi1 hi3]: lane (r, g)'s columns 8g .. 8g + 3 and
+// 8g + 4 .. 8g + 7. Data moves only between the lanes of one row r, which share
+// their active state wherever the epilogues skip rows. (Cross-lane reads through
+// the LDS crossbar cost bank-conflict cycles in every epilogue.)
 __device__ __forceinline__ uint4 span64(uint2 lo, uint2 hi, int lane) {
+  (void)lane;
+  const auto x32 = __builtin_amdgcn_permlane32_swap(lo.x, hi.x, false, false);
+  const auto y32 = __builtin_amdgcn_permlane32_swap(lo.y, hi.y, false, false);
+  const auto x16 = __builtin_amdgcn_permlane16_swap(x32[0], x32[1], false, false);
+  const auto y16 = __builtin_amdgcn_permlane16_swap(y32[0], y32[1], false, false);
+  return make_uint4(x16[0], y16[0], x16[1], y16[1]);
+}
+// The same exchange through the LDS crossbar (ds_bpermute), for an epilogue whose
+// register schedule measured faster with it (the rowwise fp8 dgu).
+__device__ __forceinline__ uint4 span64_lds(uint2 lo, uint2 hi, int lane) {
   const int g = lane >> 4;
   const int s1 = (lane & 15) + 16 * ((2 * g) & 3), s2 = s1 + 16;
   const uint32_t l0 = __shfl(lo.x, s1), l1 = __shfl(lo.y, s1), l2 = __shfl(lo.x, s2), l3 = __shfl(lo.y, s2);
