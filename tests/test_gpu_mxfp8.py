@@ -160,12 +160,22 @@ def test_mxfp8_transposing_quantizers_slab_widths(dev, width):
     assert torch.equal(dqr.cpu(), rqr.view(torch.uint8)) and torch.equal(dsr.cpu(), rsr)
     assert torch.equal(dqt.cpu()[:, :used], rq2[:, :used]) and torch.equal(dst.cpu()[:used // 32], rs2[:used // 32])
 
-def test_mxfp8_gemm_entry_points_match_emulation(dev):
+# experts, D, H, rows per expert: ragged with empty experts; tall experts over several
+# 256-row m-tiles with partial last tiles; single-row and tile-edge groups
+GEMM_SHAPES = {
+    "ragged_e6_d256_h256": (6, 256, 256, [40, 0, 130, 17, 64, 3]),
+    "tall_e3_d512_h768": (3, 512, 768, [700, 0, 517]),
+    "edges_e5_d768_h256": (5, 768, 256, [1, 255, 257, 0, 390]),
+}
+
+
+@pytest.mark.parametrize("shape", list(GEMM_SHAPES))
+def test_mxfp8_gemm_entry_points_match_emulation(dev, shape):
     """Every MXFP8 GEMM kernel against R._mx_mm on identical quantized operands."""
     banner("mxfp8 GEMM entry points")
     from torchtitan_amd import _lib, ops
 
-    e, d, h, counts = 6, 256, 256, [40, 0, 130, 17, 64, 3]
+    e, d, h, counts = GEMM_SHAPES[shape]
     gen = torch.Generator().manual_seed(2)
     r = sum(counts)
     cnt = torch.tensor(counts, dtype=torch.int64)
